@@ -1,0 +1,165 @@
+"""Benchmark of the Library read on one MI355X.
+
+Default workload: batched paged decode — B = 64 sequences, each reading its own Library of
+U{8..64} chunks x 512 slots (chunk = page, pages placed by a seeded shuffle), d_s = 2048, fp16
+K = V slots with ragged tails, top-8 routing.  One step = routing (q.S scores + top-k + softmax)
+plus the split-K masked-softmax read of the routed pages for all 64 query rows, inputs resident
+in HBM.  Prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--workload batched_paged_decode]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import statistics
+import sys
+import time
+
+import torch
+
+METRIC = "Library-read query tokens/sec + achieved HBM GB/s (% peak) at B=64 paged decode"
+HBM_PEAK_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="batched_paged_decode",
+                    choices=["batched_paged_decode", "single_decode"])
+    ap.add_argument("--nsplit", type=int, default=None)
+    ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
+    ap.add_argument("--cpu-reps", type=int, default=3)
+    return ap.parse_args()
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def cpu_baseline(P, q, top_k, n_seq, reps):
+    """The reference path on the host cores: per sequence one call of route + read over ALL of its
+    chunks in fp32 (the reference's order, xenc/injector.py:220-265), via the CPU oracle."""
+    import oracle as O
+    torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+    B = q.shape[0]
+    n_seq = min(n_seq, B)
+    qc = q.cpu()
+    times, slots = [], 0
+    for b in range(n_seq):
+        K, M, S = P.library(b)
+        K, M, S = K.cpu(), M.cpu(), S.cpu()
+        qb = qc[b].view(1, 1, -1)
+        O.branch_read(qb, K, M, S, top_k=top_k)               # warm-up
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            O.branch_read(qb, K, M, S, top_k=top_k)
+            ts.append(time.perf_counter() - t0)
+        times.append(statistics.median(ts))
+        slots += int(M.sum())
+        del K, M, S
+    total = sum(times)
+    return {"value": n_seq / total, "unit": "query tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": (f"first {n_seq} of {B} sequences, one fp32 route+read call each over all of the "
+                       f"sequence's chunks ({slots} slots), median of {reps} reps after 1 warm-up; "
+                       f"CPU oracle on {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding of the read is designed but not built", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(2)
+    from kv_skill_v2_amd import ops, synth
+
+    dev = torch.device("cuda:0")
+    P, q, qg, top_k = synth.decode_workload(args.workload, device=dev)
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    B, d = q.shape
+    read_temp, route_temp = 12.0, 10.0
+
+    def step():
+        _, idx, wsel = ops.route_topk(q, lib, qg, top_k=top_k, route_temp=route_temp)
+        return ops.library_read_decode(q, lib, idx, wsel, qg, read_temp=read_temp, nsplit=args.nsplit)
+
+    # Algorithmic bytes of the read: each routed page's valid slot rows once (K = V tied), the
+    # query rows and the output rows.  Routing is deterministic, so read it once off the clock.
+    _, idx0, wsel0 = ops.route_topk(q, lib, qg, top_k=top_k, route_temp=route_temp)
+    idx_h = idx0.cpu()
+    nv_h = P.nvalid
+    ptr_h = P.chunk_ptr.cpu().tolist()
+    routed_slots = sum(nv_h[ptr_h[b] + c] for b in range(B) for c in idx_h[b].tolist() if c >= 0)
+    read_bytes = routed_slots * d * 2 + 2 * B * d * 4
+    route_bytes = sum(P.n_chunks) * d * 4 + B * d * 4
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        _, idx, wsel = ops.route_topk(q, lib, qg, top_k=top_k, route_temp=route_temp)
+        ev[i][0].record(stream)
+        ops.library_read_decode(q, lib, idx, wsel, qg, read_temp=read_temp, nsplit=args.nsplit)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / args.steps
+    read_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    achieved = read_bytes / (read_ms * 1e-3) / 1e9
+
+    cpu = None
+    if args.cpu_sample > 0:
+        cpu = cpu_baseline(P, q, top_k, args.cpu_sample, args.cpu_reps)
+
+    out = {
+        "metric": METRIC,
+        "value": B / (ms_step * 1e-3),
+        "unit": "query tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "sequences": B, "d_s": d,
+                   "chunks_per_library": f"U{{8..64}} (total {sum(P.n_chunks)})" if B > 1 else str(P.n_chunks[0]),
+                   "slots_per_page": P.pages.shape[1], "top_k": top_k, "read_temp": read_temp,
+                   "route_temp": route_temp, "accumulate": "fp32", "page_table": "seeded shuffle",
+                   "nsplit": args.nsplit or ops.default_nsplit(B * idx_h.shape[1], P.pages.shape[1])},
+        "roofline": {"bound": "hbm", "kernel": "library_read_decode (split + merge)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": read_bytes, "avg_launch_ms": read_ms,
+                     "routed_slots": routed_slots, "route_bytes": route_bytes},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

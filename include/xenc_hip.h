@@ -1,0 +1,87 @@
+/*
+ * xenc_hip.h — C ABI of the MI355X Library-read library (libxenc_hip.so).
+ *
+ * Every entry point takes device pointers, element strides and sizes, plus an opaque
+ * `stream` (a hipStream_t; NULL = the null stream).  No entry point allocates device or host
+ * memory, synchronises the stream or reads device memory on the host, so every call can be
+ * captured into a HIP graph.  Work buffers are passed in by the caller; their sizes come from
+ * the *_workspace_bytes queries.  Return value: XENC_OK (0) or a negative XENC_E* code;
+ * xenc_strerror() names it and xenc_last_hip_error() gives the HIP error of a failed launch.
+ *
+ * Data layout shared by the Library-read entry points ("library set"):
+ *   pages        fp16 [P, slots_per_page, d]  chunk operators, one chunk per page, slot rows
+ *                contiguous (d fastest); K = V (tied): the same rows are keys and values.
+ *   chunk_ptr    int32 [G+1]    chunks of library g are global chunks chunk_ptr[g] .. chunk_ptr[g+1]-1
+ *   chunk_page   int32 [Ctot]   page holding global chunk c (any order: the page table)
+ *   chunk_nvalid int32 [Ctot]   valid slots of chunk c (1 .. slots_per_page); rows past it are masked
+ *   S            fp32  [Ctot, d] summary key of chunk c (L2-normalised masked mean of its slots)
+ *   q            fp32  [M, ldq]  query rows (already L2-normalised by the caller)
+ *   q_group      int32 [M]       library read by query row m
+ * Routed chunk indices are LOCAL to the query's library (0 .. C_g-1), as the reference's
+ * per-library top-k returns them.
+ */
+#ifndef XENC_HIP_H
+#define XENC_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  XENC_OK = 0,
+  XENC_EINVAL = -1,      /* a size/argument is out of range (d % 8 != 0, k < 0, M < 0 ...) */
+  XENC_ENULL = -2,       /* a required pointer is NULL */
+  XENC_EALIGN = -3,      /* a pointer or stride breaks the 16-byte alignment the kernels need */
+  XENC_EWORKSPACE = -4,  /* the workspace passed in is smaller than the size query returned */
+  XENC_EHIP = -5         /* a kernel launch failed; see xenc_last_hip_error() */
+};
+
+const char* xenc_strerror(int code);
+int xenc_last_hip_error(void);
+/* ABI version: bumped whenever a signature below changes. */
+int xenc_abi_version(void);
+
+/*
+ * Routing: logit[m,c] = route_temp * <q[m], S[chunk_ptr[g]+c]>, g = q_group[m].
+ * If 0 < top_k < C_g keep the top_k largest (ties -> lower chunk index), else keep all C_g.
+ * w = softmax over the kept logits (the others are -inf, i.e. weight 0).
+ * Outputs: w_dense [M, ldw] (columns >= C_g are 0; ldw >= max C_g),
+ *          idx [M, kk] int32 kept chunks in descending-logit order, -1 past the kept count,
+ *          w_sel [M, kk] their weights (0 past the kept count).
+ * kk must be >= min(top_k, C_g) for top-k and >= C_g for dense routing.
+ * Replaces LibraryInjector.route (xenc/injector.py:220-229).
+ */
+int xenc_route_topk(const float* q, long long ldq, int M, int d,
+                    const float* S, const int* chunk_ptr, const int* q_group, int G,
+                    int top_k, float route_temp,
+                    float* w_dense, long long ldw, int* idx, float* w_sel, int kk,
+                    void* stream);
+
+/*
+ * Decode read over routed pages (split-K over slots, log-sum-exp merge):
+ *   softmax=1: r[m] = sum_j w_sel[m,j] * sum_n softmax_n(read_temp*<q,K[c_j,n]>) K[c_j,n]
+ *   softmax=0: r[m] = sum_j w_sel[m,j] * sum_n <q,K[c_j,n]>/sqrt(n_valid) K[c_j,n]  (linear read)
+ * over the valid slots n of the routed chunks c_j = idx[m,j] (entries < 0 are skipped).
+ * Each slot row is read from HBM once for both the score and the value.  Page slots are
+ * split into nsplit ranges of ceil(slots_per_page/nsplit) slots (nsplit in 1..64).
+ * r is fp32 [M, ldr].  Workspace: xenc_decode_workspace_bytes(M, kk, nsplit, d).
+ * Replaces the read of LibraryInjector._branch (xenc/injector.py:236-265) when the routed
+ * chunks are known; bit-equivalent in intent to reading every chunk with w = 0 off the top-k.
+ */
+size_t xenc_decode_workspace_bytes(int M, int kk, int nsplit, int d);
+int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
+                             const void* pages, int slots_per_page, long long page_stride,
+                             const int* chunk_page, const int* chunk_nvalid,
+                             const int* chunk_ptr, const int* q_group, int G,
+                             const int* idx, const float* w_sel, int kk,
+                             float read_temp, int softmax, int nsplit,
+                             float* r, long long ldr,
+                             void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XENC_HIP_H */

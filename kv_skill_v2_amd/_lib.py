@@ -1,0 +1,88 @@
+"""ctypes binding of libxenc_hip.so (the C ABI declared in include/xenc_hip.h).
+
+The library is loaded after torch so that it binds to the HIP runtime torch already loaded
+(both carry the SONAME libamdhip64.so.7).  There is no fallback: if the library is missing or
+was built for another ABI version, every call raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import c_float, c_int, c_longlong, c_size_t, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
+ABI_VERSION = 1
+
+_lock = threading.Lock()
+_lib = None
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "xenc_strerror": (ctypes.c_char_p, [c_int]),
+    "xenc_last_hip_error": (c_int, []),
+    "xenc_abi_version": (c_int, []),
+    "xenc_route_topk": (c_int, [
+        c_void_p, c_longlong, c_int, c_int,          # q, ldq, M, d
+        c_void_p, c_void_p, c_void_p, c_int,         # S, chunk_ptr, q_group, G
+        c_int, c_float,                              # top_k, route_temp
+        c_void_p, c_longlong, c_void_p, c_void_p, c_int,  # w_dense, ldw, idx, w_sel, kk
+        c_void_p]),                                  # stream
+    "xenc_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "xenc_library_read_decode": (c_int, [
+        c_void_p, c_longlong, c_int, c_int,          # q, ldq, M, d
+        c_void_p, c_int, c_longlong,                 # pages, slots_per_page, page_stride
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,  # chunk_page, chunk_nvalid, chunk_ptr, q_group, G
+        c_void_p, c_void_p, c_int,                   # idx, w_sel, kk
+        c_float, c_int, c_int,                       # read_temp, softmax, nsplit
+        c_void_p, c_longlong,                        # r, ldr
+        c_void_p, c_size_t, c_void_p]),              # workspace, bytes, stream
+}
+
+
+class XencError(RuntimeError):
+    pass
+
+
+def lib():
+    """The loaded library (loads on first use; raises if it is missing)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise XencError(f"{LIB_PATH} is not built: run kv_skill_v2_amd._build.build() "
+                                "(the Library read has no CPU path)")
+            handle = ctypes.CDLL(str(LIB_PATH), mode=ctypes.RTLD_GLOBAL)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype, fn.argtypes = res, args
+            got = handle.xenc_abi_version()
+            if got != ABI_VERSION:
+                raise XencError(f"{LIB_PATH} has ABI version {got}, expected {ABI_VERSION}: rebuild it")
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc == 0:
+        return
+    L = lib()
+    msg = L.xenc_strerror(rc).decode()
+    if rc == -5:
+        msg += f" (hipError {L.xenc_last_hip_error()})"
+    if rc in (-1, -2, -3, -4):
+        raise ValueError(f"{what}: {msg}")
+    raise XencError(f"{what}: {msg}")
+
+
+def stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

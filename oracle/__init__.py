@@ -1,0 +1,26 @@
+"""CPU oracle of xenc's Library read — TEST INFRASTRUCTURE ONLY.
+
+A restatement of the reference math in plain PyTorch on the CPU (fp32 in the reference's own
+operation order, or fp64 for checking).  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import it, and only as the checker or the timed CPU baseline: the product
+package (kv_skill_v2_amd) never imports it and has no CPU path.
+
+Pins (each function is checked by tests/test_oracle.py against something other than itself):
+  library_tensors / summaries  closed form S = m/|m| (tests/test_library.py:200-204), centering
+                               invariants (:241-261), subset == rebuild (:186-199)
+  route                        brute-force rank counting in pure Python, sum/sparsity invariants
+                               (tests/test_library.py:126-145)
+  read                         pure-Python loops on tiny inputs; one-chunk closed form
+                               (tests/test_library.py:91-123); linear-read closed form
+                               (tests/test_integration.py:139-173); one-hot force_attn
+                               (tests/test_d6_force_attn.py:49-63); untied V (test_attn_harvest)
+  read_dq                      torch.autograd of the fp64 forward + central finite differences
+  selector_weights/apply       sparsity/sum/entropy and matched-norm identity
+                               (tests/test_selector.py:25-55)
+  decode_read_ref / ref_varlen two-part LSE merge == joint softmax (tests/test_d23_kernels.py:38-48),
+                               pure-Python loop restatement on tiny inputs
+  epilogue                     parity unpinned for rms_norm's eps and ModelInterface internals
+                               (deltaskill is absent); fixed here as documented parameters.
+"""
+
+from .xenc_oracle import *  # noqa: F401,F403

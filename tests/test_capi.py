@@ -1,0 +1,59 @@
+"""The C-ABI library loads on a GPU-less host and exports every entry point include/*.h declares
+(no compute calls here)."""
+
+from __future__ import annotations
+
+import re
+
+from conftest import ROOT
+
+
+def _declared() -> set[str]:
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(xenc_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = _declared()
+    assert {"xenc_route_topk", "xenc_library_read_decode", "xenc_strerror"} <= names, names
+
+
+def test_library_exports_every_declared_symbol():
+    from kv_skill_v2_amd import _lib
+    L = _lib.lib()
+    for name in sorted(_declared()):
+        assert hasattr(L, name), f"{name} declared in include/ but not exported by {_lib.LIB_PATH}"
+    assert L.xenc_abi_version() == _lib.ABI_VERSION
+
+
+def test_binding_covers_header():
+    from kv_skill_v2_amd import _lib
+    assert _declared() == set(_lib.SIGNATURES), "ctypes signatures and include/*.h disagree"
+
+
+def test_error_codes_and_size_queries():
+    from kv_skill_v2_amd import _lib
+    L = _lib.lib()
+    assert L.xenc_strerror(0) == b"ok"
+    assert b"aligned" in L.xenc_strerror(-3)
+    units = 64 * 8 * 4
+    assert L.xenc_decode_workspace_bytes(64, 8, 4, 2048) >= units * 2048 * 4 + units * 8
+    assert L.xenc_decode_workspace_bytes(0, 8, 4, 2048) == 0
+
+
+def test_host_side_validation_rejects_bad_sizes():
+    """Argument checks run on the host before any launch: safe without a GPU."""
+    from kv_skill_v2_amd import _lib
+    L = _lib.lib()
+    # d not a multiple of 8
+    assert L.xenc_route_topk(None, 12, 1, 12, None, None, None, 1, 2, 10.0, None, 4, None, None, 2, None) == -1
+    # NULL pointers with valid sizes
+    assert L.xenc_route_topk(None, 16, 1, 16, None, None, None, 1, 2, 10.0, None, 4, None, None, 2, None) == -2
+    assert L.xenc_library_read_decode(None, 16, 1, 16, None, 4, 64, None, None, None, None, 1, None, None, 2,
+                                      12.0, 1, 1, None, 16, None, 0, None) == -2
+    # nsplit out of range
+    assert L.xenc_library_read_decode(None, 16, 1, 16, None, 4, 64, None, None, None, None, 1, None, None, 2,
+                                      12.0, 1, 65, None, 16, None, 0, None) == -1
