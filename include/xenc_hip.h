@@ -48,7 +48,8 @@ int xenc_abi_version(void);
  * If 0 < top_k < C_g keep the top_k largest (ties -> lower chunk index), else keep all C_g.
  * w = softmax over the kept logits (the others are -inf, i.e. weight 0).
  * Outputs: w_dense [M, ldw] (columns >= C_g are 0; ldw >= max C_g),
- *          idx [M, kk] int32 kept chunks in descending-logit order, -1 past the kept count,
+ *          idx [M, kk] int32 kept chunks, -1 past the kept count: in descending-logit order
+ *          (ties -> lower index) under top-k, in chunk order 0..C_g-1 when all are kept,
  *          w_sel [M, kk] their weights (0 past the kept count).
  * kk must be >= min(top_k, C_g) for top-k and >= C_g for dense routing.
  * Replaces LibraryInjector.route (xenc/injector.py:220-229).

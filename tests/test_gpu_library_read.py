@@ -42,8 +42,9 @@ def _oracle_route(q, S, top_k, route_temp=10.0):
     """fp64 oracle weights, rank order and boundary gap for one library."""
     w = O.route(q.double(), S.double(), route_temp, top_k)
     C = S.shape[0]
-    k = C if (not top_k or top_k >= C) else top_k
-    order = O.topk_order(q.double() @ S.double().T, k)
+    if not top_k or top_k >= C:            # all chunks kept: the kernel lists them in chunk order
+        return w, torch.arange(C).view(1, C), O.boundary_gap(q, S, top_k)
+    order = O.topk_order(q.double() @ S.double().T, top_k)
     return w, order, O.boundary_gap(q, S, top_k)
 
 
