@@ -35,7 +35,23 @@ def parse():
     ap.add_argument("--nsplit", type=int, default=None)
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="after the timed loop, copy a buffer of this size 3 times (a plain copy "
+                         "kernel of known bytes, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def traffic_from_profile(workload: str):
+    """HBM bytes per launch of the read kernel measured offline with rocprofv3 --pmc
+    (FETCH_SIZE and WRITE_SIZE, scaled by the same counters on a copy of known size); the
+    summary lives in profiles/ next to the command that produced it.  None when absent."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        f"decode_read_{workload}_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def cpu_model() -> str:
@@ -129,6 +145,16 @@ def main():
     read_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
     achieved = read_bytes / (read_ms * 1e-3) / 1e9
 
+    if args.calibration_copy_mib > 0:
+        n = args.calibration_copy_mib * (1 << 20) // 2
+        src = torch.ones(n, dtype=torch.float16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+    traffic = traffic_from_profile(args.workload)
+
     cpu = None
     if args.cpu_sample > 0:
         cpu = cpu_baseline(P, q, top_k, args.cpu_sample, args.cpu_reps)
@@ -151,9 +177,11 @@ def main():
                    "slots_per_page": P.pages.shape[1], "top_k": top_k, "read_temp": read_temp,
                    "route_temp": route_temp, "accumulate": "fp32", "page_table": "seeded shuffle",
                    "nsplit": args.nsplit or ops.default_nsplit(B * idx_h.shape[1], P.pages.shape[1])},
-        "roofline": {"bound": "hbm", "kernel": "library_read_decode (split + merge)",
+        "roofline": {"bound": "hbm", "kernel": "decode_read_kernel",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
                      "algorithmic_bytes": read_bytes, "avg_launch_ms": read_ms,
                      "routed_slots": routed_slots, "route_bytes": route_bytes},
         "cpu_baseline": cpu,

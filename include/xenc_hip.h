@@ -67,11 +67,17 @@ int xenc_route_topk(const float* q, long long ldq, int M, int d,
  * over the valid slots n of the routed chunks c_j = idx[m,j] (entries < 0 are skipped).
  * Each slot row is read from HBM once for both the score and the value.  Page slots are
  * split into nsplit ranges of ceil(slots_per_page/nsplit) slots (nsplit in 1..64).
- * r is fp32 [M, ldr].  Workspace: xenc_decode_workspace_bytes(M, kk, nsplit, d).
+ * r is fp32 [M, ldr].  One kernel launch: the last workgroup of each query merges that
+ * query's partials in a fixed order, so results are deterministic.
+ * Workspace: xenc_decode_workspace_bytes(M, kk, nsplit, d) bytes whose first M ints are zero
+ * before the first call (xenc_decode_workspace_init does that with a kernel, no memset); every
+ * call leaves them zero again, so a workspace is initialised once and reused.  Calls that share
+ * a workspace must not overlap (same stream, or ordered).
  * Replaces the read of LibraryInjector._branch (xenc/injector.py:236-265) when the routed
- * chunks are known; bit-equivalent in intent to reading every chunk with w = 0 off the top-k.
+ * chunks are known: equal to reading every chunk with w = 0 off the top-k.
  */
 size_t xenc_decode_workspace_bytes(int M, int kk, int nsplit, int d);
+int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int M, void* stream);
 int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
                              const void* pages, int slots_per_page, long long page_stride,
                              const int* chunk_page, const int* chunk_nvalid,

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib = None
@@ -32,6 +32,7 @@ SIGNATURES = {
         c_void_p, c_longlong, c_void_p, c_void_p, c_int,  # w_dense, ldw, idx, w_sel, kk
         c_void_p]),                                  # stream
     "xenc_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
+    "xenc_decode_workspace_init": (c_int, [c_void_p, c_size_t, c_int, c_void_p]),
     "xenc_library_read_decode": (c_int, [
         c_void_p, c_longlong, c_int, c_int,          # q, ldq, M, d
         c_void_p, c_int, c_longlong,                 # pages, slots_per_page, page_stride

@@ -7,59 +7,272 @@
 //
 // Work unit = (query m, routed chunk j, slot split s) -> one workgroup of NW waves.
 // Layout per wave: lane owns 8 consecutive dims of each 512-dim column block (CB blocks cover
-// d), so one slot row of d fp16 values is read by the wave as CB coalesced 1 KiB
-// global_load_dwordx4 instructions.  A wave takes SPT slots per step (SPT * CB 16-byte loads in
-// flight per lane), forms the SPT partial dots, finishes them with an xor reduce-scatter
-// (SPT-1 + log2(64/SPT) shuffles for SPT dots) and broadcasts the SPT scores with readlane.
-// The same registers then feed the value accumulation, so each slot row crosses HBM once for
-// both the score and the value.  Each wave keeps its own online-softmax state (max, sum,
-// acc[8*CB]); the NW waves merge through LDS at the end and the workgroup writes one partial
-// (acc[d], max, sum).  A second kernel merges the splits of each routed chunk by log-sum-exp,
-// scales each chunk by w[j] / l_j and sums the chunks in a fixed order (deterministic).
+// d), so one slot row of d fp16 values is read by the wave as CB coalesced 1 KiB buffer loads.
+// A wave takes SPT slots per step: all SPT*CB 16-byte loads are issued before any is used
+// (nontemporal: the pages are streamed once), the SPT partial dots are finished with an xor
+// reduce-scatter and broadcast with readlane, and the same registers then feed the value
+// accumulation, so each slot row crosses HBM once for both the score and the value.  Each wave
+// keeps its own online-softmax state (max, sum, acc[8*CB]); the NW waves merge through LDS and
+// the workgroup writes one partial (acc[d], max, sum).
+//
+// Merge: every workgroup publishes its partial and increments its query's counter; the last
+// workgroup of a query merges the k*nsplit partials of that query by log-sum-exp, scales chunk j
+// by w[j] / l_j and sums the chunks in (j, s) order — a fixed order, so the result is
+// deterministic whichever workgroup arrives last — then re-arms the counter for the next call.
+#include <algorithm>
+
 #include "xenc_common.h"
+
+// Waves per workgroup and slots per wave step (for d <= 2048 / above).  Chosen by measurement.
+#ifndef XENC_DECODE_NW
+#define XENC_DECODE_NW 8
+#endif
+#ifndef XENC_DECODE_SPT
+#define XENC_DECODE_SPT 4
+#endif
+#ifndef XENC_DECODE_SPT_WIDE
+#define XENC_DECODE_SPT_WIDE 2
+#endif
+// 1: two register tiles per wave, the next one loading while the current one is consumed.
+#ifndef XENC_DECODE_PIPELINE
+#define XENC_DECODE_PIPELINE 0
+#endif
+// Score dot products with q rounded to fp16 and v_dot2_f32_f16 (fp32 accumulate).  Measured no
+// faster (the kernel is HBM-bound) and it moves scores by ~1e-5, so it is off.
+#ifndef XENC_DECODE_QF16
+#define XENC_DECODE_QF16 0
+#endif
 
 namespace xenc {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Buffer descriptor word 3 for CDNA (raw buffer, 32-bit format fields unused by b128 loads).
+constexpr int kBufferWord3 = 0x00020000;
+// Cache policy of the page loads: nt (nontemporal).  Streamed reads measured 7.1 TB/s with it
+// against 6.2 TB/s without on MI355X.
+constexpr int kLoadNT = 2;
 
 // Reduce SPT per-lane partial values over the 64 lanes.  On return v[0] holds, in every lane,
-// the full sum for slot j = lane / (64 / SPT).
-template <int SPT>
+// the full sum for slot j = lane / (64 / SPT).  Step with lane bit MASK: lanes with the bit set
+// keep the upper half of the remaining values, send the lower half to their partner and add
+// what they receive.  Written as compile-time recursion so every array index is a constant.
+template <int SPT, int CNT = SPT, int MASK = 32>
 __device__ __forceinline__ void wave_reduce_scatter(float (&v)[SPT], int lane) {
   static_assert(SPT >= 1 && SPT <= 64 && (SPT & (SPT - 1)) == 0, "SPT must be a power of 2");
-  int mask = 32;
+  if constexpr (CNT > 1) {
+    constexpr int H = CNT / 2;
+    const bool hi = (lane & MASK) != 0;
 #pragma unroll
-  for (int cnt = SPT; cnt > 1; cnt >>= 1, mask >>= 1) {
-    const int half = cnt / 2;
-    const bool hi = (lane & mask) != 0;
-#pragma unroll
-    for (int i = 0; i < half; ++i) {
-      const float send = hi ? v[i] : v[i + half];
-      const float keep = hi ? v[i + half] : v[i];
-      v[i] = keep + shfl_xor(send, mask);
+    for (int i = 0; i < H; ++i) {
+      const float send = hi ? v[i] : v[i + H];
+      const float keep = hi ? v[i + H] : v[i];
+      v[i] = keep + shfl_xor(send, MASK);
+    }
+    wave_reduce_scatter<SPT, H, MASK / 2>(v, lane);
+  } else if constexpr (MASK >= 1) {
+    v[0] += shfl_xor(v[0], MASK);
+    wave_reduce_scatter<SPT, 1, MASK / 2>(v, lane);
+  }
+}
+
+struct DecodeWorkspace {
+  int* counters;    // [M]        arrivals per query (0 between calls)
+  float2* part_ml;  // [units]    (max in log2 units, sum) per partial; sum 0 = empty
+  float* part_acc;  // [units, d] un-normalised value sums
+};
+
+// Merge the k*nsplit partials of query m into r[m] (run by the last workgroup of the query).
+__device__ void merge_query(const DecodeWorkspace& ws, int m, const int* __restrict__ idx,
+                            const float* __restrict__ w_sel, int kk, int nsplit, int d, int softmax,
+                            float* __restrict__ r, long long ldr, float* lds) {
+  const int nu = kk * nsplit;
+  float* coef = lds;                                  // [nu]
+  int* unit_of = reinterpret_cast<int*>(lds + nu);    // [nu]
+  __shared__ int nlive;
+  const long long ubase = (long long)m * nu;
+  for (int j = threadIdx.x; j < kk; j += blockDim.x) {
+    const float wj = w_sel[(long long)m * kk + j];
+    const bool live = idx[(long long)m * kk + j] >= 0;
+    float mj = -INFINITY, lj = 0.f;
+    if (live && softmax) {
+      for (int s = 0; s < nsplit; ++s) {
+        const float2 ml = ws.part_ml[ubase + (long long)j * nsplit + s];
+        if (ml.y > 0.f) mj = fmaxf(mj, ml.x);
+      }
+      for (int s = 0; s < nsplit; ++s) {
+        const float2 ml = ws.part_ml[ubase + (long long)j * nsplit + s];
+        if (ml.y > 0.f) lj += ml.y * __builtin_amdgcn_exp2f(ml.x - mj);
+      }
+    }
+    for (int s = 0; s < nsplit; ++s) {
+      const float2 ml = ws.part_ml[ubase + (long long)j * nsplit + s];
+      float c = 0.f;
+      if (live && ml.y > 0.f) c = softmax ? wj * __builtin_amdgcn_exp2f(ml.x - mj) / lj : wj;
+      coef[j * nsplit + s] = c;
     }
   }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // compact the live partials, keeping (j, s) order
+    int n = 0;
+    for (int u = 0; u < nu; ++u) {
+      if (coef[u] != 0.f) {
+        coef[n] = coef[u];
+        unit_of[n] = u;
+        ++n;
+      }
+    }
+    nlive = n;
+  }
+  __syncthreads();
+  const int n = nlive;
+  for (int i = threadIdx.x * 4; i < d; i += blockDim.x * 4) {
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int t = 0; t < n; ++t) {
+      const float c = coef[t];
+      const float4 a = *reinterpret_cast<const float4*>(ws.part_acc + (ubase + unit_of[t]) * d + i);
+      o.x = fmaf(c, a.x, o.x);
+      o.y = fmaf(c, a.y, o.y);
+      o.z = fmaf(c, a.z, o.z);
+      o.w = fmaf(c, a.w, o.w);
+    }
+    *reinterpret_cast<float4*>(r + (long long)m * ldr + i) = o;
+  }
+}
+
+// Per-workgroup constants of the tile loop.
+template <int CB>
+struct TileCtx {
+  __amdgpu_buffer_rsrc_t rsrc;
+  int voff[CB];     // byte offset of this lane's 8 columns in a slot row (last block clamped)
+  int row_bytes;
+  int s1;           // end of this split's valid slots
+  float scale2;     // read_temp * log2(e)
+  float lin_scale;  // 1 / sqrt(n_valid) (linear read)
+  int softmax;
+  int lane;
+};
+
+// Issue the SPT*CB 16-byte loads of the slot rows t0 .. t0+SPT-1.  Rows past s1 re-read row
+// s1-1 (excluded from the softmax through nval) and columns past d re-read the last 8 columns
+// (their q is 0 and their acc is never stored).  Nontemporal: pages are streamed once.
+template <int SPT, int CB>
+__device__ __forceinline__ void load_tile(u32x4 (&kv)[SPT][CB], const TileCtx<CB>& c, int t0) {
 #pragma unroll
-  for (int mk = 64 / SPT / 2; mk >= 1; mk >>= 1) v[0] += shfl_xor(v[0], mk);
+  for (int j = 0; j < SPT; ++j) {
+    const int soff = min(t0 + j, c.s1 - 1) * c.row_bytes;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+      kv[j][cb] = __builtin_amdgcn_raw_buffer_load_b128(c.rsrc, c.voff[cb], soff, kLoadNT);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+#if XENC_DECODE_QF16
+#define QV_PARAM const half8_t (&qh)[CB],
+#define QV_ARG qh,
+#else
+#define QV_PARAM
+#define QV_ARG
+#endif
+
+// Score the SPT rows of a loaded tile, update the wave's online softmax and accumulate the
+// rows into acc with the same registers (each row is read from HBM once).
+template <int SPT, int CB>
+__device__ __forceinline__ void consume_tile(u32x4 (&kv)[SPT][CB], const TileCtx<CB>& c, int t0,
+                                             const float (&qv)[CB][8], QV_PARAM float (&acc)[CB][8],
+                                             float& mrun, float& lrun) {
+  float part[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+    float p = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const half8_t h = __builtin_bit_cast(half8_t, kv[j][cb]);
+#if XENC_DECODE_QF16
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const half2_t kp = {h[2 * i], h[2 * i + 1]};
+        const half2_t qp = {qh[cb][2 * i], qh[cb][2 * i + 1]};
+        p = __builtin_amdgcn_fdot2(kp, qp, p, false);
+      }
+#else
+#pragma unroll
+      for (int i = 0; i < 8; ++i) p = fmaf(qv[cb][i], (float)h[i], p);
+#endif
+    }
+    part[j] = p;
+  }
+  wave_reduce_scatter<SPT>(part, c.lane);
+  float sc[SPT];
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) sc[j] = readlane(part[0], j * (kWave / SPT));
+  const int nval = min(SPT, c.s1 - t0);
+
+  float coef[SPT];
+  if (c.softmax) {
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < SPT; ++j)
+      if (j < nval) tmax = fmaxf(tmax, sc[j] * c.scale2);
+    const float mnew = fmaxf(mrun, tmax);
+    const float alpha = __builtin_amdgcn_exp2f(mrun - mnew);
+    float psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) {
+      coef[j] = j < nval ? __builtin_amdgcn_exp2f(sc[j] * c.scale2 - mnew) : 0.f;
+      psum += coef[j];
+    }
+    lrun = lrun * alpha + psum;
+    mrun = mnew;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[cb][i] *= alpha;
+  } else {
+#pragma unroll
+    for (int j = 0; j < SPT; ++j) coef[j] = j < nval ? sc[j] * c.lin_scale : 0.f;
+    lrun = 1.f;
+    mrun = 0.f;
+  }
+  // Keep the tile packed (2 halves per VGPR) between the score and value loops: without this
+  // the compiler reuses the fp32 conversions of the score loop and holds 8*CB*SPT floats live.
+#pragma unroll
+  for (int j = 0; j < SPT; ++j)
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) asm volatile("" : "+v"(kv[j][cb]));
+#pragma unroll
+  for (int j = 0; j < SPT; ++j) {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) {
+      const half8_t h = __builtin_bit_cast(half8_t, kv[j][cb]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[cb][i] = fmaf(coef[j], (float)h[i], acc[cb][i]);
+    }
+  }
 }
 
 template <int CB, int SPT, int NW>
-__global__ __launch_bounds__(NW* kWave) void decode_split_kernel(
+__global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
     const float* __restrict__ q, long long ldq, int d, const _Float16* __restrict__ pages,
     long long page_stride, int slots_per_page, const int* __restrict__ chunk_page,
     const int* __restrict__ chunk_nvalid, const int* __restrict__ chunk_ptr,
-    const int* __restrict__ q_group, int G, const int* __restrict__ idx, int kk, int nsplit,
-    int split_slots, float scale2, int softmax, float* __restrict__ part_acc,
-    float2* __restrict__ part_ml) {
-  extern __shared__ float red[];  // [NW][d]
+    const int* __restrict__ q_group, int G, const int* __restrict__ idx,
+    const float* __restrict__ w_sel, int kk, int nsplit, int split_slots, float scale2,
+    int softmax, float* __restrict__ r, long long ldr, DecodeWorkspace ws) {
+  extern __shared__ float red[];  // [NW/2][d] wave-merge tree; reused by the merge
   __shared__ float wml[NW][2];
+  __shared__ int is_last;
 
   const int unit = blockIdx.x;
   const int s = unit % nsplit;
   const int mj = unit / nsplit;
   const int m = mj / kk;
   const int lane = threadIdx.x & (kWave - 1);
-  const int wv = threadIdx.x / kWave;
+  // Wave index as a provably uniform value, so row offsets stay in SGPRs (buffer soffset).
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
 
   const int cl = idx[mj];
   const int g = min(max(q_group[m], 0), G - 1);
@@ -73,217 +286,209 @@ __global__ __launch_bounds__(NW* kWave) void decode_split_kernel(
   }
   const int s0 = s * split_slots;
   const int s1 = min(nv, s0 + split_slots);
-  if (s0 >= s1) {  // nothing to read (unrouted entry or a split past the chunk's valid slots)
-    if (threadIdx.x == 0) part_ml[unit] = make_float2(-INFINITY, 0.f);
-    return;
-  }
 
-  float qv[CB][8];
-  const float* qrow = q + (long long)m * ldq;
+  if (s0 < s1) {  // workgroup-uniform: a routed split with valid slots
+    float qv[CB][8];
+    const float* qrow = q + (long long)m * ldq;
+    int voff[CB];  // byte offset of this lane's 8 columns in a slot row (last block clamped)
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    const int d0 = (cb * kWave + lane) * 8;
-    if (d0 < d) {
-      const float4 a = *reinterpret_cast<const float4*>(qrow + d0);
-      const float4 b = *reinterpret_cast<const float4*>(qrow + d0 + 4);
-      qv[cb][0] = a.x; qv[cb][1] = a.y; qv[cb][2] = a.z; qv[cb][3] = a.w;
-      qv[cb][4] = b.x; qv[cb][5] = b.y; qv[cb][6] = b.z; qv[cb][7] = b.w;
-    } else {
+    for (int cb = 0; cb < CB; ++cb) {
+      const int d0 = (cb * kWave + lane) * 8;
+      voff[cb] = min(d0, d - 8) * 2;
+      if (d0 < d) {
+        const float4 a = *reinterpret_cast<const float4*>(qrow + d0);
+        const float4 b = *reinterpret_cast<const float4*>(qrow + d0 + 4);
+        qv[cb][0] = a.x; qv[cb][1] = a.y; qv[cb][2] = a.z; qv[cb][3] = a.w;
+        qv[cb][4] = b.x; qv[cb][5] = b.y; qv[cb][6] = b.z; qv[cb][7] = b.w;
+      } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qv[cb][i] = 0.f;
-    }
-  }
-
-  float acc[CB][8];
-#pragma unroll
-  for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[cb][i] = 0.f;
-  float mrun = -INFINITY, lrun = 0.f;
-  const float lin_scale = rsqrtf((float)nv);
-  const _Float16* pg = pages + pbase;
-
-  for (int t0 = s0 + wv * SPT; t0 < s1; t0 += NW * SPT) {
-    // Unconditional loads: rows past s1 re-read row s1-1 (excluded below through nval) and
-    // columns past d re-read the last 8 columns (their q is 0 and their acc is never stored).
-    uint4 kv[SPT][CB];
-#pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-      const _Float16* row = pg + (long long)min(t0 + j, s1 - 1) * d;
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-        kv[j][cb] = *reinterpret_cast<const uint4*>(row + min((cb * kWave + lane) * 8, d - 8));
-    }
-    float part[SPT];
-#pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-      float p = 0.f;
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const half8_t h = __builtin_bit_cast(half8_t, kv[j][cb]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) p = fmaf(qv[cb][i], (float)h[i], p);
-      }
-      part[j] = p;
-    }
-    wave_reduce_scatter<SPT>(part, lane);
-    float sc[SPT];
-#pragma unroll
-    for (int j = 0; j < SPT; ++j) sc[j] = readlane(part[0], j * (kWave / SPT));
-    const int nval = min(SPT, s1 - t0);
-
-    float coef[SPT];
-    if (softmax) {
-      float tmax = -INFINITY;
-#pragma unroll
-      for (int j = 0; j < SPT; ++j)
-        if (j < nval) tmax = fmaxf(tmax, sc[j] * scale2);
-      const float mnew = fmaxf(mrun, tmax);
-      const float alpha = exp2f(mrun - mnew);
-      float psum = 0.f;
-#pragma unroll
-      for (int j = 0; j < SPT; ++j) {
-        coef[j] = j < nval ? exp2f(sc[j] * scale2 - mnew) : 0.f;
-        psum += coef[j];
-      }
-      lrun = lrun * alpha + psum;
-      mrun = mnew;
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[cb][i] *= alpha;
-    } else {
-#pragma unroll
-      for (int j = 0; j < SPT; ++j) coef[j] = j < nval ? sc[j] * lin_scale : 0.f;
-      lrun = 1.f;
-      mrun = 0.f;
-    }
-    // Keep the tile packed (2 halves per VGPR) between the score and value loops: without this the
-    // compiler reuses the fp32 conversions of the score loop and holds 8*CB*SPT floats live.
-#pragma unroll
-    for (int j = 0; j < SPT; ++j)
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-        asm volatile("" : "+v"(kv[j][cb].x), "+v"(kv[j][cb].y), "+v"(kv[j][cb].z),
-                     "+v"(kv[j][cb].w));
-#pragma unroll
-    for (int j = 0; j < SPT; ++j) {
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const half8_t h = __builtin_bit_cast(half8_t, kv[j][cb]);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[cb][i] = fmaf(coef[j], (float)h[i], acc[cb][i]);
+        for (int i = 0; i < 8; ++i) qv[cb][i] = 0.f;
       }
     }
-  }
+#if XENC_DECODE_QF16
+    half8_t qh[CB];
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qh[cb][i] = (_Float16)qv[cb][i];
+#endif
 
-  // Merge the NW waves of this workgroup (fixed order: deterministic).
-  if (lane == 0) {
-    wml[wv][0] = mrun;
-    wml[wv][1] = lrun;
-  }
-  __syncthreads();
-  float mall = -INFINITY;
+    float acc[CB][8];
 #pragma unroll
-  for (int w = 0; w < NW; ++w)
-    if (wml[w][1] > 0.f) mall = fmaxf(mall, wml[w][0]);
-  const float wscale = lrun > 0.f ? (softmax ? exp2f(mrun - mall) : 1.f) : 0.f;
-  float* myred = red + wv * d;
+    for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-  for (int cb = 0; cb < CB; ++cb) {
-    const int d0 = (cb * kWave + lane) * 8;
-    if (d0 < d) {
-      *reinterpret_cast<float4*>(myred + d0) =
-          make_float4(acc[cb][0] * wscale, acc[cb][1] * wscale, acc[cb][2] * wscale,
-                      acc[cb][3] * wscale);
-      *reinterpret_cast<float4*>(myred + d0 + 4) =
-          make_float4(acc[cb][4] * wscale, acc[cb][5] * wscale, acc[cb][6] * wscale,
-                      acc[cb][7] * wscale);
+      for (int i = 0; i < 8; ++i) acc[cb][i] = 0.f;
+    float mrun = -INFINITY, lrun = 0.f;
+    const float lin_scale = rsqrtf((float)nv);
+    // One buffer descriptor per page: loads take a uniform row offset (soffset) plus this
+    // lane's column offset, so no 64-bit address is kept per load.
+    const __amdgpu_buffer_rsrc_t page_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<_Float16*>(pages + pbase), 0, slots_per_page * d * 2, kBufferWord3);
+    const int row_bytes = d * 2;
+
+    TileCtx<CB> ctx;
+    ctx.rsrc = page_rsrc;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb) ctx.voff[cb] = voff[cb];
+    ctx.row_bytes = row_bytes;
+    ctx.s1 = s1;
+    ctx.scale2 = scale2;
+    ctx.lin_scale = lin_scale;
+    ctx.softmax = softmax;
+    ctx.lane = lane;
+    // With XENC_DECODE_PIPELINE the tile after the one being consumed is already in flight; the
+    // steady-state loop has no branch around a load, so every wait is an exact vmcnt.
+    const int step = NW * SPT;
+    const int first = s0 + wv * SPT;
+    const int ntile = first < s1 ? (s1 - first + step - 1) / step : 0;
+#if XENC_DECODE_PIPELINE
+    if (ntile > 0) {
+      u32x4 ka[SPT][CB], kb[SPT][CB];
+      load_tile<SPT, CB>(ka, ctx, first);
+      int i = 0;
+      for (; i + 2 < ntile; i += 2) {
+        load_tile<SPT, CB>(kb, ctx, first + (i + 1) * step);
+        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
+        load_tile<SPT, CB>(ka, ctx, first + (i + 2) * step);
+        consume_tile<SPT, CB>(kb, ctx, first + (i + 1) * step, qv, QV_ARG acc, mrun, lrun);
+      }
+      if (i + 1 < ntile) {
+        load_tile<SPT, CB>(kb, ctx, first + (i + 1) * step);
+        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
+        consume_tile<SPT, CB>(kb, ctx, first + (i + 1) * step, qv, QV_ARG acc, mrun, lrun);
+      } else {
+        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
+      }
     }
-  }
-  __syncthreads();
-  float* out = part_acc + (long long)unit * d;
-  for (int i = threadIdx.x * 4; i < d; i += NW * kWave * 4) {
-    float4 t = *reinterpret_cast<const float4*>(red + i);
-#pragma unroll
-    for (int w = 1; w < NW; ++w) {
-      const float4 u = *reinterpret_cast<const float4*>(red + w * d + i);
-      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+#else
+    for (int i = 0; i < ntile; ++i) {
+      u32x4 ka[SPT][CB];
+      load_tile<SPT, CB>(ka, ctx, first + i * step);
+      consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
     }
-    *reinterpret_cast<float4*>(out + i) = t;
-  }
-  if (threadIdx.x == 0) {
-    float lsum = 0.f;
+#endif
+
+    // Merge the NW waves of this workgroup: rescale each wave to the common max, then a tree
+    // over LDS (round h: waves h..2h-1 hand their sums to waves 0..h-1) — a fixed order, so
+    // deterministic — and wave 0 writes the workgroup's partial from its registers.
+    if (lane == 0) {
+      wml[wv][0] = mrun;
+      wml[wv][1] = lrun;
+    }
+    __syncthreads();
+    float mall = -INFINITY;
 #pragma unroll
     for (int w = 0; w < NW; ++w)
-      if (wml[w][1] > 0.f) lsum += wml[w][1] * (softmax ? exp2f(wml[w][0] - mall) : 1.f);
-    part_ml[unit] = make_float2(softmax ? mall : 0.f, lsum);
+      if (wml[w][1] > 0.f) mall = fmaxf(mall, wml[w][0]);
+    const float wscale = lrun > 0.f ? (softmax ? __builtin_amdgcn_exp2f(mrun - mall) : 1.f) : 0.f;
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[cb][i] *= wscale;
+#pragma unroll
+    for (int h = NW / 2; h >= 1; h /= 2) {
+      if (wv >= h && wv < 2 * h) {
+        float* dst = red + (wv - h) * d;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const int d0 = (cb * kWave + lane) * 8;
+          if (d0 < d) {
+            *reinterpret_cast<float4*>(dst + d0) =
+                make_float4(acc[cb][0], acc[cb][1], acc[cb][2], acc[cb][3]);
+            *reinterpret_cast<float4*>(dst + d0 + 4) =
+                make_float4(acc[cb][4], acc[cb][5], acc[cb][6], acc[cb][7]);
+          }
+        }
+      }
+      __syncthreads();
+      if (wv < h) {
+        const float* src = red + wv * d;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) {
+          const int d0 = (cb * kWave + lane) * 8;
+          if (d0 < d) {
+            const float4 a = *reinterpret_cast<const float4*>(src + d0);
+            const float4 b = *reinterpret_cast<const float4*>(src + d0 + 4);
+            acc[cb][0] += a.x; acc[cb][1] += a.y; acc[cb][2] += a.z; acc[cb][3] += a.w;
+            acc[cb][4] += b.x; acc[cb][5] += b.y; acc[cb][6] += b.z; acc[cb][7] += b.w;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (wv == 0) {
+      float* out = ws.part_acc + (long long)unit * d;
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int d0 = (cb * kWave + lane) * 8;
+        if (d0 < d) {
+          *reinterpret_cast<float4*>(out + d0) =
+              make_float4(acc[cb][0], acc[cb][1], acc[cb][2], acc[cb][3]);
+          *reinterpret_cast<float4*>(out + d0 + 4) =
+              make_float4(acc[cb][4], acc[cb][5], acc[cb][6], acc[cb][7]);
+        }
+      }
+    }
+    if (threadIdx.x == 0) {
+      float lsum = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w)
+        if (wml[w][1] > 0.f)
+          lsum += wml[w][1] * (softmax ? __builtin_amdgcn_exp2f(wml[w][0] - mall) : 1.f);
+      ws.part_ml[unit] = make_float2(softmax ? mall : 0.f, lsum);
+    }
+  } else if (threadIdx.x == 0) {  // nothing to read: an unrouted entry or a split past the tail
+    ws.part_ml[unit] = make_float2(-INFINITY, 0.f);
   }
-}
 
-// r[m] = sum_j w_sel[m,j] / l_j * sum_s exp2(m_s - M_j) acc_s   (softmax)
-// r[m] = sum_j w_sel[m,j] * sum_s acc_s                          (linear)
-__global__ __launch_bounds__(256) void decode_merge_kernel(
-    const float* __restrict__ part_acc, const float2* __restrict__ part_ml,
-    const int* __restrict__ idx, const float* __restrict__ w_sel, int kk, int nsplit, int d,
-    int softmax, float* __restrict__ r, long long ldr) {
-  extern __shared__ float coef[];  // [kk * nsplit]
-  const int m = blockIdx.x;
-  const long long ubase = (long long)m * kk * nsplit;
-  for (int j = threadIdx.x; j < kk; j += blockDim.x) {
-    const float wj = w_sel[(long long)m * kk + j];
-    const bool live = idx[(long long)m * kk + j] >= 0;
-    float mj = -INFINITY, lj = 0.f;
-    if (live) {
-      for (int s = 0; s < nsplit; ++s) {
-        const float2 ml = part_ml[ubase + (long long)j * nsplit + s];
-        if (ml.y > 0.f) mj = fmaxf(mj, ml.x);
-      }
-      for (int s = 0; s < nsplit; ++s) {
-        const float2 ml = part_ml[ubase + (long long)j * nsplit + s];
-        if (ml.y > 0.f) lj += softmax ? ml.y * exp2f(ml.x - mj) : 0.f;
-      }
-    }
-    for (int s = 0; s < nsplit; ++s) {
-      const float2 ml = part_ml[ubase + (long long)j * nsplit + s];
-      float c = 0.f;
-      if (live && ml.y > 0.f) c = softmax ? wj * exp2f(ml.x - mj) / lj : wj;
-      coef[j * nsplit + s] = c;
-    }
+  // Publish this partial device-wide, then count it; the last workgroup of query m merges.
+  // The barrier orders every wave's partial stores before thread 0's agent-scope release (one
+  // L2 write-back per workgroup, not per wave); only the last workgroup pays the acquire.
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int prev = __hip_atomic_fetch_add(&ws.counters[m], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    is_last = prev == kk * nsplit - 1;
+    if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  const int nu = kk * nsplit;
-  for (int i = threadIdx.x * 4; i < d; i += blockDim.x * 4) {
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int u = 0; u < nu; ++u) {
-      const float c = coef[u];
-      if (c != 0.f) {
-        const float4 a = *reinterpret_cast<const float4*>(part_acc + (ubase + u) * d + i);
-        o.x = fmaf(c, a.x, o.x);
-        o.y = fmaf(c, a.y, o.y);
-        o.z = fmaf(c, a.z, o.z);
-        o.w = fmaf(c, a.w, o.w);
-      }
-    }
-    *reinterpret_cast<float4*>(r + (long long)m * ldr + i) = o;
-  }
+  if (!is_last) return;
+  merge_query(ws, m, idx, w_sel, kk, nsplit, d, softmax, r, ldr, red);
+  if (threadIdx.x == 0) atomicExch(&ws.counters[m], 0);  // re-arm for the next call
+}
+
+__global__ void fill_zero_kernel(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+static size_t host_align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+static DecodeWorkspace carve(void* base, int M, int kk, int nsplit) {
+  const size_t units = (size_t)M * kk * nsplit;
+  char* p = static_cast<char*>(base);
+  DecodeWorkspace ws;
+  ws.counters = reinterpret_cast<int*>(p);
+  p += host_align256((size_t)M * sizeof(int));
+  ws.part_ml = reinterpret_cast<float2*>(p);
+  p += host_align256(units * sizeof(float2));
+  ws.part_acc = reinterpret_cast<float*>(p);
+  return ws;
 }
 
 template <int CB>
-static void launch_split(dim3 grid, size_t lds, hipStream_t st, const float* q, long long ldq,
-                         int d, const _Float16* pages, long long page_stride, int spp,
-                         const int* chunk_page, const int* chunk_nvalid, const int* chunk_ptr,
-                         const int* q_group, int G, const int* idx, int kk, int nsplit,
-                         int split_slots, float scale2, int softmax, float* part_acc,
-                         float2* part_ml) {
-  constexpr int NW = 4;
-  constexpr int SPT = CB <= 4 ? 8 : 4;
-  hipLaunchKernelGGL((decode_split_kernel<CB, SPT, NW>), grid, dim3(NW * kWave), lds, st, q, ldq,
+static void launch_read(dim3 grid, size_t lds, hipStream_t st, const float* q, long long ldq,
+                        int d, const _Float16* pages, long long page_stride, int spp,
+                        const int* chunk_page, const int* chunk_nvalid, const int* chunk_ptr,
+                        const int* q_group, int G, const int* idx, const float* w_sel, int kk,
+                        int nsplit, int split_slots, float scale2, int softmax, float* r,
+                        long long ldr, const DecodeWorkspace& ws) {
+  constexpr int NW = XENC_DECODE_NW;
+  constexpr int SPT = CB <= 4 ? XENC_DECODE_SPT : (CB == 5 ? XENC_DECODE_SPT_WIDE : 1);
+  hipLaunchKernelGGL((decode_read_kernel<CB, SPT, NW>), grid, dim3(NW * kWave), lds, st, q, ldq,
                      d, pages, page_stride, spp, chunk_page, chunk_nvalid, chunk_ptr, q_group, G,
-                     idx, kk, nsplit, split_slots, scale2, softmax, part_acc, part_ml);
+                     idx, w_sel, kk, nsplit, split_slots, scale2, softmax, r, ldr, ws);
 }
-
-static size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 }  // namespace xenc
 
@@ -292,7 +497,20 @@ using namespace xenc;
 extern "C" size_t xenc_decode_workspace_bytes(int M, int kk, int nsplit, int d) {
   if (M <= 0 || kk <= 0 || nsplit <= 0 || d <= 0) return 0;
   const size_t units = (size_t)M * kk * nsplit;
-  return align256(units * d * sizeof(float)) + align256(units * sizeof(float2));
+  return host_align256((size_t)M * sizeof(int)) + host_align256(units * sizeof(float2)) +
+         host_align256(units * d * sizeof(float));
+}
+
+extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int M,
+                                          void* stream) {
+  if (M <= 0) return XENC_EINVAL;
+  if (!workspace) return XENC_ENULL;
+  if (!aligned16(workspace)) return XENC_EALIGN;
+  if (workspace_bytes < (size_t)M * sizeof(int)) return XENC_EWORKSPACE;
+  const int blocks = std::min((M + 255) / 256, 1024);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<int*>(workspace), M);
+  return check_launch();
 }
 
 extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
@@ -308,6 +526,7 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
   if (nsplit < 1 || nsplit > 64) return XENC_EINVAL;
   if (ldq < d || ldr < d || ldq % 4 != 0 || ldr % 4 != 0) return XENC_EINVAL;
   if (page_stride < (long long)slots_per_page * d || page_stride % 8 != 0) return XENC_EINVAL;
+  if ((long long)slots_per_page * d * 2 > 0x7fffffffLL) return XENC_EINVAL;  // buffer range
   if (M == 0) return XENC_OK;
   if (!q || !pages || !chunk_page || !chunk_nvalid || !chunk_ptr || !q_group || !idx || !w_sel ||
       !r || !workspace)
@@ -317,26 +536,24 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
   if (workspace_bytes < xenc_decode_workspace_bytes(M, kk, nsplit, d)) return XENC_EWORKSPACE;
   const long long units = (long long)M * kk * nsplit;
   if (units > 0x7fffffffLL) return XENC_EINVAL;
+  // LDS: the wave-merge tree [NW/2][d], or the merge's coefficient list [2 * kk * nsplit].
+  const size_t lds =
+      std::max((size_t)std::max(XENC_DECODE_NW / 2, 1) * d, (size_t)2 * kk * nsplit) * sizeof(float);
+  if (lds > 64 * 1024) return XENC_EINVAL;
 
-  const size_t clds = (size_t)kk * nsplit * sizeof(float);
-  if (clds > 64 * 1024) return XENC_EINVAL;
-  const size_t units_sz = (size_t)units;
-  float* part_acc = static_cast<float*>(workspace);
-  float2* part_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
-                                              align256(units_sz * d * sizeof(float)));
+  const DecodeWorkspace ws = carve(workspace, M, kk, nsplit);
   const int split_slots = (slots_per_page + nsplit - 1) / nsplit;
   const float scale2 = read_temp * kLog2e;
   const _Float16* pg = static_cast<const _Float16*>(pages);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)units);
-  const size_t lds = (size_t)4 * d * sizeof(float);
   const int cb = (d + 511) / 512;
   switch (cb) {
 #define XENC_CASE(N)                                                                           \
   case N:                                                                                      \
-    launch_split<N>(grid, lds, st, q, ldq, d, pg, page_stride, slots_per_page, chunk_page,     \
-                    chunk_nvalid, chunk_ptr, q_group, G, idx, kk, nsplit, split_slots, scale2, \
-                    softmax, part_acc, part_ml);                                               \
+    launch_read<N>(grid, lds, st, q, ldq, d, pg, page_stride, slots_per_page, chunk_page,      \
+                   chunk_nvalid, chunk_ptr, q_group, G, idx, w_sel, kk, nsplit, split_slots,   \
+                   scale2, softmax, r, ldr, ws);                                               \
     break;
     XENC_CASE(1) XENC_CASE(2) XENC_CASE(3) XENC_CASE(4)
     XENC_CASE(5) XENC_CASE(6) XENC_CASE(7) XENC_CASE(8)
@@ -344,9 +561,5 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
     default:
       return XENC_EINVAL;
   }
-  int rc = check_launch();
-  if (rc) return rc;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3(M), dim3(256), clds, st, part_acc, part_ml, idx,
-                     w_sel, kk, nsplit, d, softmax, r, ldr);
   return check_launch();
 }

@@ -6,15 +6,17 @@
 //   if top_k and top_k < C: keep topk(top_k), the rest -inf
 //   w = softmax(logit, -1)
 //
-// One workgroup per query row.  Each wave takes chunks c = wave, wave + NW, ...; a lane owns
-// float4 columns lane, lane+64, ... of the d-long dot product (coalesced 1 KiB per wave load),
-// and the dot is finished with a fixed xor-butterfly, so the fp32 summation order is the same
-// on every call.  Dots land in LDS; wave 0 then runs top_k rounds of a wave-wide argmax.
+// One workgroup (NW = 8 waves) per query row.  A lane owns float4 columns
+// (cb*64 + lane)*4 of the d-long dot product, holds q for them in registers, and each wave
+// scores CPI chunks per step (CPI * CB4 float4 loads in flight per lane), so the chunk rows of a
+// library stream in parallel instead of one dependent dot at a time.  Each dot is finished
+// with a fixed xor-butterfly: the fp32 summation order is the same on every call.  Dots land in
+// LDS; wave 0 then runs top_k rounds of a wave-wide argmax.
 #include "xenc_common.h"
 
 namespace xenc {
 
-template <int NW>
+template <int CB4, int CPI, int NW>
 __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
     const float* __restrict__ q, long long ldq, int d, const float* __restrict__ S,
     const int* __restrict__ chunk_ptr, const int* __restrict__ q_group, int G, int top_k,
@@ -36,21 +38,41 @@ __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
   const int C = min(chunk_ptr[g + 1] - c0, ldw);
   const float* qrow = q + (long long)m * ldq;
 
-  for (int c = wv; c < C; c += NW) {
-    const float* srow = S + (long long)(c0 + c) * d;
-    float acc = 0.f;
-    for (int i = lane * 4; i < d; i += kWave * 4) {
-      const float4 a = *reinterpret_cast<const float4*>(qrow + i);
-      const float4 b = *reinterpret_cast<const float4*>(srow + i);
-      acc = fmaf(a.x, b.x, acc);
-      acc = fmaf(a.y, b.y, acc);
-      acc = fmaf(a.z, b.z, acc);
-      acc = fmaf(a.w, b.w, acc);
+  // Columns past d (last block only) re-read the last float4 with q = 0 there.
+  float4 qv[CB4];
+#pragma unroll
+  for (int cb = 0; cb < CB4; ++cb) {
+    const int i = (cb * kWave + lane) * 4;
+    qv[cb] = i < d ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  for (int cbase = wv; cbase < C; cbase += NW * CPI) {
+    float acc[CPI];
+#pragma unroll
+    for (int u = 0; u < CPI; ++u) {
+      const int c = min(cbase + u * NW, C - 1);
+      const float* srow = S + (long long)(c0 + c) * d;
+      float a = 0.f;
+#pragma unroll
+      for (int cb = 0; cb < CB4; ++cb) {
+        // Summary keys are streamed once per call: nontemporal loads.
+        typedef float f32x4 __attribute__((ext_vector_type(4)));
+        const f32x4 b = __builtin_nontemporal_load(
+            reinterpret_cast<const f32x4*>(srow + min((cb * kWave + lane) * 4, d - 4)));
+        a = fmaf(qv[cb].x, b.x, a);
+        a = fmaf(qv[cb].y, b.y, a);
+        a = fmaf(qv[cb].z, b.z, a);
+        a = fmaf(qv[cb].w, b.w, a);
+      }
+      acc[u] = a;
     }
-    acc = wave_sum(acc);
-    if (lane == 0) {
-      dots[c] = acc;
-      taken[c] = 0;
+#pragma unroll
+    for (int u = 0; u < CPI; ++u) {
+      const float a = wave_sum(acc[u]);
+      const int c = cbase + u * NW;
+      if (lane == 0 && c < C) {
+        dots[c] = a;
+        taken[c] = 0;
+      }
     }
   }
   float* wrow = w_dense + (long long)m * ldw;
@@ -130,11 +152,25 @@ extern "C" int xenc_route_topk(const float* q, long long ldq, int M, int d, cons
   if (M == 0) return XENC_OK;
   if (!q || !S || !chunk_ptr || !q_group || !w_dense || !idx || !w_sel) return XENC_ENULL;
   if (!aligned16(q) || !aligned16(S)) return XENC_EALIGN;
-  constexpr int NW = 4;
+  if (d > 4096) return XENC_EINVAL;
   const size_t lds = (size_t)ldw * 3 * sizeof(float);
   if (lds > 64 * 1024) return XENC_EINVAL;  // up to 5461 chunks per library
-  hipLaunchKernelGGL(route_topk_kernel<NW>, dim3(M), dim3(NW * kWave), lds,
-                     reinterpret_cast<hipStream_t>(stream), q, ldq, d, S, chunk_ptr, q_group, G,
-                     top_k, route_temp, w_dense, (int)ldw, idx, w_sel, kk);
+  constexpr int NW = 8;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int cb4 = (d + 255) / 256;
+  switch (cb4) {
+#define XENC_CASE(N)                                                                           \
+  case N:                                                                                      \
+    hipLaunchKernelGGL((route_topk_kernel<N, (N <= 8 ? 4 : 2), NW>), dim3(M), dim3(NW * kWave), \
+                       lds, st, q, ldq, d, S, chunk_ptr, q_group, G, top_k, route_temp,        \
+                       w_dense, (int)ldw, idx, w_sel, kk);                                     \
+    break;
+    XENC_CASE(1) XENC_CASE(2) XENC_CASE(3) XENC_CASE(4) XENC_CASE(5) XENC_CASE(6)
+    XENC_CASE(7) XENC_CASE(8) XENC_CASE(9) XENC_CASE(10) XENC_CASE(11) XENC_CASE(12)
+    XENC_CASE(13) XENC_CASE(14) XENC_CASE(15) XENC_CASE(16)
+#undef XENC_CASE
+    default:
+      return XENC_EINVAL;
+  }
   return check_launch();
 }

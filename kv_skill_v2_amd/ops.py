@@ -177,10 +177,34 @@ def route_topk(q: torch.Tensor, lib_: PagedLibrary, q_group=None, top_k: int = 0
 
 
 def default_nsplit(units: int, slots_per_page: int) -> int:
-    """Slot splits per routed page: enough workgroups to fill 256 CUs several times over while
-    keeping each split >= 64 slots (the partial it writes is 1/64 of the bytes it reads or less)."""
-    want = max(1, math.ceil(2048 / max(units, 1)))
-    return int(max(1, min(want, slots_per_page // 64, 64)))
+    """Slot splits per routed page.  With >= 512 (query, page) units one workgroup per page
+    fills the 256 CUs (measured best on the B = 64 batched decode); fewer units are split down
+    to 16-slot pieces so a single query still spreads over many CUs."""
+    want = max(1, math.ceil(512 / max(units, 1)))
+    return int(max(1, min(want, max(1, slots_per_page // 16), 64)))
+
+
+class _Workspaces:
+    """Decode workspaces, one per (device, stream), grown on demand.  Its arrival counters are
+    zeroed once by a kernel (xenc_decode_workspace_init) and every call leaves them zero."""
+
+    def __init__(self):
+        self._ws = {}
+
+    def get(self, device: torch.device, stream: int, nbytes: int, M: int) -> torch.Tensor:
+        key = (device.index, stream)
+        buf, zeroed = self._ws.get(key, (None, 0))
+        if buf is None or buf.numel() < nbytes or zeroed < M:
+            size = max(nbytes, buf.numel() if buf is not None else 0)
+            buf = torch.empty(size, dtype=torch.uint8, device=device)
+            zeroed = max(M, zeroed)
+            check(lib().xenc_decode_workspace_init(ptr(buf), size, zeroed, stream),
+                  "xenc_decode_workspace_init")
+            self._ws[key] = (buf, zeroed)
+        return buf
+
+
+_WORKSPACES = _Workspaces()
 
 
 def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, w_sel: torch.Tensor,
@@ -205,12 +229,13 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
     ns = int(nsplit) if nsplit is not None else default_nsplit(M * kk, lib_.slots_per_page)
     L = lib()
     wsb = L.xenc_decode_workspace_bytes(M, kk, ns, lib_.d)
-    ws = torch.empty(wsb, dtype=torch.uint8, device=q.device)
+    st = stream_handle(q.device)
+    ws = _WORKSPACES.get(q.device, st, wsb, M)
     rc = L.xenc_library_read_decode(
         ptr(q), q.stride(0), M, lib_.d, ptr(lib_.pages), lib_.slots_per_page,
         lib_.pages.stride(0), ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), ptr(lib_.chunk_ptr),
         ptr(g), lib_.n_libraries, ptr(idx), ptr(w_sel), kk, float(read_temp), int(bool(softmax)),
-        ns, ptr(r), r.stride(0), ptr(ws), wsb, stream_handle(q.device))
+        ns, ptr(r), r.stride(0), ptr(ws), ws.numel(), st)
     check(rc, "xenc_library_read_decode")
     return r
 

@@ -176,3 +176,50 @@ def test_full_size_decode_workloads(dev, name):
         ref, _ = O.branch_read(qc[b].view(1, 1, -1).double(), K.cpu().double(), M.cpu(), S.cpu().double(),
                                top_k=top_k)
         _check_close(r[b], ref.view(-1), f"{name} row {b}")
+
+
+def test_repeated_calls_are_bit_identical(dev):
+    """The per-query arrival counters re-arm themselves: many calls in a row (different nsplit,
+    hence different workspace layouts) give bit-identical results."""
+    say("repeat determinism", dict(d=1024, N=128))
+    P = synth.pool([9, 4, 12, 6], 128, 1024, device="cpu", tail_lo=1)
+    lib = _to_lib(P, dev)
+    qg = torch.tensor([0, 1, 2, 3, 3, 2, 1, 0], dtype=torch.int32, device=dev)
+    q = synth.queries(8, 1024, device="cpu", seed=21).to(dev)
+    _, idx, wsel = ops.route_topk(q, lib, qg, top_k=3)
+    ref = {ns: ops.library_read_decode(q, lib, idx, wsel, qg, nsplit=ns) for ns in (1, 4)}
+    for rep in range(6):
+        ns = (1, 4)[rep % 2]
+        assert torch.equal(ops.library_read_decode(q, lib, idx, wsel, qg, nsplit=ns), ref[ns]), (rep, ns)
+
+
+def test_graph_capture_and_replay(dev):
+    """Route + read captured in a HIP graph and replayed several times with eager work and new
+    query values in between; every replay equals the eager result for the same inputs."""
+    say("graph capture", dict(d=2048, N=512))
+    P = synth.pool([6, 10, 3], 512, 2048, device="cpu", tail_lo=1)
+    lib = _to_lib(P, dev)
+    qg = torch.tensor([0, 1, 2, 1], dtype=torch.int32, device=dev)
+    q = synth.queries(4, 2048, device="cpu", seed=31).to(dev)
+
+    def step():
+        _, idx, wsel = ops.route_topk(q, lib, qg, top_k=4)
+        return ops.library_read_decode(q, lib, idx, wsel, qg)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()                                   # warm-up: allocates this stream's workspace
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = step()
+    for rep in range(4):
+        q.copy_(synth.queries(4, 2048, device="cpu", seed=40 + rep).to(dev))
+        g.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        _ = torch.randn(1024, device=dev).sum()   # eager work between replays
+        ref = step()
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), rep
