@@ -1,0 +1,96 @@
+"""Summaries of rocprofv3 output (CSV mode) for the Library-read kernels.
+
+    python -m kv_skill_v2_amd.profiling stats  <kernel_stats.csv> [--match decode_read_kernel]
+    python -m kv_skill_v2_amd.profiling traffic <fetch counter_collection.csv> <write counter_collection.csv>
+        --kernel decode_read_kernel --copy-bytes 1073741824 [--json out.json]
+
+`traffic` averages FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the dispatches of the
+kernel, and scales each by what the same counter reads for the plain copy kernel of known size
+that `bench.py --calibration-copy-mib` launches (expected: copy_bytes read, copy_bytes written).
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import statistics
+import sys
+
+
+def _short(name: str, width: int = 60) -> str:
+    return name if len(name) <= width else name[: width - 3] + "..."
+
+
+def kernel_stats(path: str, match: str | None = None, top: int = 12) -> list[dict]:
+    rows = list(csv.DictReader(open(path)))
+    out = []
+    for r in rows:
+        if match and match not in r["Name"]:
+            continue
+        out.append({"name": r["Name"], "calls": int(r["Calls"]), "avg_us": float(r["AverageNs"]) / 1e3,
+                    "min_us": float(r["MinNs"]) / 1e3, "max_us": float(r["MaxNs"]) / 1e3,
+                    "pct": float(r["Percentage"])})
+    return out[:top]
+
+
+def _counter(path: str, counter: str) -> list[tuple[str, float]]:
+    rows = list(csv.DictReader(open(path)))
+    return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows if r["Counter_Name"] == counter]
+
+
+def _copy_kernel(vals: list[tuple[str, float]]) -> float:
+    """The calibration copy: the largest fp16 copy dispatches, which come last in the run."""
+    cands = [v for n, v in vals if "copy" in n.lower()]
+    if not cands:
+        raise SystemExit("no copy kernel dispatches found (run bench.py with --calibration-copy-mib)")
+    return statistics.median(sorted(cands)[-3:])
+
+
+def traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int) -> dict:
+    f = _counter(fetch_csv, "FETCH_SIZE")
+    w = _counter(write_csv, "WRITE_SIZE")
+    fk = [v for n, v in f if kernel in n]
+    wk = [v for n, v in w if kernel in n]
+    if not fk or not wk:
+        raise SystemExit(f"kernel {kernel!r} not found in the counter files")
+    fetch_scale = copy_bytes / (_copy_kernel(f) * 1024.0)
+    write_scale = copy_bytes / (_copy_kernel(w) * 1024.0)
+    fetch_b = statistics.mean(fk) * 1024.0 * fetch_scale
+    write_b = statistics.mean(wk) * 1024.0 * write_scale
+    return {"kernel": kernel, "fetch_bytes": fetch_b, "write_bytes": write_b,
+            "bytes_per_launch": fetch_b + write_b, "fetch_scale": fetch_scale,
+            "write_scale": write_scale, "dispatches": len(fk)}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("csv")
+    s.add_argument("--match")
+    t = sub.add_parser("traffic")
+    t.add_argument("fetch_csv")
+    t.add_argument("write_csv")
+    t.add_argument("--kernel", required=True)
+    t.add_argument("--copy-bytes", type=int, required=True)
+    t.add_argument("--json")
+    t.add_argument("--source", default="")
+    a = ap.parse_args(argv)
+    if a.cmd == "stats":
+        print(f"{'kernel':60s} {'calls':>6s} {'avg us':>10s} {'min us':>10s} {'max us':>10s} {'%':>6s}")
+        for r in kernel_stats(a.csv, a.match):
+            print(f"{_short(r['name']):60s} {r['calls']:6d} {r['avg_us']:10.2f} {r['min_us']:10.2f} "
+                  f"{r['max_us']:10.2f} {r['pct']:6.2f}")
+    else:
+        res = traffic(a.fetch_csv, a.write_csv, a.kernel, a.copy_bytes)
+        res["source"] = a.source
+        print(json.dumps(res, indent=1))
+        if a.json:
+            with open(a.json, "w") as fh:
+                json.dump(res, fh, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
