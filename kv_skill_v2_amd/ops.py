@@ -40,6 +40,7 @@ class PagedLibrary:
     S: torch.Tensor              # fp32 [Ctot, d]
     n_chunks: list[int] = field(default_factory=list)   # host copy: chunks per library
     nvalid: list[int] = field(default_factory=list)     # host copy: valid slots per chunk
+    _pages_t: torch.Tensor | None = field(default=None, repr=False, compare=False)
 
     def __post_init__(self):
         for name in ("pages", "chunk_page", "chunk_nvalid", "chunk_ptr", "S"):
@@ -125,6 +126,24 @@ class PagedLibrary:
     def kept(self, top_k: int) -> int:
         """Width of the routed-index arrays: max over libraries of the kept chunk count."""
         return max(c if (top_k <= 0 or top_k >= c) else top_k for c in self.n_chunks)
+
+    def check_prefill(self) -> None:
+        """The MFMA prefill kernels tile d and the slots by 32 and a page by <= 512 slots."""
+        if self.d % 32 or self.slots_per_page % 32 or self.slots_per_page > 512:
+            raise ValueError(f"the prefill read needs d % 32 == 0 and slots_per_page % 32 == 0, <= 512 "
+                             f"(got d={self.d}, slots={self.slots_per_page}); build the pool with padding")
+
+    @property
+    def pages_t(self) -> torch.Tensor:
+        """Transposed pages K^T [P, d, slots] (fp16) for the readout GEMM; built once on first use
+        by the transpose kernel and kept with the pool (the library is resident across steps)."""
+        if self._pages_t is None:
+            P, N, d = self.pages.shape
+            t = torch.empty(P, d, N, dtype=torch.float16, device=self.device)
+            check(lib().xenc_transpose_pages(ptr(self.pages), P, N, d, ptr(t), stream_handle(self.device)),
+                  "xenc_transpose_pages")
+            self._pages_t = t
+        return self._pages_t
 
 
 def _groups(lib_: PagedLibrary, M: int, q_group) -> torch.Tensor:
@@ -240,4 +259,187 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
     return r
 
 
-__all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit"]
+# ---------------------------------------------------------------------------------------------
+# Prefill / registration read (MFMA) and the autograd of routing + read
+ROWS_SCORES, ROWS_READOUT, ROWS_ROUTE_BWD = 128, 256, 16
+
+
+def _prefix(counts) -> list[int]:
+    out = [0]
+    for c in counts:
+        out.append(out[-1] + int(c))
+    return out
+
+
+@dataclass
+class RowPlan:
+    """Query rows grouped by library (rows of library g are contiguous) and the per-library tile
+    offsets each prefill kernel walks.  Built on the host once per (pool, rows) shape."""
+
+    rows: list[int]
+    row_ptr: torch.Tensor
+    score_tiles: torch.Tensor
+    n_score: int
+    readout_tiles: torch.Tensor
+    n_readout: int
+    route_tiles: torch.Tensor
+    n_route: int
+
+    @property
+    def M(self) -> int:
+        return sum(self.rows)
+
+
+def row_plan(lib_: PagedLibrary, rows_per_library) -> RowPlan:
+    rows = [int(r) for r in rows_per_library]
+    if len(rows) != lib_.n_libraries or min(rows) < 0:
+        raise ValueError(f"need one non-negative row count per library ({lib_.n_libraries})")
+    dev = lib_.device
+    d_tiles = -(-lib_.d // 256)
+    sc = _prefix(-(-t // ROWS_SCORES) * c for t, c in zip(rows, lib_.n_chunks))
+    ro = _prefix(-(-t // ROWS_READOUT) * d_tiles for t in rows)
+    rb = _prefix(-(-t // ROWS_ROUTE_BWD) for t in rows)
+    return RowPlan(rows, _i32(_prefix(rows), dev), _i32(sc, dev), sc[-1], _i32(ro, dev), ro[-1],
+                   _i32(rb, dev), rb[-1])
+
+
+def cast_f16(x: torch.Tensor) -> torch.Tensor:
+    """fp32 rows -> contiguous fp16 rows (HIP cast kernel)."""
+    _require_device(x, "x")
+    x = x.to(torch.float32)
+    if x.stride(-1) != 1 or x.stride(0) % 4 or x.data_ptr() % 16:
+        x = x.contiguous()
+    M, d = x.shape
+    y = torch.empty(M, d, dtype=torch.float16, device=x.device)
+    check(lib().xenc_cast_rows_f16(ptr(x), x.stride(0), M, d, ptr(y), stream_handle(x.device)),
+          "xenc_cast_rows_f16")
+    return y
+
+
+def _ldp(lib_: PagedLibrary) -> int:
+    n = lib_.cmax * lib_.slots_per_page
+    return (n + 7) // 8 * 8
+
+
+def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
+                    read_temp: float = 12.0):
+    """(r [M, d] fp32, p [M, ldp] fp16): the route-weighted masked-softmax read of many query rows.
+    HIP kernels scores_kernel<0> + readout_kernel (kv_skill_v2_amd/csrc/prefill.hip)."""
+    lib_.check_prefill()
+    q = _query(q, lib_.d)
+    M, d = q.shape
+    if M != plan.M or w.shape != (M, lib_.cmax):
+        raise ValueError(f"q must have {plan.M} rows and w shape ({plan.M}, {lib_.cmax})")
+    w = w.to(torch.float32).contiguous()
+    L, st, N = lib(), stream_handle(q.device), lib_.slots_per_page
+    qh = cast_f16(q)
+    ldp = _ldp(lib_)
+    p = torch.empty(M, ldp, dtype=torch.float16, device=q.device)
+    check(L.xenc_prefill_scores(0, ptr(qh), d, ptr(plan.row_ptr), ptr(plan.score_tiles), lib_.n_libraries,
+                                plan.n_score, ptr(lib_.pages), N, lib_.pages.stride(0), ptr(lib_.chunk_ptr),
+                                ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), float(read_temp), None, 0,
+                                ptr(p), ldp, None, None, 0, st), "xenc_prefill_scores")
+    r = torch.empty(M, d, dtype=torch.float32, device=q.device)
+    pt = lib_.pages_t
+    check(L.xenc_prefill_readout(ptr(p), ldp, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
+                                 plan.n_readout, ptr(pt), N, d, pt.stride(0), ptr(lib_.chunk_ptr),
+                                 ptr(lib_.chunk_page), ptr(w), w.stride(0), ptr(r), r.stride(0), st),
+          "xenc_prefill_readout")
+    return r, p
+
+
+def prefill_backward(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, lib_: PagedLibrary,
+                     plan: RowPlan, read_temp: float = 12.0):
+    """(dq through the read [M, d] fp32, gamma = dL/dw through the read [M, cmax] fp32) given the
+    upstream gradient g = dL/dr.  HIP kernels scores_kernel<1> + readout_kernel."""
+    g = _query(g, lib_.d)
+    M, d = g.shape
+    w = w.to(torch.float32).contiguous()
+    L, st, N = lib(), stream_handle(g.device), lib_.slots_per_page
+    gh = cast_f16(g)
+    ldp = p.stride(0)
+    ds = torch.empty_like(p)
+    gamma = torch.zeros(M, lib_.cmax, dtype=torch.float32, device=g.device)
+    check(L.xenc_prefill_scores(1, ptr(gh), d, ptr(plan.row_ptr), ptr(plan.score_tiles), lib_.n_libraries,
+                                plan.n_score, ptr(lib_.pages), N, lib_.pages.stride(0), ptr(lib_.chunk_ptr),
+                                ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), float(read_temp), ptr(w),
+                                w.stride(0), ptr(p), ldp, ptr(ds), ptr(gamma), gamma.stride(0), st),
+          "xenc_prefill_scores")
+    dq = torch.empty(M, d, dtype=torch.float32, device=g.device)
+    pt = lib_.pages_t
+    check(L.xenc_prefill_readout(ptr(ds), ldp, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
+                                 plan.n_readout, ptr(pt), N, d, pt.stride(0), ptr(lib_.chunk_ptr),
+                                 ptr(lib_.chunk_page), None, 0, ptr(dq), dq.stride(0), st),
+          "xenc_prefill_readout")
+    return dq, gamma
+
+
+def route_backward(w: torch.Tensor, dw: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
+                   route_temp: float, dq: torch.Tensor, dw_ext: torch.Tensor | None = None) -> torch.Tensor:
+    """dq += route_temp * sum_c w (dw - sum w dw) S_c, in place (HIP route_backward_kernel)."""
+    w = w.to(torch.float32).contiguous()
+    dw = dw.to(torch.float32).contiguous()
+    if dw_ext is not None:
+        dw_ext = dw_ext.to(torch.float32).contiguous()
+    check(lib().xenc_route_backward(ptr(w), w.stride(0), ptr(dw), dw.stride(0), ptr(dw_ext),
+                                    dw_ext.stride(0) if dw_ext is not None else 0, ptr(plan.row_ptr),
+                                    ptr(plan.route_tiles), lib_.n_libraries, plan.n_route, lib_.cmax,
+                                    ptr(lib_.S), ptr(lib_.chunk_ptr), lib_.d, float(route_temp), ptr(dq),
+                                    dq.stride(0), stream_handle(dq.device)), "xenc_route_backward")
+    return dq
+
+
+def _plan_groups(plan: RowPlan) -> torch.Tensor:
+    g = torch.repeat_interleave(torch.arange(len(plan.rows)), torch.tensor(plan.rows))
+    return g.to(torch.int32)
+
+
+class RouteFn(torch.autograd.Function):
+    """w [M, cmax] = route(q); differentiable in q through the softmax over the kept logits."""
+
+    @staticmethod
+    def forward(ctx, q, lib_, plan, top_k, route_temp):
+        qg = _plan_groups(plan).to(q.device)
+        w, idx, wsel = route_topk(q.detach(), lib_, qg, top_k=top_k, route_temp=route_temp)
+        ctx.save_for_backward(w)
+        ctx.lib, ctx.plan, ctx.route_temp = lib_, plan, route_temp
+        ctx.mark_non_differentiable(idx, wsel)
+        return w, idx, wsel
+
+    @staticmethod
+    def backward(ctx, dw, _didx, _dwsel):
+        (w,) = ctx.saved_tensors
+        dq = torch.zeros(w.shape[0], ctx.lib.d, dtype=torch.float32, device=w.device)
+        if dw is not None:
+            route_backward(w, dw, ctx.lib, ctx.plan, ctx.route_temp, dq)
+        return dq, None, None, None, None
+
+
+class ReadFn(torch.autograd.Function):
+    """r [M, d] = route-weighted masked-softmax read; differentiable in q and w."""
+
+    @staticmethod
+    def forward(ctx, q, w, lib_, plan, read_temp):
+        r, p = prefill_forward(q.detach(), w.detach(), lib_, plan, read_temp)
+        ctx.save_for_backward(w, p)
+        ctx.lib, ctx.plan, ctx.read_temp = lib_, plan, read_temp
+        return r
+
+    @staticmethod
+    def backward(ctx, dr):
+        w, p = ctx.saved_tensors
+        dq, gamma = prefill_backward(dr, w, p, ctx.lib, ctx.plan, ctx.read_temp)
+        return dq, gamma, None, None, None
+
+
+def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int = 0,
+                 read_temp: float = 12.0, route_temp: float = 10.0):
+    """(r [M, d], w [M, cmax]) with autograd through both routing and the read (MFMA path)."""
+    w, _, _ = RouteFn.apply(q, lib_, plan, int(top_k), float(route_temp))
+    r = ReadFn.apply(q, w, lib_, plan, float(read_temp))
+    return r, w
+
+
+__all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
+           "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "RouteFn", "ReadFn",
+           "library_read"]

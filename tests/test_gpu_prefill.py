@@ -1,0 +1,107 @@
+"""GPU parity of the MFMA prefill read (forward and autograd backward) against the CPU oracle.
+
+The kernels take fp16 operands (q, the probabilities p, dS, the upstream gradient) with fp32
+accumulation, so the bar is the task's fp16 tolerance: max-abs 2e-3 and relative 1e-2 on r; for
+gradients (whose scale is set by the upstream gradient) the same relative bar on the norm and on
+the largest entry."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle as O
+from kv_skill_v2_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _lib(P, dev):
+    return ops.PagedLibrary(P.pages.to(dev), P.chunk_page.to(dev), P.chunk_nvalid.to(dev), P.chunk_ptr.to(dev),
+                            P.S.to(dev), n_chunks=P.n_chunks, nvalid=P.nvalid)
+
+
+def _rel(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item(), ((a - b).abs().max() / b.abs().max()).item()
+
+
+CASES = [
+    # (d, N, chunks per library, rows per library, top_k)
+    (256, 512, [4], [64], 2),
+    (128, 64, [5, 3], [300, 17], 0),
+    (256, 96, [7], [130], 3),
+    (2048, 512, [6], [256], 0),
+    (512, 128, [9, 2, 4], [40, 200, 129], 4),
+]
+
+
+@pytest.mark.parametrize("d,N,counts,rows,top_k", CASES)
+def test_prefill_forward_parity(dev, d, N, counts, rows, top_k):
+    say("prefill fwd", dict(d=d, N=N, counts=counts, rows=rows, top_k=top_k))
+    P = synth.pool(counts, N, d, device="cpu", tail_lo=1)
+    lib = _lib(P, dev)
+    plan = ops.row_plan(lib, rows)
+    q = synth.queries(sum(rows), d, device="cpu", seed=13)
+    with torch.no_grad():
+        r, w = ops.library_read(q.to(dev), lib, plan, top_k=top_k)
+        wg, _, _ = ops.route_topk(q.to(dev), lib, ops._plan_groups(plan).to(dev), top_k=top_k)
+        _, p = ops.prefill_forward(q.to(dev), wg, lib, plan)
+    torch.cuda.synchronize()
+    r, p = r.cpu().double(), p.cpu().float()
+    off = 0
+    for g, T in enumerate(rows):
+        K, M, S = P.library(g)
+        qg = q[off:off + T].double().view(1, T, d)
+        ref, _ = O.branch_read(qg, K.double(), M, S.double(), top_k=top_k)
+        err = (r[off:off + T] - ref[0]).abs().max().item()
+        rel = ((r[off:off + T] - ref[0]).norm() / ref.norm()).item()
+        assert err <= 2e-3 and rel <= 1e-2, (g, err, rel)
+        a = torch.einsum("td,cnd->tcn", qg[0], K.double())
+        pref = torch.softmax((a * 12.0).masked_fill(~M, float("-inf")), -1)
+        C = K.shape[0]
+        pk = p[off:off + T, :C * N].view(T, C, N).double()
+        assert (pk - pref).abs().max().item() <= 1e-3, g
+        off += T
+
+
+@pytest.mark.parametrize("d,N,counts,rows,top_k", CASES)
+def test_prefill_backward_parity(dev, d, N, counts, rows, top_k):
+    say("prefill bwd", dict(d=d, N=N, counts=counts, rows=rows, top_k=top_k))
+    P = synth.pool(counts, N, d, device="cpu", tail_lo=1)
+    lib = _lib(P, dev)
+    plan = ops.row_plan(lib, rows)
+    M_ = sum(rows)
+    q = synth.queries(M_, d, device="cpu", seed=17)
+    gen = torch.Generator().manual_seed(7)
+    g_up = torch.randn(M_, d, generator=gen)
+    dw_ext = torch.randn(M_, lib.cmax, generator=gen)
+    qd = q.to(dev).requires_grad_(True)
+    r, w = ops.library_read(qd, lib, plan, top_k=top_k)
+    loss = (r * g_up.to(dev)).sum() + (w * dw_ext.to(dev)).sum()
+    loss.backward()
+    torch.cuda.synchronize()
+    dq = qd.grad.cpu()
+    off = 0
+    for g, T in enumerate(rows):
+        K, M, S = P.library(g)
+        C = K.shape[0]
+        ref, _ = O.read_dq(q[off:off + T].double().view(1, T, d), K.double(), M, S.double(),
+                           g_up[off:off + T].double().view(1, T, d), 12.0, 10.0, top_k,
+                           dw_ext=dw_ext[off:off + T, :C].double().view(1, T, C))
+        rn, rm = _rel(dq[off:off + T], ref[0])
+        assert rn <= 1e-2 and rm <= 1e-2, (g, rn, rm)
+        off += T
+
+
+def test_prefill_requires_tileable_shapes(dev):
+    say("prefill shape guard")
+    P = synth.pool([3], 40, 64, device="cpu")
+    lib = _lib(P, dev)
+    plan = ops.row_plan(lib, [5])
+    with pytest.raises(ValueError):
+        ops.prefill_forward(torch.zeros(5, 64, device=dev), torch.zeros(5, 3, device=dev), lib, plan)
