@@ -31,7 +31,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="batched_paged_decode",
-                    choices=["batched_paged_decode", "single_decode"])
+                    choices=["batched_paged_decode", "single_decode", "prefill"])
     ap.add_argument("--nsplit", type=int, default=None)
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -95,6 +95,102 @@ def cpu_baseline(P, q, top_k, n_seq, reps):
                        f"CPU oracle on {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
 
 
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(args):
+    """Prefill/registration read: 4 documents x 2048 query rows, each document a Library of 32 x 512
+    slots (ragged tail), d_s = 2048, dense routing (every chunk read), fp16 MFMA with fp32
+    accumulation; forward (route + read) and the dQ backward (read + route) against a seeded
+    upstream gradient ~N(0,1).  Algorithmic FLOPs per document and direction: 4 * T * sum(n_valid) * d
+    (two GEMMs of 2 FLOPs per multiply-add; recomputation is not counted)."""
+    from kv_skill_v2_amd import ops, synth
+
+    dev = torch.device("cuda:0")
+    G, T, C, N, d = 4, 2048, 32, 512, 2048
+    P = synth.pool([C] * G, N, d, device=dev)
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    plan = ops.row_plan(lib, [T] * G)
+    q = synth.queries(G * T, d, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    g_up = torch.randn(G * T, d, generator=gen, device=dev)
+    qg = ops._plan_groups(plan).to(dev)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    lib.fragment_pages(0), lib.fragment_pages(1)  # one-time fragment-ordered copies of the pages
+    torch.cuda.synchronize()
+    frag_ms = (time.perf_counter() - t0) * 1e3
+
+    def fwd():
+        w, _, _ = ops.route_topk(q, lib, qg, top_k=0)
+        r, p = ops.prefill_forward(q, w, lib, plan)
+        return w, r, p
+
+    def bwd(w, p):
+        dq, gamma = ops.prefill_backward(g_up, w, p, lib, plan)
+        ops.route_backward(w, gamma, lib, plan, 10.0, dq)
+        return dq
+
+    for _ in range(args.warmup):
+        w, r, p = fwd()
+        bwd(w, p)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        w, r, p = fwd()
+        evs[i][1].record(stream)
+        bwd(w, p)
+        evs[i][2].record(stream)
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    fwd_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
+    bwd_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
+    nvalid = sum(P.nvalid)
+    flops = 4.0 * T * nvalid * d                  # per direction, all documents
+    fwd_tf = flops / (fwd_ms * 1e-3) / 1e12
+    bwd_tf = flops / (bwd_ms * 1e-3) / 1e12
+
+    cpu = None
+    if args.cpu_sample > 0:
+        import oracle as O
+        torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+        K, M, S = P.library(0)
+        K, M, S = K.cpu(), M.cpu(), S.cpu()
+        qc = q[:T].cpu().view(1, T, d).requires_grad_(True)
+        gc = g_up[:T].cpu().view(1, T, d)
+        t0 = time.perf_counter()
+        rr, _ = O.branch_read(qc, K, M, S, top_k=0)
+        (rr * gc).sum().backward()
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": 2 * 4.0 * T * sum(P.nvalid[:C]) * d / cpu_s / 1e12, "unit": "TFLOP/s (fwd+bwd)",
+               "cores": torch.get_num_threads(), "kind": "port",
+               "sample": (f"1 of {G} documents ({T} rows x {C} chunks), fp32 route+read forward and torch "
+                          f"autograd backward in the reference's operation order, 1 rep ({cpu_s:.2f} s); "
+                          f"CPU oracle on {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
+    out = {
+        "metric": "Prefill/registration read TFLOP/s (fwd and dQ bwd), 4 docs x 2048 rows x 32x512 slots",
+        "value": 2 * flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s (fwd+bwd)", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "prefill", "documents": G, "rows_per_document": T, "chunks": C,
+                   "slots_per_page": N, "d_s": d, "routing": "dense (top_k=0)", "accumulate": "fp32",
+                   "fragment_pages_ms_once": frag_ms},
+        "fwd": {"ms": fwd_ms, "tflops": fwd_tf, "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS},
+        "bwd": {"ms": bwd_ms, "tflops": bwd_tf, "frac": bwd_tf / MFMA_FP16_PEAK_TFLOPS},
+        "roofline": {"bound": "mfma", "kernel": "scores_kernel + readout_kernel (fwd)",
+                     "achieved": fwd_tf, "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS, "traffic": None,
+                     "algorithmic_flops": flops},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -104,6 +200,8 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "prefill":
+        return bench_prefill(args)
     from kv_skill_v2_amd import ops, synth
 
     dev = torch.device("cuda:0")

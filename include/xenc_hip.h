@@ -91,34 +91,39 @@ int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
  * ---- Prefill / registration read (many query rows per library; MFMA, fp16 in, fp32 accumulate)
  * Query rows are grouped by library: rows of library g are row_ptr[g] .. row_ptr[g+1]-1.
  * Tiles: the scores kernel takes tile_ptr[g] = sum_{g'<g} ceil(T_g'/128) * C_g' (G+1 entries,
- * n_tiles = tile_ptr[G]); the readout kernel takes tile_ptr[g] = sum ceil(T_g'/256) * ceil(d/256);
- * the route backward takes tile_ptr[g] = sum ceil(T_g'/16).  Requirements: d % 32 == 0,
- * slots_per_page % 32 == 0 and <= 512.  The probability rows p / dS are fp16 [M, ldp] with chunk c
- * of a row's library at columns c*slots_per_page .. +slots_per_page-1 (ldp >= max C * slots).
+ * n_tiles = tile_ptr[G]); the readout kernel takes tile_ptr[g] = sum ceil(T_g'/128) * ceil(d/256);
+ * the route backward takes tile_ptr[g] = sum ceil(T_g'/16).  Requirements: d % 64 == 0,
+ * slots_per_page % 64 == 0 and <= 512.  The probability rows p / dS are fp16 and octet-major:
+ * element (row t, chunk c of the row's library, slot n) sits at ((c*slots/8 + n/8)*p_rows + t)*8 + n%8
+ * (p_rows >= M; the buffer holds max_C * slots * p_rows halves).
+ * The kernels read the pages through two fragment-ordered copies built once per pool by
+ * xenc_fragment_pages: layout 0 (scores) is [P][slots/32][d/16][64][8] with lane l of block
+ * (sg, kb) = K[32sg + l%32][16kb + 8(l/32) + e]; layout 1 (readout) is [P][d/32][slots/16][64][8]
+ * with lane l of block (db, nb) = K[16nb + 8(l/32) + e][32db + l%32].  page_stride is the stride
+ * of one page in the copy (>= slots*d).
  *
  * xenc_prefill_scores(mode=0): p = masked softmax_n(temp * <x_t, K[c,n]>) per (row, chunk).
  * xenc_prefill_scores(mode=1): x = upstream gradient g; u = <g_t, K[c,n]>;
  *     gamma[t,c] = sum_n p u  (= dL/dw[t,c] through the read) and
  *     ds[t, c, n] = temp * w[t,c] * p * (u - gamma[t,c]).
  * xenc_prefill_readout: out[t] = sum_c scale(t,c) sum_n a[t, c, n] K[c, n], scale = w[t,c] when w
- *     is given (forward read) else 1 (backward: out = dq through the read); reads the transposed
- *     pages K^T [P, d, slots] (xenc_transpose_pages, built once per library).
+ *     is given (forward read) else 1 (backward: out = dq through the read).
  * xenc_route_backward: dq[t] += route_temp * sum_c w (dw - sum_c' w dw) S[c],
  *     dw = dw_read (+ dw_ext when not NULL): the gradient through routing.
  * Replace the forward and the autograd backward of LibraryInjector.route + _branch
  * (xenc/injector.py:220-265) for registration (scripts/register_doc.py:699).
  */
 int xenc_cast_rows_f16(const float* x, long long ldx, int M, int d, void* y, void* stream);
-int xenc_transpose_pages(const void* pages, int P, int slots_per_page, int d, void* pages_t,
-                         void* stream);
+int xenc_fragment_pages(const void* pages, long long P, int slots_per_page, int d, int layout,
+                        void* out, void* stream);
 int xenc_prefill_scores(int mode, const void* x, int d, const int* row_ptr, const int* tile_ptr,
-                        int G, int n_tiles, const void* pages, int slots_per_page,
+                        int G, int n_tiles, const void* pages_a, int slots_per_page,
                         long long page_stride, const int* chunk_ptr, const int* chunk_page,
                         const int* chunk_nvalid, float temp, const float* w, long long ldw,
-                        void* p, long long ldp, void* ds, float* gamma, long long ldg,
+                        void* p, long long p_rows, void* ds, float* gamma, long long ldg,
                         void* stream);
-int xenc_prefill_readout(const void* a, long long lda, const int* row_ptr, const int* tile_ptr,
-                         int G, int n_tiles, const void* pages_t, int slots_per_page, int d,
+int xenc_prefill_readout(const void* a, long long a_rows, const int* row_ptr, const int* tile_ptr,
+                         int G, int n_tiles, const void* pages_b, int slots_per_page, int d,
                          long long page_stride, const int* chunk_ptr, const int* chunk_page,
                          const float* w, long long ldw, float* out, long long ldo, void* stream);
 int xenc_route_backward(const float* w, long long ldw, const float* dw_read, long long ldr,

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib = None
@@ -42,16 +42,16 @@ SIGNATURES = {
         c_void_p, c_longlong,                        # r, ldr
         c_void_p, c_size_t, c_void_p]),              # workspace, bytes, stream
     "xenc_cast_rows_f16": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p]),
-    "xenc_transpose_pages": (c_int, [c_void_p, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "xenc_fragment_pages": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p]),
     "xenc_prefill_scores": (c_int, [
         c_int, c_void_p, c_int, c_void_p, c_void_p,  # mode, x, d, row_ptr, tile_ptr
-        c_int, c_int, c_void_p, c_int, c_longlong,   # G, n_tiles, pages, slots_per_page, page_stride
+        c_int, c_int, c_void_p, c_int, c_longlong,   # G, n_tiles, pages_a, slots_per_page, page_stride
         c_void_p, c_void_p, c_void_p, c_float,       # chunk_ptr, chunk_page, chunk_nvalid, temp
-        c_void_p, c_longlong, c_void_p, c_longlong,  # w, ldw, p, ldp
+        c_void_p, c_longlong, c_void_p, c_longlong,  # w, ldw, p, p_rows
         c_void_p, c_void_p, c_longlong, c_void_p]),  # ds, gamma, ldg, stream
     "xenc_prefill_readout": (c_int, [
-        c_void_p, c_longlong, c_void_p, c_void_p,    # a, lda, row_ptr, tile_ptr
-        c_int, c_int, c_void_p, c_int, c_int,        # G, n_tiles, pages_t, slots_per_page, d
+        c_void_p, c_longlong, c_void_p, c_void_p,    # a, a_rows, row_ptr, tile_ptr
+        c_int, c_int, c_void_p, c_int, c_int,        # G, n_tiles, pages_b, slots_per_page, d
         c_longlong, c_void_p, c_void_p,              # page_stride, chunk_ptr, chunk_page
         c_void_p, c_longlong, c_void_p, c_longlong, c_void_p]),  # w, ldw, out, ldo, stream
     "xenc_route_backward": (c_int, [

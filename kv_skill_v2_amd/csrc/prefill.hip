@@ -4,7 +4,7 @@
 //
 //   forward   S^T[n, t] = K_c[n] . q_t                 (scores kernel, MFMA, one chunk per tile)
 //             p[t, c, n] = softmax_n(read_temp * S)     (epilogue: masked per-chunk softmax)
-//             r[t]       = sum_c w[t,c] sum_n p K_c[n]  (readout kernel, MFMA over K^T pages)
+//             r[t]       = sum_c w[t,c] sum_n p K_c[n]  (readout kernel, MFMA)
 //   backward  U^T[n, t] = K_c[n] . g_t                 (scores kernel, MFMA)
 //             gamma[t,c] = sum_n p U ;  dS = read_temp * w p (U - gamma)   (epilogue)
 //             dq_read[t] = sum_{c,n} dS K_c[n]         (readout kernel)
@@ -12,11 +12,20 @@
 // This is the math of LibraryInjector._branch (xenc/injector.py:236-265) and of its autograd
 // (scripts/register_doc.py:699), with K = V tied.
 //
+// Layouts.  The library is resident across many calls, so each page is also kept in two
+// fragment-ordered copies built once (xenc_fragment_pages): in these, the 64 lanes' MFMA
+// fragments of one (32-row, 16-column) block are one contiguous 1 KiB, so every fragment load of
+// the operand that a wave owns alone is a single coalesced read.
+//   layout A [P][N/32][d/16][64][8]: lane l of block (sg, kb) = K[32sg + l%32][16kb + 8(l/32) + e]
+//   layout B [P][d/32][N/16][64][8]: lane l of block (db, nb) = K[16nb + 8(l/32) + e][32db + l%32]
+// The probabilities p and the backward dS are stored octet-major, [C*N/8][M][8] (8 slots of a
+// row in 16 bytes, rows fastest), so the scores epilogue writes 512 contiguous bytes per
+// instruction and the readout stages them with contiguous row loads.
+//
 // The scores tile covers a whole chunk (512 slots) x 128 query rows, so the chunk softmax is
-// local to the workgroup; Sᵀ is formed (slots as the MFMA M dimension) so that each lane holds 32
+// local to the workgroup; S^T is formed (slots as the MFMA M dimension) so that each lane holds 32
 // slot scores of 4 query rows: the softmax over slots is an in-lane reduction plus one xor-32
-// shuffle plus an 8-wave LDS exchange.  The readout is a plain NT GEMM over the transposed pages
-// K^T [d, N] (a one-time copy), so both GEMMs read k-contiguous operands.
+// shuffle plus an 8-wave LDS exchange.
 #include <algorithm>
 
 #include "xenc_common.h"
@@ -25,18 +34,35 @@ namespace xenc {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int BK = 32;              // k (d or slot) columns per main-loop step: two MFMA k16 steps
-constexpr int LROW = BK + 8;        // LDS row stride in halves (80 B): conflict-free b128 reads
+constexpr int BK = 64;              // k (d or slot) columns per main-loop step: four MFMA k16 steps
 constexpr int kRowsPerTile = 128;   // query rows per scores tile
 constexpr int kSlotsPerTile = 512;  // slots per scores tile (a whole page)
+constexpr int kReadoutRows = 128;   // query rows per readout tile
+
+// LDS tiles hold rows of BK = 64 halves (128 B = 8 chunks of 16 B).  Chunk c of row r sits at
+// position c ^ ((r ^ (r >> 3)) & 7): the 8 (or 16) rows that one ds_read_b128 fragment load
+// serves per cycle then fall on disjoint banks, for 32 and for 64 banks alike.
+__device__ __forceinline__ int swz(int r, int c) { return r * BK + ((c ^ ((r ^ (r >> 3)) & 7)) << 3); }
 
 __device__ __forceinline__ f32x16 mfma32(const half8_t& a, const half8_t& b, const f32x16& c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Tile b is
+// remapped so that XCD x runs a contiguous range of logical tiles; the logical order then puts
+// tiles that share operands next to each other, so the workgroups resident on one XCD at a time
+// hit in that XCD's L2 instead of re-reading HBM.  A bijection on [0, n).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  const int x = b % kXcds, j = b / kXcds;
+  const int per = (n + kXcds - 1) / kXcds, rem = n % kXcds;
+  const int start = rem == 0 ? x * per : x * per - max(0, x - rem);
+  return start + j;
+}
+constexpr int kChunkGroup = 4;  // scores tiles: chunks per group, all row tiles of a group adjacent
 
 // Library g of tile b: tile_ptr[g] <= b < tile_ptr[g+1] (binary search; G is small).
 __device__ __forceinline__ int find_group(const int* __restrict__ tile_ptr, int G, int b) {
@@ -62,55 +88,73 @@ __global__ void cast_rows_f16_kernel(const float* __restrict__ x, long long ldx,
   }
 }
 
-// pages [P, N, d] -> pagesT [P, d, N] through 32x32 LDS tiles.
-__global__ __launch_bounds__(256) void transpose_pages_kernel(const _Float16* __restrict__ pages,
-                                                              int N, int d,
-                                                              _Float16* __restrict__ pagesT) {
-  __shared__ _Float16 tile[32][33];
-  const long long base = (long long)blockIdx.z * N * d;
-  const int d0 = blockIdx.x * 32, n0 = blockIdx.y * 32;
-  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;  // 32 x 8
-  for (int i = ty; i < 32; i += 8) {
-    const int n = n0 + i, dd = d0 + tx;
-    tile[i][tx] = (n < N && dd < d) ? pages[base + (long long)n * d + dd] : (_Float16)0;
-  }
-  __syncthreads();
-  for (int i = ty; i < 32; i += 8) {
-    const int dd = d0 + i, n = n0 + tx;
-    if (dd < d && n < N) pagesT[base + (long long)dd * N + n] = tile[tx][i];
+// pages [P, N, d] -> a fragment-ordered copy (layout A or B above); one thread per lane-chunk.
+template <int LAYOUT>
+__global__ __launch_bounds__(256) void fragment_pages_kernel(const _Float16* __restrict__ pages,
+                                                             long long P, int N, int d,
+                                                             _Float16* __restrict__ out) {
+  const long long total = P * (long long)N * d / 8;
+  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < total;
+       i += (long long)gridDim.x * blockDim.x) {
+    const int lane = (int)(i & 63);
+    const long long blk = i >> 6;
+    half8_t v;
+    if (LAYOUT == 0) {  // [P][N/32][d/16][64][8]
+      const int nkb = d / 16, nsg = N / 32;
+      const int kb = (int)(blk % nkb), sg = (int)((blk / nkb) % nsg);
+      const long long p = blk / ((long long)nkb * nsg);
+      const _Float16* src = pages + (p * N + 32 * sg + (lane & 31)) * d + 16 * kb + 8 * (lane >> 5);
+      v = *reinterpret_cast<const half8_t*>(src);
+    } else {            // [P][d/32][N/16][64][8]
+      const int nnb = N / 16, ndb = d / 32;
+      const int nb = (int)(blk % nnb), db = (int)((blk / nnb) % ndb);
+      const long long p = blk / ((long long)nnb * ndb);
+      const _Float16* src = pages + (p * N + 16 * nb + 8 * (lane >> 5)) * d + 32 * db + (lane & 31);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = src[(long long)e * d];
+    }
+    *reinterpret_cast<half8_t*>(out + i * 8) = v;
   }
 }
 
 // ------------------------------------------------------------------------------------------
 // Scores kernel: one workgroup = (library g, 128-row tile, chunk c), 8 waves; wave w owns slots
-// [64w, 64w+64) (two 32-row MFMA tiles) x all 128 rows (four 32-column tiles).
-// MODE 0 (forward): writes p = masked softmax over the chunk's slots (fp16) into P[t, c*N + n].
-// MODE 1 (backward): reads p, writes dS = read_temp * w[t,c] * p * (U - gamma) into dS[t, c*N+n]
+// [64w, 64w+64) (two 32-row MFMA tiles) x all 128 rows (four 32-column tiles).  The slot rows of
+// a wave are private to it: their fragments come straight from the layout-A page copy (one
+// coalesced 1 KiB load each), refilled for the next k-step as soon as they are consumed; the 128
+// query rows are shared by all waves and staged through LDS (two swizzled stages, one barrier
+// per k-step).
+// MODE 0 (forward): writes p = masked softmax over the chunk's slots (fp16, octet-major).
+// MODE 1 (backward): reads p, writes dS = read_temp * w[t,c] * p * (U - gamma) (octet-major)
 //                    and gamma[t, c] = sum_n p U.
 template <int MODE>
 __global__ __launch_bounds__(512) void scores_kernel(
     const _Float16* __restrict__ X, int d, const int* __restrict__ row_ptr,
-    const int* __restrict__ tile_ptr, int G, const _Float16* __restrict__ pages, int N,
+    const int* __restrict__ tile_ptr, int G, const _Float16* __restrict__ pages_a, int N,
     long long page_stride, const int* __restrict__ chunk_ptr, const int* __restrict__ chunk_page,
     const int* __restrict__ chunk_nvalid, float temp, const float* __restrict__ w, long long ldw,
-    _Float16* __restrict__ P, long long ldp, _Float16* __restrict__ dS,
+    _Float16* __restrict__ P, long long p_rows, _Float16* __restrict__ dS,
     float* __restrict__ gamma, long long ldg) {
-  __shared__ _Float16 lA[kSlotsPerTile * LROW];  // K_c tile [512][BK] (+pad)
-  __shared__ _Float16 lB[kRowsPerTile * LROW];   // X tile [128][BK] (+pad)
+  __shared__ _Float16 lB[2][kRowsPerTile * BK];  // X tile [128][64], two stages (32 KiB)
   __shared__ float red[8][kRowsPerTile];          // per-wave row statistics
 
-  const int b = blockIdx.x;
+  const int b = xcd_remap(blockIdx.x, gridDim.x);
   const int g = find_group(tile_ptr, G, b);
   const int cbeg = chunk_ptr[g];
   const int C = chunk_ptr[g + 1] - cbeg;
-  const int local = b - tile_ptr[g];
-  const int c = local % C;
-  const int rt = local / C;
   const int rbeg = row_ptr[g], rend = row_ptr[g + 1];
+  // Logical order inside a library: groups of kChunkGroup chunks; within a group, row tile major.
+  const int RTn = (rend - rbeg + kRowsPerTile - 1) / kRowsPerTile;
+  const int local = b - tile_ptr[g];
+  const int cg = local / (RTn * kChunkGroup);
+  const int gsz = min(kChunkGroup, C - cg * kChunkGroup);
+  const int off = local - cg * RTn * kChunkGroup;
+  const int rt = off / gsz;
+  const int c = cg * kChunkGroup + off % gsz;
   const int row0 = rbeg + rt * kRowsPerTile;
   const int gc = cbeg + c;
   const int nv = min(chunk_nvalid[gc], N);
-  const _Float16* K = pages + (long long)chunk_page[gc] * page_stride;
+  const _Float16* Ka = pages_a + (long long)chunk_page[gc] * page_stride;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -118,25 +162,31 @@ __global__ __launch_bounds__(512) void scores_kernel(
   const int hl = lane >> 5;   // lane half: k-group of the fragments, +4 row offset of D
   const int l32 = lane & 31;
 
-  // Global -> LDS staging: A is 512 rows x 4 16-byte chunks (4 per thread), B is 128 x 4 (1 each).
-  u32x4 ra[4], rb;
-  auto gload = [&](int k0) {
+  // A fragments of this wave's two slot groups (groups past N/32 re-read the last one; those
+  // slots are masked in the epilogue).  Block (sg, kb) starts at ((sg * d/16 + kb) * 64) * 8.
+  const _Float16* abase[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ch = tid + 512 * i;
-      const int row = min(ch >> 2, N - 1);  // rows past N are masked below
-      ra[i] = *reinterpret_cast<const u32x4*>(K + (long long)row * d + k0 + (ch & 3) * 8);
-    }
-    const int xr = min(row0 + (tid >> 2), rend - 1);  // rows past the library are not stored
-    rb = *reinterpret_cast<const u32x4*>(X + (long long)xr * d + k0 + (tid & 3) * 8);
+  for (int mt = 0; mt < 2; ++mt)
+    abase[mt] = Ka + (long long)min(wv * 2 + mt, N / 32 - 1) * (d / 16) * 512 + lane * 8;
+  // B staging: 128 rows x 8 chunks, 2 per thread (rows past the library are not stored).
+  int brow[2], bch[2];
+  const _Float16* xrow[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int id = tid + 512 * i;
+    brow[i] = id >> 3;
+    bch[i] = id & 7;
+    xrow[i] = X + (long long)min(row0 + brow[i], rend - 1) * d + bch[i] * 8;
+  }
+  half8_t fa[2][4];  // [mt][k16 step]: refilled for the next k-step as soon as it is consumed
+  u32x4 rb[2];
+  auto load_b = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) rb[i] = *reinterpret_cast<const u32x4*>(xrow[i] + k0);
   };
-  auto lstore = [&]() {
+  auto store_b = [&](int st) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ch = tid + 512 * i;
-      *reinterpret_cast<u32x4*>(lA + (ch >> 2) * LROW + (ch & 3) * 8) = ra[i];
-    }
-    *reinterpret_cast<u32x4*>(lB + (tid >> 2) * LROW + (tid & 3) * 8) = rb;
+    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&lB[st][swz(brow[i], bch[i])]) = rb[i];
   };
 
   f32x16 acc[2][4];
@@ -144,31 +194,51 @@ __global__ __launch_bounds__(512) void scores_kernel(
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = (f32x16){};
-
-  gload(0);
-  for (int k0 = 0; k0 < d; k0 += BK) {
-    __syncthreads();  // previous tile fully consumed
-    lstore();
-    __syncthreads();
-    if (k0 + BK < d) gload(k0 + BK);  // next tile in flight during the MFMAs
+  // One k-step on LDS stage st.  The scheduling barriers keep every global load where it is
+  // written: the compiler otherwise sinks them next to their first use and each k-step waits
+  // out a full memory latency.
+  auto compute = [&](int st, int knext) {
 #pragma unroll
-    for (int ks = 0; ks < BK; ks += 16) {
-      half8_t fa[2], fb[4];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-        fa[mt] = *reinterpret_cast<const half8_t*>(lA + (wv * 64 + mt * 32 + l32) * LROW + ks + hl * 8);
+    for (int ks = 0; ks < 4; ++ks) {
+      half8_t fb[4];
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
-        fb[nt] = *reinterpret_cast<const half8_t*>(lB + (nt * 32 + l32) * LROW + ks + hl * 8);
+        fb[nt] = *reinterpret_cast<const half8_t*>(&lB[st][swz(nt * 32 + l32, ks * 2 + hl)]);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = mfma32(fa[mt], fb[nt], acc[mt][nt]);
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = mfma32(fa[mt][ks], fb[nt], acc[mt][nt]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+        fa[mt][ks] = *reinterpret_cast<const half8_t*>(abase[mt] + (knext / 16 + ks) * 512);
+      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+
+  // The prefetch past the last k-step re-reads it (no branch around a load).
+  const int nk = d / BK;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) fa[mt][ks] = *reinterpret_cast<const half8_t*>(abase[mt] + ks * 512);
+  load_b(0);
+  store_b(0);
+  __syncthreads();
+  for (int k = 0; k < nk; ++k) {
+    const int k1 = min(k + 1, nk - 1) * BK;
+    load_b(k1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(k & 1, k1);
+    store_b((k + 1) & 1);  // that stage was last read before the previous barrier
+    __syncthreads();
   }
 
   // acc[mt][nt][r] = S^T[slot][row]: slot = 64w + 32mt + 8(r/4) + 4hl + r%4, row = 32nt + l32.
   auto slot_of = [&](int mt, int r) { return wv * 64 + mt * 32 + (r >> 2) * 8 + hl * 4 + (r & 3); };
+  // Octet-major element (row t, slot s of chunk c): ((c*N/8 + s/8) * p_rows + t) * 8 + s%8.
+  auto poff = [&](int t, int s0) {
+    return ((long long)(c * (N / 8) + (s0 >> 3)) * p_rows + t) * 8 + (s0 & 7);
+  };
 
   if (MODE == 0) {
     // ---- masked softmax over the chunk's slots, per query row
@@ -227,7 +297,6 @@ __global__ __launch_bounds__(512) void scores_kernel(
     for (int nt = 0; nt < 4; ++nt) {
       const int t = row0 + nt * 32 + l32;
       if (t >= rend) continue;
-      _Float16* prow = P + (long long)t * ldp + (long long)c * N;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -238,7 +307,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
                          (_Float16)(acc[mt][nt][q4 * 4 + 1] * rsum[nt]),
                          (_Float16)(acc[mt][nt][q4 * 4 + 2] * rsum[nt]),
                          (_Float16)(acc[mt][nt][q4 * 4 + 3] * rsum[nt])};
-            *reinterpret_cast<half4_t*>(prow + s0) = h;
+            *reinterpret_cast<half4_t*>(P + poff(t, s0)) = h;
           }
         }
     }
@@ -249,14 +318,13 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {
       const int t = min(row0 + nt * 32 + l32, rend - 1);
-      const _Float16* prow = P + (long long)t * ldp + (long long)c * N;
       float s = 0.f;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const int s0 = slot_of(mt, q4 * 4);
-          pv[mt][nt][q4] = s0 < N ? *reinterpret_cast<const half4_t*>(prow + s0) : (half4_t){};
+          pv[mt][nt][q4] = s0 < N ? *reinterpret_cast<const half4_t*>(P + poff(t, s0)) : (half4_t){};
 #pragma unroll
           for (int e = 0; e < 4; ++e) s += (float)pv[mt][nt][q4][e] * acc[mt][nt][q4 * 4 + e];
         }
@@ -271,12 +339,10 @@ __global__ __launch_bounds__(512) void scores_kernel(
       float s = 0.f;
 #pragma unroll
       for (int w2 = 0; w2 < 8; ++w2) s += red[w2][nt * 32 + l32];
-      gpart[nt] = s;
       const int t = row0 + nt * 32 + l32;
       if (t >= rend) continue;
       if (wv == 0 && hl == 0) gamma[(long long)t * ldg + c] = s;
       const float coef = temp * w[(long long)t * ldw + c];
-      _Float16* drow = dS + (long long)t * ldp + (long long)c * N;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -287,7 +353,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               h[e] = (_Float16)(coef * (float)pv[mt][nt][q4][e] * (acc[mt][nt][q4 * 4 + e] - s));
-            *reinterpret_cast<half4_t*>(drow + s0) = h;
+            *reinterpret_cast<half4_t*>(dS + poff(t, s0)) = h;
           }
         }
     }
@@ -295,26 +361,29 @@ __global__ __launch_bounds__(512) void scores_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// Readout kernel: out[t, :] = sum_c scale(t,c) sum_n A[t, c*N + n] K_c[n, :], as an NT GEMM over
-// the transposed pages K^T_c [d, N].  Workgroup tile 256 rows x 256 dims, 8 waves (2 x 4), wave
-// tile 128 x 64 (4 x 2 MFMA 32x32 tiles).  scale = w[t, c] when w != nullptr (forward read),
-// else 1 (the backward dS already carries it).  Rows of one tile belong to one library.
-__global__ __launch_bounds__(512) void readout_kernel(
-    const _Float16* __restrict__ A, long long lda, const int* __restrict__ row_ptr,
-    const int* __restrict__ tile_ptr, int G, const _Float16* __restrict__ pagesT, int N, int d,
+// Readout kernel: out[t, :] = sum_c scale(t,c) sum_n A[t, c, n] K_c[n, :] (A octet-major).
+// Workgroup tile 128 rows x 256 dims, 4 waves; wave w owns dims [64w, 64w+64) x all 128 rows
+// (4 x 2 MFMA 32x32 tiles).  The dims of a wave are private to it: their fragments come from the
+// layout-B page copy (coalesced 1 KiB loads), refilled for the next k-step as they are consumed;
+// the 128 A rows are shared and staged through LDS (two swizzled stages of 16 KiB).
+// scale = w[t, c] when w != nullptr (forward read), else 1 (the backward dS already carries it).
+// Rows of one tile belong to one library.
+__global__ __launch_bounds__(256) void readout_kernel(
+    const _Float16* __restrict__ A, long long a_rows, const int* __restrict__ row_ptr,
+    const int* __restrict__ tile_ptr, int G, const _Float16* __restrict__ pages_b, int N, int d,
     long long page_stride, const int* __restrict__ chunk_ptr, const int* __restrict__ chunk_page,
     const float* __restrict__ w, long long ldw, float* __restrict__ out, long long ldo) {
-  __shared__ _Float16 lA[256 * LROW];
-  __shared__ _Float16 lB[256 * LROW];
+  constexpr int RT = kReadoutRows;
+  __shared__ _Float16 lA[2][RT * BK];
 
-  const int b = blockIdx.x;
+  const int b = xcd_remap(blockIdx.x, gridDim.x);
   const int g = find_group(tile_ptr, G, b);
   const int local = b - tile_ptr[g];
   const int ntile_d = (d + 255) / 256;
   const int dt = local % ntile_d;
   const int rt = local / ntile_d;
   const int rbeg = row_ptr[g], rend = row_ptr[g + 1];
-  const int row0 = rbeg + rt * 256;
+  const int row0 = rbeg + rt * RT;
   const int d0 = dt * 256;
   const int cbeg = chunk_ptr[g];
   const int C = chunk_ptr[g + 1] - cbeg;
@@ -322,84 +391,101 @@ __global__ __launch_bounds__(512) void readout_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wv >> 2, wn = wv & 3;  // wave tile rows [128wm, +128), dims [64wn, +64)
   const int hl = lane >> 5;
   const int l32 = lane & 31;
 
-  // staging: A 256 rows x 4 chunks (2 per thread), B 256 dims x 4 chunks (2 per thread)
-  u32x4 ra[2], rb[2];
-  const float* wrow[2];
-  const _Float16* arow[2];
-  const int ar0 = tid >> 2, ach = tid & 3;
+  // A staging: RT rows x 8 octets; thread chunk i covers row (tid % RT), octet (tid/RT + 2i):
+  // consecutive lanes read consecutive rows of one octet (contiguous in the octet-major A).
+  constexpr int NA = RT * 8 / 256;
+  int arow[NA], aoct[NA];
+  long long aoff[NA];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int t = min(row0 + ar0 + 128 * i, rend - 1);
-    arow[i] = A + (long long)t * lda;
-    wrow[i] = w ? w + (long long)t * ldw : nullptr;
+  for (int i = 0; i < NA; ++i) {
+    const int id = tid + 256 * i;
+    arow[i] = id % RT;
+    aoct[i] = id / RT;
+    aoff[i] = min(row0 + arow[i], rend - 1);
   }
-  auto gload = [&](int c, int n0) {
-    const long long acol = (long long)c * N + n0 + ach * 8;
-    const _Float16* Kt = pagesT + (long long)chunk_page[cbeg + c] * page_stride;
+  u32x4 ra[NA];
+  auto load_a = [&](int c, int n0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      ra[i] = *reinterpret_cast<const u32x4*>(arow[i] + acol);
+    for (int i = 0; i < NA; ++i) {
+      const long long oct = (long long)c * (N / 8) + n0 / 8 + aoct[i];
+      ra[i] = *reinterpret_cast<const u32x4*>(A + (oct * a_rows + aoff[i]) * 8);
       if (w) {
-        const _Float16 wh = (_Float16)wrow[i][c];
-        half8_t h = __builtin_bit_cast(half8_t, ra[i]);
-        const half8_t s = {wh, wh, wh, wh, wh, wh, wh, wh};
-        ra[i] = __builtin_bit_cast(u32x4, h * s);
+        const _Float16 wh = (_Float16)w[aoff[i] * ldw + c];
+        const half8_t sc = {wh, wh, wh, wh, wh, wh, wh, wh};
+        ra[i] = __builtin_bit_cast(u32x4, __builtin_bit_cast(half8_t, ra[i]) * sc);
       }
-      const int dd = min(d0 + ar0 + 128 * i, d - 1);
-      rb[i] = *reinterpret_cast<const u32x4*>(Kt + (long long)dd * N + n0 + ach * 8);
     }
   };
-  auto lstore = [&]() {
+  auto store_a = [&](int st) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      *reinterpret_cast<u32x4*>(lA + (ar0 + 128 * i) * LROW + ach * 8) = ra[i];
-      *reinterpret_cast<u32x4*>(lB + (ar0 + 128 * i) * LROW + ach * 8) = rb[i];
-    }
+    for (int i = 0; i < NA; ++i) *reinterpret_cast<u32x4*>(&lA[st][swz(arow[i], aoct[i])]) = ra[i];
   };
+  // B fragments of this wave's two 32-dim groups (groups past d/32 re-read the last one; those
+  // columns are not stored).  Block (db, nb) starts at ((db * N/16 + nb) * 64) * 8.
+  int dbk[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) dbk[nt] = min((d0 + wv * 64 + nt * 32) / 32, d / 32 - 1);
+  auto kb_base = [&](int c) {
+    return pages_b + (long long)chunk_page[cbeg + c] * page_stride + lane * 8;
+  };
+  half8_t fb[2][4];  // [nt][k16 step]
 
-  f32x16 acc[4][2];
+  f32x16 acc[NA][2];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+  for (int mt = 0; mt < NA; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = (f32x16){};
-
-  const int ksteps = N / BK;
-  const int total = C * ksteps;
-  gload(0, 0);
-  for (int it = 0; it < total; ++it) {
-    __syncthreads();
-    lstore();
-    __syncthreads();
-    if (it + 1 < total) gload((it + 1) / ksteps, ((it + 1) % ksteps) * BK);
+  auto compute = [&](int st, const _Float16* kbn, int nbn) {
 #pragma unroll
-    for (int ks = 0; ks < BK; ks += 16) {
-      half8_t fa[4], fb[2];
+    for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-        fa[mt] = *reinterpret_cast<const half8_t*>(lA + (wm * 128 + mt * 32 + l32) * LROW + ks + hl * 8);
+      for (int mt = 0; mt < NA; ++mt) {
+        const half8_t fa = *reinterpret_cast<const half8_t*>(&lA[st][swz(mt * 32 + l32, ks * 2 + hl)]);
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(fa, fb[nt][ks], acc[mt][nt]);
+      }
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
-        fb[nt] = *reinterpret_cast<const half8_t*>(lB + (wn * 64 + nt * 32 + l32) * LROW + ks + hl * 8);
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(fa[mt], fb[nt], acc[mt][nt]);
+        fb[nt][ks] = *reinterpret_cast<const half8_t*>(kbn + ((long long)dbk[nt] * (N / 16) + nbn + ks) * 512);
+      __builtin_amdgcn_sched_barrier(0);  // keep the refill here (see the scores kernel)
     }
-  }
-  // acc[mt][nt][r] = out[row0 + 128wm + 32mt + 8(r/4) + 4hl + r%4][d0 + 64wn + 32nt + l32]
+  };
+
+  const int kpc = N / BK;  // k-steps per chunk
+  const int total = C * kpc;
+  {
+    const _Float16* kb0 = kb_base(0);
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt)
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        fb[nt][ks] = *reinterpret_cast<const half8_t*>(kb0 + ((long long)dbk[nt] * (N / 16) + ks) * 512);
+  }
+  load_a(0, 0);
+  store_a(0);
+  __syncthreads();
+  for (int it = 0; it < total; ++it) {
+    const int nx = min(it + 1, total - 1);  // the prefetch past the last step re-reads it
+    const int cn = nx / kpc, nn = (nx % kpc) * BK;
+    load_a(cn, nn);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(it & 1, kb_base(cn), nn / 16);
+    store_a((it + 1) & 1);
+    __syncthreads();
+  }
+  // acc[mt][nt][r] = out[row0 + 32mt + 8(r/4) + 4hl + r%4][d0 + 64w + 32nt + l32]
+#pragma unroll
+  for (int mt = 0; mt < NA; ++mt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int t = row0 + wm * 128 + mt * 32 + (r >> 2) * 8 + hl * 4 + (r & 3);
+      const int t = row0 + mt * 32 + (r >> 2) * 8 + hl * 4 + (r & 3);
       if (t >= rend) continue;
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
-        const int dd = d0 + wn * 64 + nt * 32 + l32;
+        const int dd = d0 + wv * 64 + nt * 32 + l32;
         if (dd < d) out[(long long)t * ldo + dd] = acc[mt][nt][r];
       }
     }
@@ -492,73 +578,80 @@ extern "C" int xenc_cast_rows_f16(const float* x, long long ldx, int M, int d, v
   return check_launch();
 }
 
-extern "C" int xenc_transpose_pages(const void* pages, int P, int slots_per_page, int d,
-                                    void* pages_t, void* stream) {
-  if (P < 0 || slots_per_page <= 0 || d <= 0 || d % 8 != 0) return XENC_EINVAL;
+extern "C" int xenc_fragment_pages(const void* pages, long long P, int slots_per_page, int d,
+                                   int layout, void* out, void* stream) {
+  if (P < 0 || slots_per_page <= 0 || d <= 0 || (layout != 0 && layout != 1)) return XENC_EINVAL;
+  if (slots_per_page % 32 != 0 || d % 32 != 0) return XENC_EINVAL;
   if (P == 0) return XENC_OK;
-  if (!pages || !pages_t) return XENC_ENULL;
-  if (P > 65535) return XENC_EINVAL;
-  const dim3 grid((d + 31) / 32, (slots_per_page + 31) / 32, P);
-  hipLaunchKernelGGL(transpose_pages_kernel, grid, dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream),
-                     static_cast<const _Float16*>(pages), slots_per_page, d,
-                     static_cast<_Float16*>(pages_t));
+  if (!pages || !out) return XENC_ENULL;
+  if (!aligned16(pages) || !aligned16(out)) return XENC_EALIGN;
+  const long long total = P * (long long)slots_per_page * d / 8;
+  const int blocks = (int)std::min<long long>((total + 255) / 256, 65536);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const _Float16* src = static_cast<const _Float16*>(pages);
+  _Float16* dst = static_cast<_Float16*>(out);
+  if (layout == 0)
+    hipLaunchKernelGGL(fragment_pages_kernel<0>, dim3(blocks), dim3(256), 0, st, src, P,
+                       slots_per_page, d, dst);
+  else
+    hipLaunchKernelGGL(fragment_pages_kernel<1>, dim3(blocks), dim3(256), 0, st, src, P,
+                       slots_per_page, d, dst);
   return check_launch();
 }
 
 static int check_prefill_common(int d, int N, long long page_stride) {
-  if (d <= 0 || d % BK != 0) return XENC_EINVAL;          // k loop of the scores kernel
+  if (d <= 0 || d % BK != 0) return XENC_EINVAL;                       // scores k loop
   if (N <= 0 || N > kSlotsPerTile || N % BK != 0) return XENC_EINVAL;  // readout k loop
   if (page_stride < (long long)N * d || page_stride % 8 != 0) return XENC_EINVAL;
   return XENC_OK;
 }
 
 extern "C" int xenc_prefill_scores(int mode, const void* x, int d, const int* row_ptr,
-                                   const int* tile_ptr, int G, int n_tiles, const void* pages,
+                                   const int* tile_ptr, int G, int n_tiles, const void* pages_a,
                                    int slots_per_page, long long page_stride,
                                    const int* chunk_ptr, const int* chunk_page,
                                    const int* chunk_nvalid, float temp, const float* w,
-                                   long long ldw, void* p, long long ldp, void* ds, float* gamma,
-                                   long long ldg, void* stream) {
+                                   long long ldw, void* p, long long p_rows, void* ds,
+                                   float* gamma, long long ldg, void* stream) {
   if (mode != 0 && mode != 1) return XENC_EINVAL;
   if (int rc = check_prefill_common(d, slots_per_page, page_stride)) return rc;
-  if (G <= 0 || n_tiles < 0 || ldp % 8 != 0) return XENC_EINVAL;
+  if (G <= 0 || n_tiles < 0 || p_rows < 0) return XENC_EINVAL;
   if (n_tiles == 0) return XENC_OK;
-  if (!x || !row_ptr || !tile_ptr || !pages || !chunk_ptr || !chunk_page || !chunk_nvalid || !p)
+  if (!x || !row_ptr || !tile_ptr || !pages_a || !chunk_ptr || !chunk_page || !chunk_nvalid || !p)
     return XENC_ENULL;
   if (mode == 1 && (!w || !ds || !gamma)) return XENC_ENULL;
-  if (!aligned16(x) || !aligned16(pages) || !aligned16(p) || (mode == 1 && !aligned16(ds)))
+  if (!aligned16(x) || !aligned16(pages_a) || !aligned16(p) || (mode == 1 && !aligned16(ds)))
     return XENC_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const _Float16* X = static_cast<const _Float16*>(x);
-  const _Float16* pg = static_cast<const _Float16*>(pages);
+  const _Float16* pg = static_cast<const _Float16*>(pages_a);
   if (mode == 0)
     hipLaunchKernelGGL(scores_kernel<0>, dim3(n_tiles), dim3(512), 0, st, X, d, row_ptr, tile_ptr,
                        G, pg, slots_per_page, page_stride, chunk_ptr, chunk_page, chunk_nvalid,
-                       temp * kLog2e, w, ldw, static_cast<_Float16*>(p), ldp,
+                       temp * kLog2e, w, ldw, static_cast<_Float16*>(p), p_rows,
                        static_cast<_Float16*>(ds), gamma, ldg);
   else
     hipLaunchKernelGGL(scores_kernel<1>, dim3(n_tiles), dim3(512), 0, st, X, d, row_ptr, tile_ptr,
                        G, pg, slots_per_page, page_stride, chunk_ptr, chunk_page, chunk_nvalid,
-                       temp, w, ldw, static_cast<_Float16*>(p), ldp, static_cast<_Float16*>(ds),
+                       temp, w, ldw, static_cast<_Float16*>(p), p_rows, static_cast<_Float16*>(ds),
                        gamma, ldg);
   return check_launch();
 }
 
-extern "C" int xenc_prefill_readout(const void* a, long long lda, const int* row_ptr,
-                                    const int* tile_ptr, int G, int n_tiles, const void* pages_t,
+extern "C" int xenc_prefill_readout(const void* a, long long a_rows, const int* row_ptr,
+                                    const int* tile_ptr, int G, int n_tiles, const void* pages_b,
                                     int slots_per_page, int d, long long page_stride,
                                     const int* chunk_ptr, const int* chunk_page, const float* w,
                                     long long ldw, float* out, long long ldo, void* stream) {
   if (int rc = check_prefill_common(d, slots_per_page, page_stride)) return rc;
-  if (G <= 0 || n_tiles < 0 || lda % 8 != 0 || ldo < d) return XENC_EINVAL;
+  if (G <= 0 || n_tiles < 0 || a_rows < 0 || ldo < d) return XENC_EINVAL;
   if (n_tiles == 0) return XENC_OK;
-  if (!a || !row_ptr || !tile_ptr || !pages_t || !chunk_ptr || !chunk_page || !out)
+  if (!a || !row_ptr || !tile_ptr || !pages_b || !chunk_ptr || !chunk_page || !out)
     return XENC_ENULL;
-  if (!aligned16(a) || !aligned16(pages_t)) return XENC_EALIGN;
-  hipLaunchKernelGGL(readout_kernel, dim3(n_tiles), dim3(512), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<const _Float16*>(a), lda,
-                     row_ptr, tile_ptr, G, static_cast<const _Float16*>(pages_t), slots_per_page,
+  if (!aligned16(a) || !aligned16(pages_b)) return XENC_EALIGN;
+  hipLaunchKernelGGL(readout_kernel, dim3(n_tiles), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<const _Float16*>(a), a_rows,
+                     row_ptr, tile_ptr, G, static_cast<const _Float16*>(pages_b), slots_per_page,
                      d, page_stride, chunk_ptr, chunk_page, w, ldw, out, ldo);
   return check_launch();
 }

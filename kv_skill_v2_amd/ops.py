@@ -40,7 +40,7 @@ class PagedLibrary:
     S: torch.Tensor              # fp32 [Ctot, d]
     n_chunks: list[int] = field(default_factory=list)   # host copy: chunks per library
     nvalid: list[int] = field(default_factory=list)     # host copy: valid slots per chunk
-    _pages_t: torch.Tensor | None = field(default=None, repr=False, compare=False)
+    _frag: dict = field(default_factory=dict, repr=False, compare=False)
 
     def __post_init__(self):
         for name in ("pages", "chunk_page", "chunk_nvalid", "chunk_ptr", "S"):
@@ -128,22 +128,23 @@ class PagedLibrary:
         return max(c if (top_k <= 0 or top_k >= c) else top_k for c in self.n_chunks)
 
     def check_prefill(self) -> None:
-        """The MFMA prefill kernels tile d and the slots by 32 and a page by <= 512 slots."""
-        if self.d % 32 or self.slots_per_page % 32 or self.slots_per_page > 512:
-            raise ValueError(f"the prefill read needs d % 32 == 0 and slots_per_page % 32 == 0, <= 512 "
+        """The MFMA prefill kernels step d and the slots by 64 and take a page of <= 512 slots."""
+        if self.d % 64 or self.slots_per_page % 64 or self.slots_per_page > 512:
+            raise ValueError(f"the prefill read needs d % 64 == 0 and slots_per_page % 64 == 0, <= 512 "
                              f"(got d={self.d}, slots={self.slots_per_page}); build the pool with padding")
 
-    @property
-    def pages_t(self) -> torch.Tensor:
-        """Transposed pages K^T [P, d, slots] (fp16) for the readout GEMM; built once on first use
-        by the transpose kernel and kept with the pool (the library is resident across steps)."""
-        if self._pages_t is None:
+    def fragment_pages(self, layout: int) -> torch.Tensor:
+        """Fragment-ordered copy of the pages for the prefill MFMA kernels (layout 0: scores,
+        [P][slots/32][d/16][64][8]; layout 1: readout, [P][d/32][slots/16][64][8]), built on first
+        use by xenc_fragment_pages and kept with the pool (the library is resident across steps)."""
+        t = self._frag.get(layout)
+        if t is None:
             P, N, d = self.pages.shape
-            t = torch.empty(P, d, N, dtype=torch.float16, device=self.device)
-            check(lib().xenc_transpose_pages(ptr(self.pages), P, N, d, ptr(t), stream_handle(self.device)),
-                  "xenc_transpose_pages")
-            self._pages_t = t
-        return self._pages_t
+            t = torch.empty(P, N, d, dtype=torch.float16, device=self.device)
+            check(lib().xenc_fragment_pages(ptr(self.pages), P, N, d, layout, ptr(t),
+                                            stream_handle(self.device)), "xenc_fragment_pages")
+            self._frag[layout] = t
+        return t
 
 
 def _groups(lib_: PagedLibrary, M: int, q_group) -> torch.Tensor:
@@ -261,7 +262,7 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
 
 # ---------------------------------------------------------------------------------------------
 # Prefill / registration read (MFMA) and the autograd of routing + read
-ROWS_SCORES, ROWS_READOUT, ROWS_ROUTE_BWD = 128, 256, 16
+ROWS_SCORES, ROWS_READOUT, ROWS_ROUTE_BWD = 128, 128, 16
 
 
 def _prefix(counts) -> list[int]:
@@ -316,15 +317,16 @@ def cast_f16(x: torch.Tensor) -> torch.Tensor:
     return y
 
 
-def _ldp(lib_: PagedLibrary) -> int:
-    n = lib_.cmax * lib_.slots_per_page
-    return (n + 7) // 8 * 8
+def unpack_p(p: torch.Tensor, M: int) -> torch.Tensor:
+    """Octet-major p / dS [cmax*slots/8, M, 8] -> row-major [M, cmax*slots] (a view copy)."""
+    return p.view(-1, M, 8).permute(1, 0, 2).reshape(M, -1)
 
 
 def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
                     read_temp: float = 12.0):
-    """(r [M, d] fp32, p [M, ldp] fp16): the route-weighted masked-softmax read of many query rows.
-    HIP kernels scores_kernel<0> + readout_kernel (kv_skill_v2_amd/csrc/prefill.hip)."""
+    """(r [M, d] fp32, p fp16 octet-major [cmax*slots/8, M, 8]): the route-weighted masked-softmax
+    read of many query rows.  HIP kernels scores_kernel<0> + readout_kernel
+    (kv_skill_v2_amd/csrc/prefill.hip); unpack_p gives p row-major."""
     lib_.check_prefill()
     q = _query(q, lib_.d)
     M, d = q.shape
@@ -333,16 +335,15 @@ def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: 
     w = w.to(torch.float32).contiguous()
     L, st, N = lib(), stream_handle(q.device), lib_.slots_per_page
     qh = cast_f16(q)
-    ldp = _ldp(lib_)
-    p = torch.empty(M, ldp, dtype=torch.float16, device=q.device)
+    pa, pb = lib_.fragment_pages(0), lib_.fragment_pages(1)
+    p = torch.empty(lib_.cmax * N // 8, M, 8, dtype=torch.float16, device=q.device)
     check(L.xenc_prefill_scores(0, ptr(qh), d, ptr(plan.row_ptr), ptr(plan.score_tiles), lib_.n_libraries,
-                                plan.n_score, ptr(lib_.pages), N, lib_.pages.stride(0), ptr(lib_.chunk_ptr),
+                                plan.n_score, ptr(pa), N, pa.stride(0), ptr(lib_.chunk_ptr),
                                 ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), float(read_temp), None, 0,
-                                ptr(p), ldp, None, None, 0, st), "xenc_prefill_scores")
+                                ptr(p), M, None, None, 0, st), "xenc_prefill_scores")
     r = torch.empty(M, d, dtype=torch.float32, device=q.device)
-    pt = lib_.pages_t
-    check(L.xenc_prefill_readout(ptr(p), ldp, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
-                                 plan.n_readout, ptr(pt), N, d, pt.stride(0), ptr(lib_.chunk_ptr),
+    check(L.xenc_prefill_readout(ptr(p), M, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
+                                 plan.n_readout, ptr(pb), N, d, pb.stride(0), ptr(lib_.chunk_ptr),
                                  ptr(lib_.chunk_page), ptr(w), w.stride(0), ptr(r), r.stride(0), st),
           "xenc_prefill_readout")
     return r, p
@@ -357,18 +358,19 @@ def prefill_backward(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, lib_: Pa
     w = w.to(torch.float32).contiguous()
     L, st, N = lib(), stream_handle(g.device), lib_.slots_per_page
     gh = cast_f16(g)
-    ldp = p.stride(0)
+    if p.shape != (lib_.cmax * N // 8, M, 8) or not p.is_contiguous():
+        raise ValueError("p must be the octet-major probabilities prefill_forward returned")
+    pa, pb = lib_.fragment_pages(0), lib_.fragment_pages(1)
     ds = torch.empty_like(p)
     gamma = torch.zeros(M, lib_.cmax, dtype=torch.float32, device=g.device)
     check(L.xenc_prefill_scores(1, ptr(gh), d, ptr(plan.row_ptr), ptr(plan.score_tiles), lib_.n_libraries,
-                                plan.n_score, ptr(lib_.pages), N, lib_.pages.stride(0), ptr(lib_.chunk_ptr),
+                                plan.n_score, ptr(pa), N, pa.stride(0), ptr(lib_.chunk_ptr),
                                 ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), float(read_temp), ptr(w),
-                                w.stride(0), ptr(p), ldp, ptr(ds), ptr(gamma), gamma.stride(0), st),
+                                w.stride(0), ptr(p), M, ptr(ds), ptr(gamma), gamma.stride(0), st),
           "xenc_prefill_scores")
     dq = torch.empty(M, d, dtype=torch.float32, device=g.device)
-    pt = lib_.pages_t
-    check(L.xenc_prefill_readout(ptr(ds), ldp, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
-                                 plan.n_readout, ptr(pt), N, d, pt.stride(0), ptr(lib_.chunk_ptr),
+    check(L.xenc_prefill_readout(ptr(ds), M, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
+                                 plan.n_readout, ptr(pb), N, d, pb.stride(0), ptr(lib_.chunk_ptr),
                                  ptr(lib_.chunk_page), None, 0, ptr(dq), dq.stride(0), st),
           "xenc_prefill_readout")
     return dq, gamma

@@ -34,7 +34,7 @@ CASES = [
     # (d, N, chunks per library, rows per library, top_k)
     (256, 512, [4], [64], 2),
     (128, 64, [5, 3], [300, 17], 0),
-    (256, 96, [7], [130], 3),
+    (256, 192, [7], [130], 3),
     (2048, 512, [6], [256], 0),
     (512, 128, [9, 2, 4], [40, 200, 129], 4),
 ]
@@ -52,7 +52,7 @@ def test_prefill_forward_parity(dev, d, N, counts, rows, top_k):
         wg, _, _ = ops.route_topk(q.to(dev), lib, ops._plan_groups(plan).to(dev), top_k=top_k)
         _, p = ops.prefill_forward(q.to(dev), wg, lib, plan)
     torch.cuda.synchronize()
-    r, p = r.cpu().double(), p.cpu().float()
+    r, p = r.cpu().double(), ops.unpack_p(p, sum(rows)).cpu().float()
     off = 0
     for g, T in enumerate(rows):
         K, M, S = P.library(g)
