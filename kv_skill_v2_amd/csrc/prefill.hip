@@ -395,33 +395,35 @@ __global__ __launch_bounds__(256) void readout_kernel(
   const int l32 = lane & 31;
 
   // A staging: RT rows x 8 octets; thread chunk i covers row (tid % RT), octet (tid/RT + 2i):
-  // consecutive lanes read consecutive rows of one octet (contiguous in the octet-major A).
+  // consecutive lanes read consecutive rows of one octet (contiguous in the octet-major A).  All
+  // chunks of a thread share its row, hence one scale per k-step, applied when the chunks are
+  // stored to LDS (after the k-step's MFMAs, by which time the loads have landed).
   constexpr int NA = RT * 8 / 256;
-  int arow[NA], aoct[NA];
-  long long aoff[NA];
+  const int arow = tid % RT;
+  const long long arow_g = min(row0 + arow, rend - 1);
+  int aoct[NA];
 #pragma unroll
-  for (int i = 0; i < NA; ++i) {
-    const int id = tid + 256 * i;
-    arow[i] = id % RT;
-    aoct[i] = id / RT;
-    aoff[i] = min(row0 + arow[i], rend - 1);
-  }
+  for (int i = 0; i < NA; ++i) aoct[i] = tid / RT + 2 * i;
   u32x4 ra[NA];
+  float wa = 1.f;
   auto load_a = [&](int c, int n0) {
 #pragma unroll
     for (int i = 0; i < NA; ++i) {
       const long long oct = (long long)c * (N / 8) + n0 / 8 + aoct[i];
-      ra[i] = *reinterpret_cast<const u32x4*>(A + (oct * a_rows + aoff[i]) * 8);
-      if (w) {
-        const _Float16 wh = (_Float16)w[aoff[i] * ldw + c];
-        const half8_t sc = {wh, wh, wh, wh, wh, wh, wh, wh};
-        ra[i] = __builtin_bit_cast(u32x4, __builtin_bit_cast(half8_t, ra[i]) * sc);
-      }
+      ra[i] = *reinterpret_cast<const u32x4*>(A + (oct * a_rows + arow_g) * 8);
     }
+    if (w) wa = w[arow_g * ldw + c];
   };
   auto store_a = [&](int st) {
+    if (w) {
+      const _Float16 wh = (_Float16)wa;
+      const half8_t sc = {wh, wh, wh, wh, wh, wh, wh, wh};
 #pragma unroll
-    for (int i = 0; i < NA; ++i) *reinterpret_cast<u32x4*>(&lA[st][swz(arow[i], aoct[i])]) = ra[i];
+      for (int i = 0; i < NA; ++i)
+        ra[i] = __builtin_bit_cast(u32x4, __builtin_bit_cast(half8_t, ra[i]) * sc);
+    }
+#pragma unroll
+    for (int i = 0; i < NA; ++i) *reinterpret_cast<u32x4*>(&lA[st][swz(arow, aoct[i])]) = ra[i];
   };
   // B fragments of this wave's two 32-dim groups (groups past d/32 re-read the last one; those
   // columns are not stored).  Block (db, nb) starts at ((db * N/16 + nb) * 64) * 8.
