@@ -127,6 +127,9 @@ __global__ __launch_bounds__(256) void fragment_pages_kernel(const _Float16* __r
 // MODE 0 (forward): writes p = masked softmax over the chunk's slots (fp16, octet-major).
 // MODE 1 (backward): reads p, writes dS = read_temp * w[t,c] * p * (U - gamma) (octet-major)
 //                    and gamma[t, c] = sum_n p U.
+// MODE 2 (forward, linear read): writes p = S / sqrt(n_valid) on valid slots, 0 on the others.
+// MODE 3 (backward, linear read): reads p, writes dS = w[t,c] * U / sqrt(n_valid) (0 on masked
+//                    slots) and gamma[t, c] = sum_n p U.
 template <int MODE>
 __global__ __launch_bounds__(512) void scores_kernel(
     const _Float16* __restrict__ X, int d, const int* __restrict__ row_ptr,
@@ -240,7 +243,28 @@ __global__ __launch_bounds__(512) void scores_kernel(
     return ((long long)(c * (N / 8) + (s0 >> 3)) * p_rows + t) * 8 + (s0 & 7);
   };
 
-  if (MODE == 0) {
+  if (MODE == 2) {
+    // ---- linear read: p = S / sqrt(n_valid), masked slots 0
+    const float inv = 1.f / sqrtf((float)nv);
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt) {
+      const int t = row0 + nt * 32 + l32;
+      if (t >= rend) continue;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int s0 = slot_of(mt, q4 * 4);
+          if (s0 < N) {
+            half4_t h;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              h[e] = (_Float16)(s0 + e < nv ? acc[mt][nt][q4 * 4 + e] * inv : 0.f);
+            *reinterpret_cast<half4_t*>(P + poff(t, s0)) = h;
+          }
+        }
+    }
+  } else if (MODE == 0) {
     // ---- masked softmax over the chunk's slots, per query row
     float rmax[4];
 #pragma unroll
@@ -342,7 +366,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
       const int t = row0 + nt * 32 + l32;
       if (t >= rend) continue;
       if (wv == 0 && hl == 0) gamma[(long long)t * ldg + c] = s;
-      const float coef = temp * w[(long long)t * ldw + c];
+      const float coef = (MODE == 1 ? temp : 1.f / sqrtf((float)nv)) * w[(long long)t * ldw + c];
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -351,8 +375,11 @@ __global__ __launch_bounds__(512) void scores_kernel(
           if (s0 < N) {
             half4_t h;
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              h[e] = (_Float16)(coef * (float)pv[mt][nt][q4][e] * (acc[mt][nt][q4 * 4 + e] - s));
+            for (int e = 0; e < 4; ++e) {
+              const float u = acc[mt][nt][q4 * 4 + e];
+              h[e] = (_Float16)(MODE == 1 ? coef * (float)pv[mt][nt][q4][e] * (u - s)
+                                          : (s0 + e < nv ? coef * u : 0.f));
+            }
             *reinterpret_cast<half4_t*>(dS + poff(t, s0)) = h;
           }
         }
@@ -615,28 +642,30 @@ extern "C" int xenc_prefill_scores(int mode, const void* x, int d, const int* ro
                                    const int* chunk_nvalid, float temp, const float* w,
                                    long long ldw, void* p, long long p_rows, void* ds,
                                    float* gamma, long long ldg, void* stream) {
-  if (mode != 0 && mode != 1) return XENC_EINVAL;
+  if (mode < 0 || mode > 3) return XENC_EINVAL;
   if (int rc = check_prefill_common(d, slots_per_page, page_stride)) return rc;
   if (G <= 0 || n_tiles < 0 || p_rows < 0) return XENC_EINVAL;
   if (n_tiles == 0) return XENC_OK;
   if (!x || !row_ptr || !tile_ptr || !pages_a || !chunk_ptr || !chunk_page || !chunk_nvalid || !p)
     return XENC_ENULL;
-  if (mode == 1 && (!w || !ds || !gamma)) return XENC_ENULL;
-  if (!aligned16(x) || !aligned16(pages_a) || !aligned16(p) || (mode == 1 && !aligned16(ds)))
+  const bool bwd = mode & 1;
+  if (bwd && (!w || !ds || !gamma)) return XENC_ENULL;
+  if (!aligned16(x) || !aligned16(pages_a) || !aligned16(p) || (bwd && !aligned16(ds)))
     return XENC_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const _Float16* X = static_cast<const _Float16*>(x);
   const _Float16* pg = static_cast<const _Float16*>(pages_a);
-  if (mode == 0)
-    hipLaunchKernelGGL(scores_kernel<0>, dim3(n_tiles), dim3(512), 0, st, X, d, row_ptr, tile_ptr,
-                       G, pg, slots_per_page, page_stride, chunk_ptr, chunk_page, chunk_nvalid,
-                       temp * kLog2e, w, ldw, static_cast<_Float16*>(p), p_rows,
-                       static_cast<_Float16*>(ds), gamma, ldg);
-  else
-    hipLaunchKernelGGL(scores_kernel<1>, dim3(n_tiles), dim3(512), 0, st, X, d, row_ptr, tile_ptr,
-                       G, pg, slots_per_page, page_stride, chunk_ptr, chunk_page, chunk_nvalid,
-                       temp, w, ldw, static_cast<_Float16*>(p), p_rows, static_cast<_Float16*>(ds),
-                       gamma, ldg);
+  auto launch = [&](auto kernel, float t) {
+    hipLaunchKernelGGL(kernel, dim3(n_tiles), dim3(512), 0, st, X, d, row_ptr, tile_ptr, G, pg,
+                       slots_per_page, page_stride, chunk_ptr, chunk_page, chunk_nvalid, t, w, ldw,
+                       static_cast<_Float16*>(p), p_rows, static_cast<_Float16*>(ds), gamma, ldg);
+  };
+  switch (mode) {
+    case 0: launch(scores_kernel<0>, temp * kLog2e); break;
+    case 1: launch(scores_kernel<1>, temp); break;
+    case 2: launch(scores_kernel<2>, temp); break;
+    default: launch(scores_kernel<3>, temp); break;
+  }
   return check_launch();
 }
 

@@ -40,7 +40,10 @@ class PagedLibrary:
     S: torch.Tensor              # fp32 [Ctot, d]
     n_chunks: list[int] = field(default_factory=list)   # host copy: chunks per library
     nvalid: list[int] = field(default_factory=list)     # host copy: valid slots per chunk
+    values: torch.Tensor | None = None   # fp16 [P, slots_per_page, d] when V is untied from K
+    d_valid: int = 0                     # leading feature dims in use (the rest is zero padding)
     _frag: dict = field(default_factory=dict, repr=False, compare=False)
+    _plans: dict = field(default_factory=dict, repr=False, compare=False)
 
     def __post_init__(self):
         for name in ("pages", "chunk_page", "chunk_nvalid", "chunk_ptr", "S"):
@@ -65,22 +68,39 @@ class PagedLibrary:
         cpg = self.chunk_page
         if int(cpg.min()) < 0 or int(cpg.max()) >= P:
             raise ValueError(f"page table entries must lie in [0, {P})")
+        if self.values is not None:
+            _require_device(self.values, "values")
+            if (self.values.shape != self.pages.shape or self.values.dtype != torch.float16
+                    or not self.values.is_contiguous()):
+                raise ValueError("values must be a contiguous fp16 tensor shaped like pages")
+        if not 0 < self.d_valid <= d:
+            self.d_valid = d
 
     # ------------------------------------------------------------------ constructors
     @staticmethod
-    def from_padded(K: torch.Tensor, mask: torch.Tensor, S: torch.Tensor, device=None) -> "PagedLibrary":
-        """One library from the reference layout K [C, N, d], mask [C, N] (valid prefix), S [C, d]."""
-        return PagedLibrary.from_libraries([(K, mask, S)], device=device)
+    def from_padded(K: torch.Tensor, mask: torch.Tensor, S: torch.Tensor, device=None, V=None,
+                    pad_to: int = 1) -> "PagedLibrary":
+        """One library from the reference layout K [C, N, d], mask [C, N] (valid prefix), S [C, d]
+        (and untied values V [C, N, d])."""
+        return PagedLibrary.from_libraries([(K, mask, S, V)], device=device, pad_to=pad_to)
 
     @staticmethod
-    def from_libraries(libs, device=None, slots_per_page: int | None = None) -> "PagedLibrary":
-        """Several libraries [(K [C,N,d], mask [C,N], S [C,d]), ...] packed into one pool, page id =
-        global chunk id.  Masks must be valid prefixes (slots 0..n-1 valid), as Library builds them."""
+    def from_libraries(libs, device=None, slots_per_page: int | None = None,
+                       pad_to: int = 1) -> "PagedLibrary":
+        """Several libraries [(K [C,N,d], mask [C,N], S [C,d][, V [C,N,d]]), ...] packed into one
+        pool, page id = global chunk id.  Masks must be valid prefixes (slots 0..n-1 valid), as
+        Library builds them.  pad_to > 1 rounds d and the page size up to a multiple of it with
+        zero features / masked slots (the read is unchanged; the MFMA prefill path needs 64)."""
         device = torch.device(device) if device is not None else libs[0][0].device
         d = libs[0][0].shape[-1]
-        N = slots_per_page or max(int(K.shape[1]) for K, _, _ in libs)
-        pages, Ss, nv, nch = [], [], [], []
-        for K, M, S in libs:
+        rnd = lambda x: -(-x // pad_to) * pad_to  # noqa: E731
+        N = rnd(slots_per_page or max(int(lb[0].shape[1]) for lb in libs))
+        dp = rnd(d)
+        untied = any(len(lb) > 3 and lb[3] is not None for lb in libs)
+        pages, vals, Ss, nv, nch = [], [], [], [], []
+        for lb in libs:
+            K, M, S = lb[:3]
+            V = lb[3] if len(lb) > 3 else None
             C, n_max, dk = K.shape
             if dk != d:
                 raise ValueError("all libraries must share d")
@@ -88,10 +108,16 @@ class PagedLibrary:
             pref = torch.arange(n_max, device=M.device).view(1, -1) < cnt.view(-1, 1)
             if not torch.equal(pref, M.bool()):
                 raise ValueError("mask must mark a prefix of valid slots per chunk")
-            pg = torch.zeros(C, N, d, dtype=torch.float16, device=device)
-            pg[:, :n_max] = K.to(device=device, dtype=torch.float16)
+            pg = torch.zeros(C, N, dp, dtype=torch.float16, device=device)
+            pg[:, :n_max, :d] = K.to(device=device, dtype=torch.float16)
             pages.append(pg)
-            Ss.append(S.to(device=device, dtype=torch.float32))
+            if untied:
+                vg = torch.zeros(C, N, dp, dtype=torch.float16, device=device)
+                vg[:, :n_max, :d] = (V if V is not None else K).to(device=device, dtype=torch.float16)
+                vals.append(vg)
+            sp = torch.zeros(C, dp, dtype=torch.float32, device=device)
+            sp[:, :d] = S.to(device=device, dtype=torch.float32)
+            Ss.append(sp)
             nv += cnt.tolist()
             nch.append(C)
         ptr_ = [0]
@@ -100,7 +126,8 @@ class PagedLibrary:
         Ctot = ptr_[-1]
         return PagedLibrary(torch.cat(pages).contiguous(), _i32(list(range(Ctot)), device),
                             _i32(nv, device), _i32(ptr_, device), torch.cat(Ss).contiguous(),
-                            n_chunks=nch, nvalid=nv)
+                            n_chunks=nch, nvalid=nv,
+                            values=torch.cat(vals).contiguous() if untied else None, d_valid=d)
 
     # ------------------------------------------------------------------ properties
     @property
@@ -133,18 +160,32 @@ class PagedLibrary:
             raise ValueError(f"the prefill read needs d % 64 == 0 and slots_per_page % 64 == 0, <= 512 "
                              f"(got d={self.d}, slots={self.slots_per_page}); build the pool with padding")
 
-    def fragment_pages(self, layout: int) -> torch.Tensor:
-        """Fragment-ordered copy of the pages for the prefill MFMA kernels (layout 0: scores,
-        [P][slots/32][d/16][64][8]; layout 1: readout, [P][d/32][slots/16][64][8]), built on first
-        use by xenc_fragment_pages and kept with the pool (the library is resident across steps)."""
-        t = self._frag.get(layout)
+    def fragment_pages(self, layout: int, values: bool = False) -> torch.Tensor:
+        """Fragment-ordered copy of the pages (or of the untied values) for the prefill MFMA
+        kernels (layout 0: scores operand, [P][slots/32][d/16][64][8]; layout 1: readout operand,
+        [P][d/32][slots/16][64][8]), built on first use by xenc_fragment_pages and kept with the
+        pool (the library is resident across steps)."""
+        src = self.values if (values and self.values is not None) else self.pages
+        key = (layout, src is self.values)
+        t = self._frag.get(key)
         if t is None:
-            P, N, d = self.pages.shape
+            P, N, d = src.shape
             t = torch.empty(P, N, d, dtype=torch.float16, device=self.device)
-            check(lib().xenc_fragment_pages(ptr(self.pages), P, N, d, layout, ptr(t),
+            check(lib().xenc_fragment_pages(ptr(src), P, N, d, layout, ptr(t),
                                             stream_handle(self.device)), "xenc_fragment_pages")
-            self._frag[layout] = t
+            self._frag[key] = t
         return t
+
+    def plan(self, rows_per_library) -> "RowPlan":
+        """Row plan for this pool, cached per row-count tuple (avoids small host->device copies
+        on every step of a fixed-shape loop)."""
+        key = tuple(int(r) for r in rows_per_library)
+        p = self._plans.get(key)
+        if p is None:
+            if len(self._plans) >= 64:
+                self._plans.clear()
+            p = self._plans[key] = row_plan(self, key)
+        return p
 
 
 def _groups(lib_: PagedLibrary, M: int, q_group) -> torch.Tensor:
@@ -236,6 +277,8 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
     replaces the read of LibraryInjector._branch (xenc/injector.py:239-265)."""
     q = _query(q, lib_.d)
     M = q.shape[0]
+    if lib_.values is not None:
+        raise ValueError("the decode kernel reads K = V tied pages; untied values take the prefill path")
     g = _groups(lib_, M, q_group)
     _require_device(idx, "idx")
     if idx.dim() != 2 or idx.shape[0] != M or w_sel.shape != idx.shape:
@@ -323,9 +366,9 @@ def unpack_p(p: torch.Tensor, M: int) -> torch.Tensor:
 
 
 def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
-                    read_temp: float = 12.0):
+                    read_temp: float = 12.0, softmax: bool = True):
     """(r [M, d] fp32, p fp16 octet-major [cmax*slots/8, M, 8]): the route-weighted masked-softmax
-    read of many query rows.  HIP kernels scores_kernel<0> + readout_kernel
+    (or linear) read of many query rows.  HIP kernels scores_kernel<0|2> + readout_kernel
     (kv_skill_v2_amd/csrc/prefill.hip); unpack_p gives p row-major."""
     lib_.check_prefill()
     q = _query(q, lib_.d)
@@ -335,24 +378,25 @@ def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: 
     w = w.to(torch.float32).contiguous()
     L, st, N = lib(), stream_handle(q.device), lib_.slots_per_page
     qh = cast_f16(q)
-    pa, pb = lib_.fragment_pages(0), lib_.fragment_pages(1)
+    ka, vb = lib_.fragment_pages(0), lib_.fragment_pages(1, values=True)
     p = torch.empty(lib_.cmax * N // 8, M, 8, dtype=torch.float16, device=q.device)
-    check(L.xenc_prefill_scores(0, ptr(qh), d, ptr(plan.row_ptr), ptr(plan.score_tiles), lib_.n_libraries,
-                                plan.n_score, ptr(pa), N, pa.stride(0), ptr(lib_.chunk_ptr),
-                                ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), float(read_temp), None, 0,
-                                ptr(p), M, None, None, 0, st), "xenc_prefill_scores")
+    check(L.xenc_prefill_scores(0 if softmax else 2, ptr(qh), d, ptr(plan.row_ptr), ptr(plan.score_tiles),
+                                lib_.n_libraries, plan.n_score, ptr(ka), N, ka.stride(0),
+                                ptr(lib_.chunk_ptr), ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid),
+                                float(read_temp), None, 0, ptr(p), M, None, None, 0, st), "xenc_prefill_scores")
     r = torch.empty(M, d, dtype=torch.float32, device=q.device)
     check(L.xenc_prefill_readout(ptr(p), M, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
-                                 plan.n_readout, ptr(pb), N, d, pb.stride(0), ptr(lib_.chunk_ptr),
+                                 plan.n_readout, ptr(vb), N, d, vb.stride(0), ptr(lib_.chunk_ptr),
                                  ptr(lib_.chunk_page), ptr(w), w.stride(0), ptr(r), r.stride(0), st),
           "xenc_prefill_readout")
     return r, p
 
 
 def prefill_backward(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, lib_: PagedLibrary,
-                     plan: RowPlan, read_temp: float = 12.0):
+                     plan: RowPlan, read_temp: float = 12.0, softmax: bool = True):
     """(dq through the read [M, d] fp32, gamma = dL/dw through the read [M, cmax] fp32) given the
-    upstream gradient g = dL/dr.  HIP kernels scores_kernel<1> + readout_kernel."""
+    upstream gradient g = dL/dr.  HIP kernels scores_kernel<1|3> (u = g . V) + readout_kernel
+    (dq = dS . K)."""
     g = _query(g, lib_.d)
     M, d = g.shape
     w = w.to(torch.float32).contiguous()
@@ -360,17 +404,17 @@ def prefill_backward(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, lib_: Pa
     gh = cast_f16(g)
     if p.shape != (lib_.cmax * N // 8, M, 8) or not p.is_contiguous():
         raise ValueError("p must be the octet-major probabilities prefill_forward returned")
-    pa, pb = lib_.fragment_pages(0), lib_.fragment_pages(1)
+    va, kb = lib_.fragment_pages(0, values=True), lib_.fragment_pages(1)
     ds = torch.empty_like(p)
     gamma = torch.zeros(M, lib_.cmax, dtype=torch.float32, device=g.device)
-    check(L.xenc_prefill_scores(1, ptr(gh), d, ptr(plan.row_ptr), ptr(plan.score_tiles), lib_.n_libraries,
-                                plan.n_score, ptr(pa), N, pa.stride(0), ptr(lib_.chunk_ptr),
-                                ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), float(read_temp), ptr(w),
-                                w.stride(0), ptr(p), M, ptr(ds), ptr(gamma), gamma.stride(0), st),
-          "xenc_prefill_scores")
+    check(L.xenc_prefill_scores(1 if softmax else 3, ptr(gh), d, ptr(plan.row_ptr), ptr(plan.score_tiles),
+                                lib_.n_libraries, plan.n_score, ptr(va), N, va.stride(0),
+                                ptr(lib_.chunk_ptr), ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid),
+                                float(read_temp), ptr(w), w.stride(0), ptr(p), M, ptr(ds), ptr(gamma),
+                                gamma.stride(0), st), "xenc_prefill_scores")
     dq = torch.empty(M, d, dtype=torch.float32, device=g.device)
     check(L.xenc_prefill_readout(ptr(ds), M, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
-                                 plan.n_readout, ptr(pb), N, d, pb.stride(0), ptr(lib_.chunk_ptr),
+                                 plan.n_readout, ptr(kb), N, d, kb.stride(0), ptr(lib_.chunk_ptr),
                                  ptr(lib_.chunk_page), None, 0, ptr(dq), dq.stride(0), st),
           "xenc_prefill_readout")
     return dq, gamma
@@ -418,30 +462,91 @@ class RouteFn(torch.autograd.Function):
 
 
 class ReadFn(torch.autograd.Function):
-    """r [M, d] = route-weighted masked-softmax read; differentiable in q and w."""
+    """r [M, d] = route-weighted masked-softmax (or linear) read; differentiable in q and w."""
 
     @staticmethod
-    def forward(ctx, q, w, lib_, plan, read_temp):
-        r, p = prefill_forward(q.detach(), w.detach(), lib_, plan, read_temp)
+    def forward(ctx, q, w, lib_, plan, read_temp, softmax=True):
+        r, p = prefill_forward(q.detach(), w.detach(), lib_, plan, read_temp, softmax)
         ctx.save_for_backward(w, p)
-        ctx.lib, ctx.plan, ctx.read_temp = lib_, plan, read_temp
+        ctx.lib, ctx.plan, ctx.read_temp, ctx.softmax = lib_, plan, read_temp, softmax
         return r
 
     @staticmethod
     def backward(ctx, dr):
         w, p = ctx.saved_tensors
-        dq, gamma = prefill_backward(dr, w, p, ctx.lib, ctx.plan, ctx.read_temp)
-        return dq, gamma, None, None, None
+        dq, gamma = prefill_backward(dr, w, p, ctx.lib, ctx.plan, ctx.read_temp, ctx.softmax)
+        return dq, gamma, None, None, None, None
 
 
 def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int = 0,
-                 read_temp: float = 12.0, route_temp: float = 10.0):
+                 read_temp: float = 12.0, route_temp: float = 10.0, read_softmax: bool = True):
     """(r [M, d], w [M, cmax]) with autograd through both routing and the read (MFMA path)."""
     w, _, _ = RouteFn.apply(q, lib_, plan, int(top_k), float(route_temp))
-    r = ReadFn.apply(q, w, lib_, plan, float(read_temp))
+    r = ReadFn.apply(q, w, lib_, plan, float(read_temp), bool(read_softmax))
     return r, w
+
+
+# Above this many query rows on one library the MFMA prefill path reads it (each page once per
+# 128-row tile); at or below it the split-K decode path does (each page once per row).
+DECODE_MAX_ROWS = 8
+
+
+def prefill_ok(lib_: PagedLibrary) -> bool:
+    return lib_.d % 64 == 0 and lib_.slots_per_page % 64 == 0 and lib_.slots_per_page <= 512
+
+
+def _pad_rows(q: torch.Tensor, lib_: PagedLibrary) -> torch.Tensor:
+    _require_device(q, "q")
+    if q.dim() != 2 or q.shape[1] != lib_.d_valid:
+        raise ValueError(f"q must be [M, {lib_.d_valid}], got {tuple(q.shape)}")
+    q = q.to(torch.float32)
+    return torch.nn.functional.pad(q, (0, lib_.d - lib_.d_valid)) if lib_.d != lib_.d_valid else q
+
+
+def _single(lib_: PagedLibrary) -> None:
+    if lib_.n_libraries != 1:
+        raise ValueError("this entry point reads one library; use route_topk / library_read_decode for pools")
+
+
+def route_rows(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, route_temp: float = 10.0):
+    """(w [M, C], idx [M, kk], w_sel [M, kk]) for M query rows over ONE library
+    (LibraryInjector.route, xenc/injector.py:220-229).  Differentiable in q (through w) when q
+    requires grad; q has d_valid features (zero-padded here to the pool's width)."""
+    _single(lib_)
+    qp = _pad_rows(q, lib_)
+    if torch.is_grad_enabled() and q.requires_grad:
+        return RouteFn.apply(qp, lib_, lib_.plan([qp.shape[0]]), int(top_k), float(route_temp))
+    return route_topk(qp, lib_, None, top_k, route_temp)
+
+
+def read_rows(q: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, w_sel: torch.Tensor,
+              lib_: PagedLibrary, read_temp: float = 12.0, read_softmax: bool = True) -> torch.Tensor:
+    """r [M, d_valid]: the read of M query rows over ONE library given their routing (the read of
+    LibraryInjector._branch, xenc/injector.py:239-265).
+
+    With autograd (q or w requires grad), untied values, or more than DECODE_MAX_ROWS rows it runs
+    the MFMA prefill path (differentiable in q and w); otherwise the split-K decode path."""
+    _single(lib_)
+    qp = _pad_rows(q, lib_)
+    M = qp.shape[0]
+    grad = torch.is_grad_enabled() and (q.requires_grad or w.requires_grad)
+    if grad or lib_.values is not None or M > DECODE_MAX_ROWS:
+        if not prefill_ok(lib_):
+            raise ValueError("this read needs the MFMA prefill path, which takes pages of <= 512 "
+                             f"slots (got {lib_.slots_per_page}); split the chunks")
+        r = ReadFn.apply(qp, w, lib_, lib_.plan([M]), float(read_temp), bool(read_softmax))
+    else:
+        r = library_read_decode(qp, lib_, idx, w_sel, None, read_temp, read_softmax)
+    return r[:, :lib_.d_valid] if lib_.d != lib_.d_valid else r
+
+
+def branch_read(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, read_temp: float = 12.0,
+                route_temp: float = 10.0, read_softmax: bool = True):
+    """(r [M, d_valid], w [M, C]): route_rows + read_rows."""
+    w, idx, wsel = route_rows(q, lib_, top_k, route_temp)
+    return read_rows(q, w, idx, wsel, lib_, read_temp, read_softmax), w
 
 
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
            "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "RouteFn", "ReadFn",
-           "library_read"]
+           "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS"]
