@@ -273,7 +273,8 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
                         nsplit: int | None = None) -> torch.Tensor:
     """r [M, d] fp32: route-weighted masked-softmax (or linear) read over the routed pages.
 
-    HIP kernels `decode_split_kernel` + `decode_merge_kernel` (kv_skill_v2_amd/csrc/decode.hip);
+    HIP kernel `decode_read_kernel` (kv_skill_v2_amd/csrc/decode.hip: split-K partials merged by
+    the last-arriving workgroup of each query row);
     replaces the read of LibraryInjector._branch (xenc/injector.py:239-265)."""
     q = _query(q, lib_.d)
     M = q.shape[0]
