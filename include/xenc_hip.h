@@ -69,15 +69,17 @@ int xenc_route_topk(const float* q, long long ldq, int M, int d,
  * split into nsplit ranges of ceil(slots_per_page/nsplit) slots (nsplit in 1..64).
  * r is fp32 [M, ldr].  One kernel launch: the last workgroup of each query merges that
  * query's partials in a fixed order, so results are deterministic.
- * Workspace: xenc_decode_workspace_bytes(M, kk, nsplit, d) bytes whose first M ints are zero
- * before the first call (xenc_decode_workspace_init does that with a kernel, no memset); every
- * call leaves them zero again, so a workspace is initialised once and reused.  Calls that share
- * a workspace must not overlap (same stream, or ordered).
+ * Workspace: xenc_decode_workspace_bytes(max_rows, kk, nsplit, d) bytes for calls of up to
+ * max_rows query rows (pass the same max_rows to every call); its first max_rows ints are
+ * arrival counters that must be zero before the first call (xenc_decode_workspace_init does that
+ * with a kernel, no memset).  Every call leaves them zero again, so a workspace is initialised
+ * once and reused by calls of any M <= max_rows.  Calls that share a workspace must not overlap
+ * (same stream, or ordered).
  * Replaces the read of LibraryInjector._branch (xenc/injector.py:236-265) when the routed
  * chunks are known: equal to reading every chunk with w = 0 off the top-k.
  */
-size_t xenc_decode_workspace_bytes(int M, int kk, int nsplit, int d);
-int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int M, void* stream);
+size_t xenc_decode_workspace_bytes(int max_rows, int kk, int nsplit, int d);
+int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int max_rows, void* stream);
 int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
                              const void* pages, int slots_per_page, long long page_stride,
                              const int* chunk_page, const int* chunk_nvalid,
@@ -85,7 +87,7 @@ int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
                              const int* idx, const float* w_sel, int kk,
                              float read_temp, int softmax, int nsplit,
                              float* r, long long ldr,
-                             void* workspace, size_t workspace_bytes, void* stream);
+                             void* workspace, size_t workspace_bytes, int max_rows, void* stream);
 
 /*
  * ---- Prefill / registration read (many query rows per library; MFMA, fp16 in, fp32 accumulate)
@@ -131,6 +133,39 @@ int xenc_route_backward(const float* w, long long ldw, const float* dw_read, lon
                         const int* tile_ptr, int G, int n_tiles, int cmax, const float* S,
                         const int* chunk_ptr, int d, float route_temp, float* dq, long long ldq,
                         void* stream);
+
+/*
+ * ---- Op B: joint decode read over a document operator's pages and the request's own pages
+ * For query row n < N and query head hq_i = h*G + g (G = hq / hkv, 1 <= G <= 8):
+ *   keys/values = [op pool rows 0..op_len[n]-1 ; own pool rows 0..own_len[n]-1]
+ *   out[n, hq_i] = softmax_l(scale * <q[n, hq_i], K_l[h]>) . V_l[h]    (one softmax over both)
+ * Row l of a pool is block bt[n, l / block_size], slot l % block_size.  Pools are
+ * [num_blocks, block_size, hkv, d] with element strides (sb, ss, sh) and d contiguous; K and V
+ * pools of one kind share shape and strides.  dtype: 0 = fp16, 1 = bf16 (q, pools); out fp32
+ * [N, hq, d] with strides (s_on, s_oh).  d % 8 == 0, d <= 512, G * d <= 4096.  Rows with no keys
+ * give 0.  The joined range is split into nsplit ranges of `chunk` keys (the last split also
+ * takes any keys past nsplit * chunk).  The caller guarantees op_len[n] <= op_bt row width *
+ * block size and that block ids lie in the pool (they are device data; nothing is read back).
+ * Workspace: xenc_joint_workspace_bytes(max_n, hkv, nsplit, G, d) bytes, initialised once by
+ * xenc_joint_workspace_init (its per-(row, kv head) counters are left zero by every call); each
+ * call passes the same max_n and N <= max_n.
+ * Replaces DecodeReader.__call__ (xenc/d23_read_kernels.py:134-160; math :31-47) as called by
+ * read_static (xenc/d23_vllm_plugin.py:489-491).
+ */
+size_t xenc_joint_workspace_bytes(int max_n, int hkv, int nsplit, int g, int d);
+int xenc_joint_workspace_init(void* workspace, size_t workspace_bytes, int max_n, int hkv,
+                              void* stream);
+int xenc_paged_decode_joint(int dtype, int N, int hq, int hkv, int d,
+                            const void* q, long long s_qn, long long s_qh,
+                            const void* op_k, const void* op_v, long long op_sb, long long op_ss,
+                            long long op_sh, int op_bs, const int* op_bt, long long op_bt_stride,
+                            const int* op_len,
+                            const void* own_k, const void* own_v, long long own_sb,
+                            long long own_ss, long long own_sh, int own_bs, const int* own_bt,
+                            long long own_bt_stride, const int* own_len,
+                            float scale, int nsplit, int chunk,
+                            float* out, long long s_on, long long s_oh,
+                            void* workspace, size_t workspace_bytes, int max_n, void* stream);
 
 #ifdef __cplusplus
 }

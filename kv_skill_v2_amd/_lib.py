@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lock = threading.Lock()
 _lib = None
@@ -40,7 +40,7 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int,                   # idx, w_sel, kk
         c_float, c_int, c_int,                       # read_temp, softmax, nsplit
         c_void_p, c_longlong,                        # r, ldr
-        c_void_p, c_size_t, c_void_p]),              # workspace, bytes, stream
+        c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_rows, stream
     "xenc_cast_rows_f16": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p]),
     "xenc_fragment_pages": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p]),
     "xenc_prefill_scores": (c_int, [
@@ -54,6 +54,18 @@ SIGNATURES = {
         c_int, c_int, c_void_p, c_int, c_int,        # G, n_tiles, pages_b, slots_per_page, d
         c_longlong, c_void_p, c_void_p,              # page_stride, chunk_ptr, chunk_page
         c_void_p, c_longlong, c_void_p, c_longlong, c_void_p]),  # w, ldw, out, ldo, stream
+    "xenc_joint_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "xenc_joint_workspace_init": (c_int, [c_void_p, c_size_t, c_int, c_int, c_void_p]),
+    "xenc_paged_decode_joint": (c_int, [
+        c_int, c_int, c_int, c_int, c_int,           # dtype, N, hq, hkv, d
+        c_void_p, c_longlong, c_longlong,            # q, s_qn, s_qh
+        c_void_p, c_void_p, c_longlong, c_longlong, c_longlong, c_int,  # op_k, op_v, strides, bs
+        c_void_p, c_longlong, c_void_p,              # op_bt, op_bt_stride, op_len
+        c_void_p, c_void_p, c_longlong, c_longlong, c_longlong, c_int,  # own_k, own_v, strides, bs
+        c_void_p, c_longlong, c_void_p,              # own_bt, own_bt_stride, own_len
+        c_float, c_int, c_int,                       # scale, nsplit, chunk
+        c_void_p, c_longlong, c_longlong,            # out, s_on, s_oh
+        c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_n, stream
     "xenc_route_backward": (c_int, [
         c_void_p, c_longlong, c_void_p, c_longlong,  # w, ldw, dw_read, ldr
         c_void_p, c_longlong, c_void_p, c_void_p,    # dw_ext, lde, row_ptr, tile_ptr

@@ -464,12 +464,15 @@ __global__ void fill_zero_kernel(int* p, int n) {
 
 static size_t host_align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-static DecodeWorkspace carve(void* base, int M, int kk, int nsplit) {
+// Workspace: [counters: max_rows ints, 256-B aligned | (m, l) per partial | acc per partial].
+// The counter region depends only on the capacity max_rows, never on the call's row count, so
+// counters zeroed once stay in place (and zero) whatever sizes later calls use.
+static DecodeWorkspace carve(void* base, int max_rows, int M, int kk, int nsplit) {
   const size_t units = (size_t)M * kk * nsplit;
   char* p = static_cast<char*>(base);
   DecodeWorkspace ws;
   ws.counters = reinterpret_cast<int*>(p);
-  p += host_align256((size_t)M * sizeof(int));
+  p += host_align256((size_t)max_rows * sizeof(int));
   ws.part_ml = reinterpret_cast<float2*>(p);
   p += host_align256(units * sizeof(float2));
   ws.part_acc = reinterpret_cast<float*>(p);
@@ -494,22 +497,25 @@ static void launch_read(dim3 grid, size_t lds, hipStream_t st, const float* q, l
 
 using namespace xenc;
 
-extern "C" size_t xenc_decode_workspace_bytes(int M, int kk, int nsplit, int d) {
-  if (M <= 0 || kk <= 0 || nsplit <= 0 || d <= 0) return 0;
-  const size_t units = (size_t)M * kk * nsplit;
-  return host_align256((size_t)M * sizeof(int)) + host_align256(units * sizeof(float2)) +
+static size_t workspace_need(int max_rows, long long units, int d) {
+  return host_align256((size_t)max_rows * sizeof(int)) + host_align256(units * sizeof(float2)) +
          host_align256(units * d * sizeof(float));
 }
 
-extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int M,
+extern "C" size_t xenc_decode_workspace_bytes(int max_rows, int kk, int nsplit, int d) {
+  if (max_rows <= 0 || kk <= 0 || nsplit <= 0 || d <= 0) return 0;
+  return workspace_need(max_rows, (long long)max_rows * kk * nsplit, d);
+}
+
+extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int max_rows,
                                           void* stream) {
-  if (M <= 0) return XENC_EINVAL;
+  if (max_rows <= 0) return XENC_EINVAL;
   if (!workspace) return XENC_ENULL;
   if (!aligned16(workspace)) return XENC_EALIGN;
-  if (workspace_bytes < (size_t)M * sizeof(int)) return XENC_EWORKSPACE;
-  const int blocks = std::min((M + 255) / 256, 1024);
+  if (workspace_bytes < (size_t)max_rows * sizeof(int)) return XENC_EWORKSPACE;
+  const int blocks = std::min((max_rows + 255) / 256, 1024);
   hipLaunchKernelGGL(fill_zero_kernel, dim3(blocks), dim3(256), 0,
-                     reinterpret_cast<hipStream_t>(stream), static_cast<int*>(workspace), M);
+                     reinterpret_cast<hipStream_t>(stream), static_cast<int*>(workspace), max_rows);
   return check_launch();
 }
 
@@ -520,8 +526,9 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
                                         const int* q_group, int G, const int* idx,
                                         const float* w_sel, int kk, float read_temp, int softmax,
                                         int nsplit, float* r, long long ldr, void* workspace,
-                                        size_t workspace_bytes, void* stream) {
+                                        size_t workspace_bytes, int max_rows, void* stream) {
   if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || slots_per_page <= 0) return XENC_EINVAL;
+  if (M > max_rows) return XENC_EWORKSPACE;
   if (d % 8 != 0 || d > 8 * 512) return XENC_EINVAL;
   if (nsplit < 1 || nsplit > 64) return XENC_EINVAL;
   if (ldq < d || ldr < d || ldq % 4 != 0 || ldr % 4 != 0) return XENC_EINVAL;
@@ -533,15 +540,15 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
     return XENC_ENULL;
   if (!aligned16(q) || !aligned16(pages) || !aligned16(r) || !aligned16(workspace))
     return XENC_EALIGN;
-  if (workspace_bytes < xenc_decode_workspace_bytes(M, kk, nsplit, d)) return XENC_EWORKSPACE;
   const long long units = (long long)M * kk * nsplit;
   if (units > 0x7fffffffLL) return XENC_EINVAL;
+  if (workspace_bytes < workspace_need(max_rows, units, d)) return XENC_EWORKSPACE;
   // LDS: the wave-merge tree [NW/2][d], or the merge's coefficient list [2 * kk * nsplit].
   const size_t lds =
       std::max((size_t)std::max(XENC_DECODE_NW / 2, 1) * d, (size_t)2 * kk * nsplit) * sizeof(float);
   if (lds > 64 * 1024) return XENC_EINVAL;
 
-  const DecodeWorkspace ws = carve(workspace, M, kk, nsplit);
+  const DecodeWorkspace ws = carve(workspace, max_rows, M, kk, nsplit);
   const int split_slots = (slots_per_page + nsplit - 1) / nsplit;
   const float scale2 = read_temp * kLog2e;
   const _Float16* pg = static_cast<const _Float16*>(pages);

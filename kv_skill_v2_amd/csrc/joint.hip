@@ -1,0 +1,361 @@
+// Op B: the serving-side decode read of a document operator joined with the request's own rows
+// (xenc/d23_read_kernels.py:31-47 is the math, :134-160 the calling contract).
+//
+// For query row n and kv head h with its G query heads (GQA):
+//   keys / values = [ operator pool rows 0 .. op_len[n]-1 (block table op_bt[n])
+//                   ; own pool rows      0 .. own_len[n]-1 (block table own_bt[n]) ]
+//   out[n, h*G + g] = softmax_l(scale * <q[n, h*G+g], K_l>) . V_l       (one softmax over both)
+// Pools are [num_blocks, block_size, Hkv, D] (fp16 or bf16, D contiguous).
+//
+// One launch.  Workgroup (n, h, split s) streams keys [s*chunk, (s+1)*chunk) of the joined range
+// (the last split also takes any keys past nsplit*chunk, so none is ever dropped) and keeps an
+// online max / sum / accumulator per query head in the log2 domain.  A key row of D elements is
+// read by a group of D/8 lanes (16-byte loads; groups padded to a power of two), so a wave reads
+// 64/TPR keys per step; 4 keys per lane group are in flight (block-table lookups first, then the
+// K / V loads).  Lane groups merge by shuffles, the 4 waves through LDS, and wave 0 writes the
+// split's partial.  The last split of (n, h) to arrive (release / acquire on a per-(n, h)
+// counter) merges the partials in split order, so results are deterministic, and re-arms the
+// counter: the workspace is zeroed once and stays valid across calls and graph replays.
+#include <algorithm>
+
+#include "xenc_common.h"
+
+namespace xenc {
+namespace {
+
+constexpr int kJointThreads = 256;
+constexpr int kJointWaves = kJointThreads / kWave;
+constexpr int kKeysInFlight = 4;
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+
+// 8 consecutive elements -> fp32.
+template <typename T> __device__ __forceinline__ void to_f32(const u32x4_t& v, float (&f)[8]);
+template <> __device__ __forceinline__ void to_f32<_Float16>(const u32x4_t& v, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned w = v[i];
+    f[2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w & 0xffffu));
+    f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(w >> 16));
+  }
+}
+template <> __device__ __forceinline__ void to_f32<__bf16>(const u32x4_t& v, float (&f)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned w = v[i];
+    f[2 * i] = __uint_as_float(w << 16);
+    f[2 * i + 1] = __uint_as_float(w & 0xffff0000u);
+  }
+}
+
+struct JointArgs {
+  const void* q; long long s_qn, s_qh;
+  const void* op_k; const void* op_v; long long op_sb, op_ss, op_sh; int op_bs;
+  const int* op_bt; long long op_bts; const int* op_len;
+  const void* own_k; const void* own_v; long long own_sb, own_ss, own_sh; int own_bs;
+  const int* own_bt; long long own_bts; const int* own_len;
+  int hkv, d, tpr, nsplit, chunk;
+  float scale_log2;
+  float* out; long long s_on, s_oh;
+  int* counters; float2* part_ml; float* part_acc;   // [N*Hkv], [N*Hkv][S][G], [N*Hkv][S][G][D]
+};
+
+// Online-softmax merge of state (mo, lo, ao) into (m, l, a); all in the log2 domain.
+__device__ __forceinline__ void lse_merge(float& m, float& l, float (&a)[8], float mo, float lo,
+                                          const float (&ao)[8]) {
+  const float mn = fmaxf(m, mo);
+  const float c0 = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+  const float c1 = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mo - mn);
+  l = l * c0 + lo * c1;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) a[e] = a[e] * c0 + ao[e] * c1;
+  m = mn;
+}
+
+template <typename T, int G>
+__global__ __launch_bounds__(kJointThreads) void joint_read_kernel(JointArgs A) {
+  __shared__ float lds_acc[2][G][512];
+  __shared__ float lds_ml[2][G][2];
+  __shared__ bool is_last_s;
+
+  const int S = A.nsplit;
+  const int s = blockIdx.x % S;
+  const int nh = blockIdx.x / S;
+  const int h = nh % A.hkv;
+  const int n = nh / A.hkv;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int tpr = A.tpr;                 // lanes per key row (power of two, >= D/8)
+  const int lr = lane & (tpr - 1);
+  const int grp = lane / tpr;
+  const int groups = kWave / tpr;        // keys per wave step
+  const int dim0 = lr * 8;
+  const bool active = dim0 < A.d;
+
+  // q of the G heads, pre-scaled into the log2 domain.
+  float qf[G][8];
+  {
+    const T* qb = static_cast<const T*>(A.q) + n * A.s_qn + (long long)h * G * A.s_qh;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      u32x4_t v = active ? *reinterpret_cast<const u32x4_t*>(qb + g * A.s_qh + dim0) : (u32x4_t){};
+      to_f32<T>(v, qf[g]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[g][e] *= A.scale_log2;
+    }
+  }
+  const int lo = A.op_len[n];
+  const int L = lo + A.own_len[n];
+  const int k0 = s * A.chunk;
+  const int k1 = s == S - 1 ? L : min(L, k0 + A.chunk);
+
+  float m[G], l[G], acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[g][e] = 0.f;
+  }
+  const T* opk = static_cast<const T*>(A.op_k);
+  const T* opv = static_cast<const T*>(A.op_v);
+  const T* owk = static_cast<const T*>(A.own_k);
+  const T* owv = static_cast<const T*>(A.own_v);
+  const int* opbt = A.op_bt + n * A.op_bts;
+  const int* owbt = A.own_bt + n * A.own_bts;
+
+  const int step = kJointWaves * groups;              // keys per workgroup step
+  for (int base = k0 + wv * groups + grp; base < k1; base += step * kKeysInFlight) {
+    long long offk[kKeysInFlight];
+    bool own[kKeysInFlight], live[kKeysInFlight];
+#pragma unroll
+    for (int u = 0; u < kKeysInFlight; ++u) {
+      const int key = base + u * step;
+      live[u] = key < k1;
+      own[u] = key >= lo;
+      const int kk = live[u] ? (own[u] ? key - lo : key) : 0;
+      const int bs = own[u] ? A.own_bs : A.op_bs;
+      const int blk = live[u] ? (own[u] ? owbt[kk / bs] : opbt[kk / bs]) : 0;
+      offk[u] = own[u] ? blk * A.own_sb + (kk % bs) * A.own_ss + h * A.own_sh
+                       : blk * A.op_sb + (kk % bs) * A.op_ss + h * A.op_sh;
+    }
+    u32x4_t kv[kKeysInFlight], vv[kKeysInFlight];
+#pragma unroll
+    for (int u = 0; u < kKeysInFlight; ++u) {
+      const bool ld = live[u] && active;
+      const T* kp = (own[u] ? owk : opk) + offk[u] + dim0;
+      const T* vp = (own[u] ? owv : opv) + offk[u] + dim0;
+      kv[u] = ld ? *reinterpret_cast<const u32x4_t*>(kp) : (u32x4_t){};
+      vv[u] = ld ? *reinterpret_cast<const u32x4_t*>(vp) : (u32x4_t){};
+    }
+#pragma unroll
+    for (int u = 0; u < kKeysInFlight; ++u) {
+      float kf[8], vf[8];
+      to_f32<T>(kv[u], kf);
+      to_f32<T>(vv[u], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float sc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sc = fmaf(qf[g][e], kf[e], sc);
+        for (int o = 1; o < tpr; o <<= 1) sc += shfl_xor(sc, o);
+        if (live[u]) {
+          const float mn = fmaxf(m[g], sc);
+          const float c = __builtin_amdgcn_exp2f(m[g] - mn);   // exp2(-inf) = 0 on the first key
+          const float p = __builtin_amdgcn_exp2f(sc - mn);
+          l[g] = l[g] * c + p;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e] * c);
+          m[g] = mn;
+        }
+      }
+    }
+  }
+
+  // Lane groups of a wave hold the same dims for different keys: butterfly merge.
+  for (int o = tpr; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float ao[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ao[e] = shfl_xor(acc[g][e], o);
+      const float mo = shfl_xor(m[g], o), lo2 = shfl_xor(l[g], o);
+      lse_merge(m[g], l[g], acc[g], mo, lo2, ao);
+    }
+  }
+  // Waves 2,3 -> 0,1, then 1 -> 0, through LDS (group 0 lanes carry the wave's state).
+  for (int half = kJointWaves / 2; half >= 1; half >>= 1) {
+    if (wv >= half && wv < 2 * half && grp == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        if (active) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) lds_acc[wv - half][g][dim0 + e] = acc[g][e];
+        }
+        if (lr == 0) {
+          lds_ml[wv - half][g][0] = m[g];
+          lds_ml[wv - half][g][1] = l[g];
+        }
+      }
+    }
+    __syncthreads();
+    if (wv < half && grp == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float ao[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ao[e] = active ? lds_acc[wv][g][dim0 + e] : 0.f;
+        lse_merge(m[g], l[g], acc[g], lds_ml[wv][g][0], lds_ml[wv][g][1], ao);
+      }
+    }
+    __syncthreads();
+  }
+  // Wave 0 (group 0) writes the split's partial.
+  const long long part = (long long)nh * S + s;
+  if (wv == 0 && grp == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (lr == 0) A.part_ml[part * G + g] = make_float2(m[g], l[g]);
+      if (active) {
+        float* dst = A.part_acc + (part * G + g) * A.d + dim0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[e] = acc[g][e];
+      }
+    }
+  }
+  // Publish; the last split of (n, h) to arrive merges.
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int prev = __hip_atomic_fetch_add(&A.counters[nh], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == S - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    is_last_s = last;
+  }
+  __syncthreads();
+  if (!is_last_s) return;
+  const long long p0 = (long long)nh * S;
+  for (int i = threadIdx.x; i < G * A.d; i += kJointThreads) {
+    const int g = i / A.d, dd = i % A.d;
+    float M = -INFINITY;
+    for (int j = 0; j < S; ++j) {
+      const float2 ml = A.part_ml[(p0 + j) * G + g];
+      if (ml.y > 0.f) M = fmaxf(M, ml.x);
+    }
+    float num = 0.f, den = 0.f;
+    for (int j = 0; j < S; ++j) {
+      const float2 ml = A.part_ml[(p0 + j) * G + g];
+      if (ml.y > 0.f) {
+        const float c = __builtin_amdgcn_exp2f(ml.x - M);
+        den += c * ml.y;
+        num += c * A.part_acc[((p0 + j) * G + g) * A.d + dd];
+      }
+    }
+    A.out[n * A.s_on + (long long)(h * G + g) * A.s_oh + dd] = den > 0.f ? num / den : 0.f;
+  }
+  if (threadIdx.x == 0) atomicExch(&A.counters[nh], 0);
+}
+
+__global__ void joint_zero_kernel(int* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+struct JointLayout {
+  size_t counters, ml, acc, total;
+};
+
+// [counters: max_n*Hkv ints | (m, l) per (n, h, split, head) | acc per (n, h, split, head, dim)].
+// The counter region depends only on the capacity max_n, so counters zeroed once stay in place
+// whatever row counts later calls use.
+JointLayout joint_layout(int max_n, int N, int hkv, int nsplit, int g, int d) {
+  JointLayout L;
+  const size_t units = (size_t)N * hkv;
+  L.counters = 0;
+  L.ml = align256((size_t)max_n * hkv * sizeof(int));
+  L.acc = align256(L.ml + units * nsplit * g * sizeof(float2));
+  L.total = align256(L.acc + units * nsplit * g * (size_t)d * sizeof(float));
+  return L;
+}
+
+template <typename T>
+int launch_joint(int G, dim3 grid, hipStream_t st, const JointArgs& a) {
+  switch (G) {
+    case 1: hipLaunchKernelGGL((joint_read_kernel<T, 1>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((joint_read_kernel<T, 2>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((joint_read_kernel<T, 3>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((joint_read_kernel<T, 4>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((joint_read_kernel<T, 5>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((joint_read_kernel<T, 6>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((joint_read_kernel<T, 7>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 8: hipLaunchKernelGGL((joint_read_kernel<T, 8>), grid, dim3(kJointThreads), 0, st, a); break;
+    default: return XENC_EINVAL;
+  }
+  return check_launch();
+}
+
+}  // namespace
+}  // namespace xenc
+
+using namespace xenc;
+
+extern "C" size_t xenc_joint_workspace_bytes(int max_n, int hkv, int nsplit, int g, int d) {
+  if (max_n < 0 || hkv <= 0 || nsplit <= 0 || g <= 0 || d <= 0) return 0;
+  return joint_layout(max_n, max_n, hkv, nsplit, g, d).total;
+}
+
+extern "C" int xenc_joint_workspace_init(void* workspace, size_t workspace_bytes, int max_n, int hkv,
+                                         void* stream) {
+  if (max_n < 0 || hkv <= 0) return XENC_EINVAL;
+  const long long n = (long long)max_n * hkv;
+  if (n == 0) return XENC_OK;
+  if (!workspace) return XENC_ENULL;
+  if (workspace_bytes < (size_t)n * sizeof(int)) return XENC_EWORKSPACE;
+  const int blocks = (int)std::min<long long>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(joint_zero_kernel, dim3(blocks), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), static_cast<int*>(workspace), (int)n);
+  return check_launch();
+}
+
+extern "C" int xenc_paged_decode_joint(
+    int dtype, int N, int hq, int hkv, int d,
+    const void* q, long long s_qn, long long s_qh,
+    const void* op_k, const void* op_v, long long op_sb, long long op_ss, long long op_sh, int op_bs,
+    const int* op_bt, long long op_bt_stride, const int* op_len,
+    const void* own_k, const void* own_v, long long own_sb, long long own_ss, long long own_sh,
+    int own_bs, const int* own_bt, long long own_bt_stride, const int* own_len,
+    float scale, int nsplit, int chunk, float* out, long long s_on, long long s_oh,
+    void* workspace, size_t workspace_bytes, int max_n, void* stream) {
+  if (dtype != 0 && dtype != 1) return XENC_EINVAL;
+  if (N < 0 || hq <= 0 || hkv <= 0 || hq % hkv != 0) return XENC_EINVAL;
+  if (N > max_n) return XENC_EWORKSPACE;
+  const int G = hq / hkv;
+  if (G > 8 || d <= 0 || d % 8 != 0 || d > 512 || G * d > 4096) return XENC_EINVAL;
+  if (nsplit <= 0 || nsplit > 4096 || chunk <= 0 || op_bs <= 0 || own_bs <= 0) return XENC_EINVAL;
+  if (s_qh < d || s_qn < (long long)hq * s_qh || s_oh < d || s_on < (long long)hq * s_oh) return XENC_EINVAL;
+  for (long long st : {s_qn, s_qh, op_sb, op_ss, op_sh, own_sb, own_ss, own_sh})
+    if (st % 8 != 0 || st < 0) return XENC_EALIGN;
+  if (N == 0) return XENC_OK;
+  if (!q || !op_k || !op_v || !op_bt || !op_len || !own_k || !own_v || !own_bt || !own_len ||
+      !out || !workspace)
+    return XENC_ENULL;
+  for (const void* p : {q, op_k, op_v, own_k, own_v, (const void*)out, (const void*)workspace})
+    if (!aligned16(p)) return XENC_EALIGN;
+  const JointLayout lay = joint_layout(max_n, N, hkv, nsplit, G, d);
+  if (workspace_bytes < lay.total) return XENC_EWORKSPACE;
+  int tpr = 1;
+  while (tpr * 8 < d) tpr <<= 1;
+  char* ws = static_cast<char*>(workspace);
+  JointArgs a{q, s_qn, s_qh, op_k, op_v, op_sb, op_ss, op_sh, op_bs, op_bt, op_bt_stride, op_len,
+              own_k, own_v, own_sb, own_ss, own_sh, own_bs, own_bt, own_bt_stride, own_len,
+              hkv, d, tpr, nsplit, chunk, scale * kLog2e, out, s_on, s_oh,
+              reinterpret_cast<int*>(ws + lay.counters), reinterpret_cast<float2*>(ws + lay.ml),
+              reinterpret_cast<float*>(ws + lay.acc)};
+  const long long blocks = (long long)N * hkv * nsplit;
+  if (blocks > 0x7fffffffLL) return XENC_EINVAL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  return dtype == 0 ? launch_joint<_Float16>(G, dim3((unsigned)blocks), st, a)
+                    : launch_joint<__bf16>(G, dim3((unsigned)blocks), st, a);
+}

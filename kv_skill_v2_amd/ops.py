@@ -246,23 +246,26 @@ def default_nsplit(units: int, slots_per_page: int) -> int:
 
 
 class _Workspaces:
-    """Decode workspaces, one per (device, stream), grown on demand.  Its arrival counters are
-    zeroed once by a kernel (xenc_decode_workspace_init) and every call leaves them zero."""
+    """Decode workspaces, one per (device, stream), grown on demand.  A workspace serves calls of
+    up to `rows` query rows (its capacity, passed to every call); its arrival counters are zeroed
+    once by a kernel (xenc_decode_workspace_init) and every call leaves them zero."""
 
     def __init__(self):
         self._ws = {}
 
-    def get(self, device: torch.device, stream: int, nbytes: int, M: int) -> torch.Tensor:
+    def get(self, device: torch.device, stream: int, M: int, kk: int, nsplit: int, d: int):
         key = (device.index, stream)
-        buf, zeroed = self._ws.get(key, (None, 0))
-        if buf is None or buf.numel() < nbytes or zeroed < M:
-            size = max(nbytes, buf.numel() if buf is not None else 0)
+        buf, rows = self._ws.get(key, (None, 0))
+        L = lib()
+        if buf is None or rows < M or buf.numel() < L.xenc_decode_workspace_bytes(rows, kk, nsplit, d):
+            rows = max(rows, M, 64)
+            size = L.xenc_decode_workspace_bytes(rows, kk, nsplit, d)
+            if buf is not None:
+                size = max(size, buf.numel())
             buf = torch.empty(size, dtype=torch.uint8, device=device)
-            zeroed = max(M, zeroed)
-            check(lib().xenc_decode_workspace_init(ptr(buf), size, zeroed, stream),
-                  "xenc_decode_workspace_init")
-            self._ws[key] = (buf, zeroed)
-        return buf
+            check(L.xenc_decode_workspace_init(ptr(buf), size, rows, stream), "xenc_decode_workspace_init")
+            self._ws[key] = (buf, rows)
+        return buf, rows
 
 
 _WORKSPACES = _Workspaces()
@@ -292,14 +295,13 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
         return r.zero_()
     ns = int(nsplit) if nsplit is not None else default_nsplit(M * kk, lib_.slots_per_page)
     L = lib()
-    wsb = L.xenc_decode_workspace_bytes(M, kk, ns, lib_.d)
     st = stream_handle(q.device)
-    ws = _WORKSPACES.get(q.device, st, wsb, M)
+    ws, rows = _WORKSPACES.get(q.device, st, M, kk, ns, lib_.d)
     rc = L.xenc_library_read_decode(
         ptr(q), q.stride(0), M, lib_.d, ptr(lib_.pages), lib_.slots_per_page,
         lib_.pages.stride(0), ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), ptr(lib_.chunk_ptr),
         ptr(g), lib_.n_libraries, ptr(idx), ptr(w_sel), kk, float(read_temp), int(bool(softmax)),
-        ns, ptr(r), r.stride(0), ptr(ws), ws.numel(), st)
+        ns, ptr(r), r.stride(0), ptr(ws), ws.numel(), rows, st)
     check(rc, "xenc_library_read_decode")
     return r
 

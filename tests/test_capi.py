@@ -53,7 +53,25 @@ def test_host_side_validation_rejects_bad_sizes():
     # NULL pointers with valid sizes
     assert L.xenc_route_topk(None, 16, 1, 16, None, None, None, 1, 2, 10.0, None, 4, None, None, 2, None) == -2
     assert L.xenc_library_read_decode(None, 16, 1, 16, None, 4, 64, None, None, None, None, 1, None, None, 2,
-                                      12.0, 1, 1, None, 16, None, 0, None) == -2
+                                      12.0, 1, 1, None, 16, None, 0, 1, None) == -2
     # nsplit out of range
     assert L.xenc_library_read_decode(None, 16, 1, 16, None, 4, 64, None, None, None, None, 1, None, None, 2,
-                                      12.0, 1, 65, None, 16, None, 0, None) == -1
+                                      12.0, 1, 65, None, 16, None, 0, 1, None) == -1
+    # more rows than the workspace capacity
+    assert L.xenc_library_read_decode(None, 16, 2, 16, None, 4, 64, None, None, None, None, 1, None, None, 2,
+                                      12.0, 1, 1, None, 16, None, 0, 1, None) == -4
+    # op B: G = hq / hkv above 8, d not a multiple of 8, NULL pointers, N above the capacity
+    args = dict(dtype=1, N=1, hq=16, hkv=4, d=64)
+
+    def joint(**kw):
+        a = {**args, **kw}
+        return L.xenc_paged_decode_joint(a["dtype"], a["N"], a["hq"], a["hkv"], a["d"], None, 16 * 64, 64,
+                                         None, None, 64 * 4 * 16, 64 * 4, 64, 16, None, 8, None,
+                                         None, None, 64 * 4 * 16, 64 * 4, 64, 16, None, 8, None,
+                                         0.125, 2, 512, None, 16 * 64, 64, None, 0, a.get("max_n", 4), None)
+    assert joint(hq=36, hkv=4) == -1
+    assert joint(d=60) == -1
+    assert joint(dtype=2) == -1
+    assert joint() == -2
+    assert joint(N=5) == -4
+    assert L.xenc_joint_workspace_bytes(4, 4, 2, 4, 64) >= 4 * 4 * 2 * 4 * 64 * 4
