@@ -85,52 +85,85 @@ struct DecodeWorkspace {
 };
 
 // Merge the k*nsplit partials of query m into r[m] (run by the last workgroup of the query).
+// LDS: [m | l | coefficient | unit] per partial (4 * nu words).  Every step is parallel over the
+// partials; the value sum runs over the live partials in (chunk, split) order with 8 loads in
+// flight, so the result is independent of arrival order.
 __device__ void merge_query(const DecodeWorkspace& ws, int m, const int* __restrict__ idx,
                             const float* __restrict__ w_sel, int kk, int nsplit, int d, int softmax,
                             float* __restrict__ r, long long ldr, float* lds) {
   const int nu = kk * nsplit;
-  float* coef = lds;                                  // [nu]
-  int* unit_of = reinterpret_cast<int*>(lds + nu);    // [nu]
+  float* pm = lds;                                        // [nu] partial max (log2 units)
+  float* pl = lds + nu;                                   // [nu] partial sum (0 = empty)
+  float* coef = lds + 2 * nu;                             // [nu] -> compacted coefficients
+  int* unit_of = reinterpret_cast<int*>(lds + 3 * nu);    // [nu] -> compacted partial ids
   __shared__ int nlive;
   const long long ubase = (long long)m * nu;
-  for (int j = threadIdx.x; j < kk; j += blockDim.x) {
-    const float wj = w_sel[(long long)m * kk + j];
-    const bool live = idx[(long long)m * kk + j] >= 0;
-    float mj = -INFINITY, lj = 0.f;
-    if (live && softmax) {
-      for (int s = 0; s < nsplit; ++s) {
-        const float2 ml = ws.part_ml[ubase + (long long)j * nsplit + s];
-        if (ml.y > 0.f) mj = fmaxf(mj, ml.x);
-      }
-      for (int s = 0; s < nsplit; ++s) {
-        const float2 ml = ws.part_ml[ubase + (long long)j * nsplit + s];
-        if (ml.y > 0.f) lj += ml.y * __builtin_amdgcn_exp2f(ml.x - mj);
-      }
-    }
-    for (int s = 0; s < nsplit; ++s) {
-      const float2 ml = ws.part_ml[ubase + (long long)j * nsplit + s];
-      float c = 0.f;
-      if (live && ml.y > 0.f) c = softmax ? wj * __builtin_amdgcn_exp2f(ml.x - mj) / lj : wj;
-      coef[j * nsplit + s] = c;
-    }
+  for (int u = threadIdx.x; u < nu; u += blockDim.x) {
+    const float2 ml = ws.part_ml[ubase + u];
+    pm[u] = ml.y > 0.f ? ml.x : -INFINITY;
+    pl[u] = ml.y;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {  // compact the live partials, keeping (j, s) order
-    int n = 0;
-    for (int u = 0; u < nu; ++u) {
-      if (coef[u] != 0.f) {
-        coef[n] = coef[u];
-        unit_of[n] = u;
-        ++n;
+  // Coefficient of partial u = (j, s): w_j * 2^(m_s - M_j) / l_j (softmax) or w_j (linear).
+  for (int u = threadIdx.x; u < nu; u += blockDim.x) {
+    const int j = u / nsplit;
+    float c = 0.f;
+    if (idx[(long long)m * kk + j] >= 0 && pl[u] > 0.f) {
+      const float wj = w_sel[(long long)m * kk + j];
+      if (softmax) {
+        float mj = -INFINITY, lj = 0.f;
+        for (int t = 0; t < nsplit; ++t) mj = fmaxf(mj, pm[j * nsplit + t]);
+        for (int t = 0; t < nsplit; ++t) {
+          const float lt = pl[j * nsplit + t];
+          if (lt > 0.f) lj += lt * __builtin_amdgcn_exp2f(pm[j * nsplit + t] - mj);
+        }
+        c = wj * __builtin_amdgcn_exp2f(pm[u] - mj) / lj;
+      } else {
+        c = wj;
       }
     }
-    nlive = n;
+    coef[u] = c;
+  }
+  __syncthreads();
+  if (threadIdx.x < kWave) {                             // wave 0: ordered ballot compaction
+    int n = 0;
+    for (int base = 0; base < nu; base += kWave) {
+      const int u = base + (int)threadIdx.x;
+      const float c = u < nu ? coef[u] : 0.f;
+      const bool live = c != 0.f;
+      const unsigned long long mask = __ballot(live);
+      const int pos = n + __popcll(mask & ((1ull << threadIdx.x) - 1ull));
+      __builtin_amdgcn_wave_barrier();
+      if (live) {
+        coef[pos] = c;       // pos <= u: never overwrites an entry a later step still reads
+        unit_of[pos] = u;
+      }
+      __builtin_amdgcn_wave_barrier();
+      n += __popcll(mask);
+    }
+    if (threadIdx.x == 0) nlive = n;
   }
   __syncthreads();
   const int n = nlive;
+  constexpr int kInFlight = 8;
   for (int i = threadIdx.x * 4; i < d; i += blockDim.x * 4) {
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int t = 0; t < n; ++t) {
+    int t = 0;
+    for (; t + kInFlight <= n; t += kInFlight) {
+      float4 a[kInFlight];
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k)
+        a[k] = *reinterpret_cast<const float4*>(ws.part_acc + (ubase + unit_of[t + k]) * d + i);
+#pragma unroll
+      for (int k = 0; k < kInFlight; ++k) {
+        const float c = coef[t + k];
+        o.x = fmaf(c, a[k].x, o.x);
+        o.y = fmaf(c, a[k].y, o.y);
+        o.z = fmaf(c, a[k].z, o.z);
+        o.w = fmaf(c, a[k].w, o.w);
+      }
+    }
+    for (; t < n; ++t) {
       const float c = coef[t];
       const float4 a = *reinterpret_cast<const float4*>(ws.part_acc + (ubase + unit_of[t]) * d + i);
       o.x = fmaf(c, a.x, o.x);
@@ -543,9 +576,9 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
   const long long units = (long long)M * kk * nsplit;
   if (units > 0x7fffffffLL) return XENC_EINVAL;
   if (workspace_bytes < workspace_need(max_rows, units, d)) return XENC_EWORKSPACE;
-  // LDS: the wave-merge tree [NW/2][d], or the merge's coefficient list [2 * kk * nsplit].
+  // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
   const size_t lds =
-      std::max((size_t)std::max(XENC_DECODE_NW / 2, 1) * d, (size_t)2 * kk * nsplit) * sizeof(float);
+      std::max((size_t)std::max(XENC_DECODE_NW / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
   if (lds > 64 * 1024) return XENC_EINVAL;
 
   const DecodeWorkspace ws = carve(workspace, max_rows, M, kk, nsplit);
