@@ -13,6 +13,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import statistics
@@ -31,7 +32,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="batched_paged_decode",
-                    choices=["batched_paged_decode", "single_decode", "prefill"])
+                    choices=["batched_paged_decode", "single_decode", "prefill", "multi_depth"])
     ap.add_argument("--nsplit", type=int, default=None)
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -191,6 +192,112 @@ def bench_prefill(args):
     print(json.dumps(out), flush=True)
 
 
+def bench_multi_depth(args):
+    """Multi-depth selector decode: 8 depth Libraries (64 x 512 slots, d_s = 2560) shared by a batch
+    of 32 tokens; the selector keeps the top-2 depths per token (seeded logits), so 64 (token,
+    depth) query rows are routed (top-8 chunks of their depth) and read in ONE route and ONE read
+    launch (the depth is the row's library).  Each read is written back through its depth's
+    B [5120, 2560] fp32 (one padded batched GEMM reads every B once), times gate and gain, then
+    rescaled to the selector's matched norm and weighted.  The unselected depths are not read (the
+    reference reads all 8 and multiplies 6 by zero).  Step = everything after the selector logits;
+    the two updates of a token (one per selected depth, applied at different layers in a model)
+    are summed into one [32, 5120] output here.  Algorithmic bytes: the unique routed pages of each
+    depth (union over the batch) x valid slots x d x 2, the S of the 8 Libraries, every B read,
+    and the activations."""
+    from kv_skill_v2_amd import ops, synth
+    from kv_skill_v2_amd.selector import LayerSelector, rms_norm
+
+    c = synth.MULTI_DEPTH
+    dev = torch.device("cuda:0")
+    P, z, q_all, h, BwT = synth.multi_depth_workload(dev)
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    B, L, d, dr, k = c["B"], c["depths"], c["d"], c["d_r"], c["top_k"]
+    sel = LayerSelector(dr, list(range(L)), k=c["k_sel"]).to(dev)
+    gate_w = torch.zeros(dr, device=dev)
+    gate_b = torch.full((L,), -2.0, device=dev)
+    log_gain = torch.zeros(L, device=dev)
+    bidx = torch.arange(B, device=dev).repeat_interleave(c["k_sel"])
+    hn = rms_norm(h)
+
+    def step():
+        with torch.no_grad():
+            wsl = sel._weights_from_logits(z)                         # [B, 8], 2 nonzeros per row
+            top = z.topk(c["k_sel"], dim=-1).indices                  # the selected depths
+            qg = top.reshape(-1).to(torch.int32)
+            ql = qg.long()
+            qr = q_all[ql, bidx]                                      # [64, d]
+            _, idx, wsel = ops.route_topk(qr, lib, qg, top_k=k)
+            r = ops.library_read_decode(qr, lib, idx, wsel, qg)
+            rp = torch.zeros(L, B, d, device=dev)
+            rp[ql, bidx] = r
+            dl = torch.bmm(rp, BwT)[ql, bidx]                         # [64, d_r]
+            g = torch.sigmoid(hn[bidx] @ gate_w + gate_b[ql]).unsqueeze(-1)
+            dl = torch.exp(log_gain[ql]).unsqueeze(-1) * g * dl
+            hb = h[bidx]
+            rel = dl.norm(dim=-1, keepdim=True) / (hb.norm(dim=-1, keepdim=True) + 1e-6)
+            dl = dl / (rel + 1e-6) * sel.log_alpha.exp() * wsl[bidx, ql].unsqueeze(-1)
+            return torch.zeros(B, dr, device=dev).index_add_(0, bidx, dl), idx, qg
+
+    _, idx0, qg0 = step()
+    torch.cuda.synchronize()
+    pages = set()
+    ptr_h = P.chunk_ptr.cpu().tolist()
+    for row, (g, cs) in enumerate(zip(qg0.cpu().tolist(), idx0.cpu().tolist())):
+        pages.update((g, ch) for ch in cs if ch >= 0)
+    page_bytes = sum(P.nvalid[ptr_h[g] + ch] for g, ch in pages) * d * 2
+    used = len(set(qg0.cpu().tolist()))
+    bytes_step = (page_bytes + L * c["chunks"] * d * 4 + used * d * dr * 4
+                  + 2 * B * c["k_sel"] * (d + dr) * 4 + B * dr * 4 * 2)
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    achieved = bytes_step / (ms_step * 1e-3) / 1e9
+
+    cpu = None
+    if args.cpu_sample > 0:
+        import oracle as O
+        torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+        K, M, S = P.library(0)
+        K, M, S = K.cpu(), M.cpu(), S.cpu()
+        ql0 = q_all[0].cpu().view(B, 1, d)
+        Bw0 = BwT[0].cpu().t().contiguous()
+        hc = h.cpu().view(B, 1, dr)
+        O.branch_read(ql0[:1], K, M, S, top_k=k)                       # warm-up
+        t0 = time.perf_counter()
+        r0, _ = O.branch_read(ql0, K, M, S, top_k=k)
+        dl0 = O.epilogue(O.rms_norm(hc), r0, Bw0, None, gate_w.cpu(), gate_b[0].cpu(), log_gain[0].cpu())
+        O.selector_apply(dl0, hc, torch.ones(B, 1), math.log(0.02))
+        t_layer = time.perf_counter() - t0
+        cpu = {"value": B / (L * t_layer), "unit": "query tokens/s", "cores": torch.get_num_threads(),
+               "kind": "port",
+               "sample": (f"1 of the {L} depth layers the reference reads per token (all 64 chunks, fp32, "
+                          f"route + read + B write-back + selector rescale for the batch of {B}), "
+                          f"{t_layer:.2f} s, scaled by {L}; CPU oracle on {cpu_model()}, "
+                          f"os.cpu_count()={os.cpu_count()}")}
+    out = {
+        "metric": "Multi-depth selector decode query tokens/sec + achieved HBM GB/s (% peak)",
+        "value": B / (ms_step * 1e-3), "unit": "query tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "multi_depth", "depths": L, "chunks_per_depth": c["chunks"],
+                   "slots_per_page": c["N"], "d_s": d, "d_reader": dr, "batch": B,
+                   "selector_top_k": c["k_sel"], "top_k": k, "B_dtype": "fp32", "accumulate": "fp32"},
+        "roofline": {"bound": "hbm", "kernel": "whole step (route + read + B GEMM + epilogue)",
+                     "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": bytes_step, "unique_routed_pages": len(pages),
+                     "routed_page_reads": int((idx0 >= 0).sum()), "depths_used": used},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -202,6 +309,8 @@ def main():
         sys.exit(2)
     if args.workload == "prefill":
         return bench_prefill(args)
+    if args.workload == "multi_depth":
+        return bench_multi_depth(args)
     from kv_skill_v2_amd import ops, synth
 
     dev = torch.device("cuda:0")

@@ -113,6 +113,25 @@ WORKLOADS = {
 }
 
 
+# C5: 8 candidate depths, each a Library of 64 x 512 slots (d_s = 2560) shared by the batch of 32
+# tokens; a selector keeps the top-2 depths per token (seeded logits), routing keeps top-8 chunks
+# per selected depth, and each read is written back through that depth's B [5120, 2560] (fp32).
+MULTI_DEPTH = dict(depths=8, chunks=64, N=512, d=2560, B=32, k_sel=2, top_k=8, d_r=5120)
+
+
+def multi_depth_workload(device="cuda"):
+    """(SynthPool of the 8 depth Libraries, selector logits z [B, 8] (seed 5), queries
+    q_all [8, B, d] (seed 2), hidden states h [B, d_r] and B_w^T [8, d, d_r] ~ N(0, 1/d) (seed 6))."""
+    c = MULTI_DEPTH
+    P = pool([c["chunks"]] * c["depths"], c["N"], c["d"], device=device)
+    z = torch.randn(c["B"], c["depths"], generator=_gen(5, "cpu")).to(device)
+    q_all = queries(c["depths"] * c["B"], c["d"], device=device).view(c["depths"], c["B"], c["d"])
+    g6 = _gen(6, device)
+    h = torch.randn(c["B"], c["d_r"], generator=g6, device=device)
+    BwT = torch.randn(c["depths"], c["d"], c["d_r"], generator=g6, device=device) / c["d"] ** 0.5
+    return P, z, q_all, h, BwT
+
+
 def decode_workload(name: str, device="cuda", **over):
     """(SynthPool, q [B, d], q_group [B], top_k) for a named decode workload."""
     cfg = {**WORKLOADS[name], **over}
@@ -125,4 +144,4 @@ def decode_workload(name: str, device="cuda", **over):
 
 
 __all__ = ["SynthPool", "pool", "queries", "unit_rows_fp16", "masked_summaries", "batched_chunk_counts",
-           "decode_workload", "WORKLOADS"]
+           "decode_workload", "WORKLOADS", "MULTI_DEPTH", "multi_depth_workload"]
