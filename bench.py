@@ -125,7 +125,7 @@ def bench_prefill(args):
     frag_ms = (time.perf_counter() - t0) * 1e3
 
     def fwd():
-        w, _, _ = ops.route_topk(q, lib, qg, top_k=0)
+        w, _, _ = ops.route_topk_rows(q, lib, plan, top_k=0)
         r, p = ops.prefill_forward(q, w, lib, plan)
         return w, r, p
 

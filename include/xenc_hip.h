@@ -61,6 +61,18 @@ int xenc_route_topk(const float* q, long long ldq, int M, int d,
                     void* stream);
 
 /*
+ * Routing of many query rows grouped by library (prefill / registration): rows of library g are
+ * row_ptr[g] .. row_ptr[g+1]-1; tile_ptr[g] = sum_{g'<g} ceil(T_g'/32) * ceil(C_g'/32) (G+1
+ * entries, n_tiles = tile_ptr[G]).  Same outputs and top-k / softmax as xenc_route_topk; the dots
+ * are computed as 32-row x 32-chunk fp32 tiles (each summary row read once per 32 query rows).
+ * ldw <= 1365.  Replaces LibraryInjector.route (xenc/injector.py:220-229) for many tokens.
+ */
+int xenc_route_topk_rows(const float* q, long long ldq, int M, int d, const float* S,
+                         const int* chunk_ptr, const int* row_ptr, const int* tile_ptr, int G,
+                         int n_tiles, int top_k, float route_temp, float* w_dense, long long ldw,
+                         int* idx, float* w_sel, int kk, void* stream);
+
+/*
  * Decode read over routed pages (split-K over slots, log-sum-exp merge):
  *   softmax=1: r[m] = sum_j w_sel[m,j] * sum_n softmax_n(read_temp*<q,K[c_j,n]>) K[c_j,n]
  *   softmax=0: r[m] = sum_j w_sel[m,j] * sum_n <q,K[c_j,n]>/sqrt(n_valid) K[c_j,n]  (linear read)

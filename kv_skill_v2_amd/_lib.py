@@ -31,6 +31,11 @@ SIGNATURES = {
         c_int, c_float,                              # top_k, route_temp
         c_void_p, c_longlong, c_void_p, c_void_p, c_int,  # w_dense, ldw, idx, w_sel, kk
         c_void_p]),                                  # stream
+    "xenc_route_topk_rows": (c_int, [
+        c_void_p, c_longlong, c_int, c_int, c_void_p,  # q, ldq, M, d, S
+        c_void_p, c_void_p, c_void_p, c_int, c_int,  # chunk_ptr, row_ptr, tile_ptr, G, n_tiles
+        c_int, c_float, c_void_p, c_longlong,        # top_k, route_temp, w_dense, ldw
+        c_void_p, c_void_p, c_int, c_void_p]),       # idx, w_sel, kk, stream
     "xenc_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "xenc_decode_workspace_init": (c_int, [c_void_p, c_size_t, c_int, c_void_p]),
     "xenc_library_read_decode": (c_int, [

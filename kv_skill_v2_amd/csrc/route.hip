@@ -16,6 +16,72 @@
 
 namespace xenc {
 
+// Wave-level top-k (ties -> lower chunk index) and softmax over the kept logits
+// (logit = dot * route_temp, scaled before the softmax as the reference does).  dots[0..C) hold
+// the raw dot products; taken / order are scratch of C entries.  Writes the kept weights into
+// wrow (which the caller has zeroed), and idx / w_sel rows (-1 / 0 past the kept count).
+__device__ void select_topk_softmax(const float* dots, int* taken, int* order, int C, int top_k,
+                                    int kk, float route_temp, float* wrow, int* irow, float* selrow,
+                                    int lane) {
+  const bool dense = top_k <= 0 || top_k >= C;
+  const int nsel = min(dense ? C : top_k, kk);
+  if (dense) {
+    for (int r = lane; r < nsel; r += kWave) order[r] = r;
+  } else {
+    for (int c = lane; c < C; c += kWave) taken[c] = 0;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    for (int r = 0; r < nsel; ++r) {
+      float bv = -INFINITY;
+      int bc = 0x7fffffff;
+      for (int c = lane; c < C; c += kWave) {
+        if (!taken[c]) {
+          const float v = dots[c];
+          if (bc == 0x7fffffff || ranks_before(v, c, bv, bc)) {
+            bv = v;
+            bc = c;
+          }
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = shfl_xor(bv, o);
+        const int oc = shfl_xor(bc, o);
+        if (oc != 0x7fffffff && (bc == 0x7fffffff || ranks_before(ov, oc, bv, bc))) {
+          bv = ov;
+          bc = oc;
+        }
+      }
+      // bc is the same in every lane; C >= 1 guarantees a candidate exists for r < C.
+      if (lane == 0) {
+        taken[bc] = 1;
+        order[r] = bc;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+
+  float lmax = -INFINITY;
+  for (int r = lane; r < nsel; r += kWave) lmax = fmaxf(lmax, dots[order[r]] * route_temp);
+  lmax = wave_max(lmax);
+  float part = 0.f;
+  for (int r = lane; r < nsel; r += kWave) part += expf(dots[order[r]] * route_temp - lmax);
+  const float inv = 1.f / wave_sum(part);
+  for (int r = lane; r < nsel; r += kWave) {
+    const int c = order[r];
+    const float wr = expf(dots[c] * route_temp - lmax) * inv;
+    irow[r] = c;
+    selrow[r] = wr;
+    wrow[c] = wr;
+  }
+  for (int r = nsel + lane; r < kk; r += kWave) {
+    irow[r] = -1;
+    selrow[r] = 0.f;
+  }
+}
+
 template <int CB4, int CPI, int NW>
 __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
     const float* __restrict__ q, long long ldq, int d, const float* __restrict__ S,
@@ -69,74 +135,144 @@ __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
     for (int u = 0; u < CPI; ++u) {
       const float a = wave_sum(acc[u]);
       const int c = cbase + u * NW;
-      if (lane == 0 && c < C) {
-        dots[c] = a;
-        taken[c] = 0;
-      }
+      if (lane == 0 && c < C) dots[c] = a;
     }
   }
   float* wrow = w_dense + (long long)m * ldw;
   for (int c = threadIdx.x; c < ldw; c += NW * kWave) wrow[c] = 0.f;
   __syncthreads();
   if (wv != 0) return;
+  select_topk_softmax(dots, taken, order, C, top_k, kk, route_temp, wrow, idx + (long long)m * kk,
+                      w_sel + (long long)m * kk, lane);
+}
 
-  const bool dense = top_k <= 0 || top_k >= C;
-  const int nsel = min(dense ? C : top_k, kk);
-  if (dense) {
-    for (int r = lane; r < nsel; r += kWave) order[r] = r;
-  } else {
-    for (int r = 0; r < nsel; ++r) {
-      float bv = -INFINITY;
-      int bc = 0x7fffffff;
-      for (int c = lane; c < C; c += kWave) {
-        if (!taken[c]) {
-          const float v = dots[c];
-          if (bc == 0x7fffffff || ranks_before(v, c, bv, bc)) {
-            bv = v;
-            bc = c;
-          }
-        }
-      }
+
+// ------------------------------------------------------------------------------------------
+// Routing of many query rows (prefill / registration): rows are grouped by library and the
+// q . S dots of a 32-row x 32-chunk tile are one fp32 register-blocked GEMM tile (each summary
+// row is read once per 32 query rows instead of once per row).  Thread (tr, tc) of 256 owns rows
+// tr, tr + 16 and chunks tc, tc + 16; k steps of 128 through LDS (row stride 132 floats), the
+// next step's global loads in flight while the current step computes.  The raw dots land in
+// w_dense; route_rows_select_kernel then runs the same wave top-k + softmax as the per-row
+// kernel, one wave per row.  Fixed summation order per (row, chunk).
+constexpr int kRouteRows = 32, kRouteChunks = 32, kRouteK = 128, kRouteLd = kRouteK + 4;
+constexpr int kRouteLoads = kRouteRows * kRouteK / 4 / 256;   // float4 per thread per operand
+
+__device__ __forceinline__ int find_tile_group(const int* __restrict__ tile_ptr, int G, int b) {
+  int lo = 0, hi = G - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (tile_ptr[mid] <= b) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__global__ __launch_bounds__(256) void route_rows_logits_kernel(
+    const float* __restrict__ q, long long ldq, int d, const float* __restrict__ S,
+    const int* __restrict__ chunk_ptr, const int* __restrict__ row_ptr,
+    const int* __restrict__ tile_ptr, int G, float* __restrict__ w_dense, long long ldw) {
+  __shared__ float qs[kRouteRows * kRouteLd];
+  __shared__ float ss[kRouteChunks * kRouteLd];
+  const int b = blockIdx.x;
+  const int g = find_tile_group(tile_ptr, G, b);
+  const int rbeg = row_ptr[g], rend = row_ptr[g + 1];
+  const int c0 = chunk_ptr[g];
+  const int C = min(chunk_ptr[g + 1] - c0, (int)ldw);
+  const int nct = (C + kRouteChunks - 1) / kRouteChunks;
+  const int local = b - tile_ptr[g];
+  const int row0 = rbeg + (local / nct) * kRouteRows;
+  const int cb0 = (local % nct) * kRouteChunks;
+  const int tid = threadIdx.x;
+  const int tr = tid >> 4, tc = tid & 15;
+  // Staging: 32 rows x 32 float4 per k step, kRouteLoads per thread and operand (rows / chunks
+  // past the end re-read the last one; their dots are not stored).
+  const float* qsrc[kRouteLoads];
+  const float* ssrc[kRouteLoads];
+  int lrow[kRouteLoads], lk[kRouteLoads];
 #pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = shfl_xor(bv, o);
-        const int oc = shfl_xor(bc, o);
-        if (oc != 0x7fffffff && (bc == 0x7fffffff || ranks_before(ov, oc, bv, bc))) {
-          bv = ov;
-          bc = oc;
+  for (int i = 0; i < kRouteLoads; ++i) {
+    const int id = tid + 256 * i;
+    lrow[i] = id / (kRouteK / 4);
+    lk[i] = (id % (kRouteK / 4)) * 4;
+    qsrc[i] = q + (long long)min(row0 + lrow[i], rend - 1) * ldq + lk[i];
+    ssrc[i] = S + (long long)(c0 + min(cb0 + lrow[i], C - 1)) * d + lk[i];
+  }
+  float4 qv[kRouteLoads], sv[kRouteLoads];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < kRouteLoads; ++i) {
+      const bool in = k0 + lk[i] < d;   // d % 4 == 0: a float4 is all in or all out
+      qv[i] = in ? *reinterpret_cast<const float4*>(qsrc[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      sv[i] = in ? *reinterpret_cast<const float4*>(ssrc[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  };
+  float acc[2][2] = {};
+  load(0);
+  for (int k0 = 0; k0 < d; k0 += kRouteK) {
+    __syncthreads();   // the previous step's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < kRouteLoads; ++i) {
+      *reinterpret_cast<float4*>(&qs[lrow[i] * kRouteLd + lk[i]]) = qv[i];
+      *reinterpret_cast<float4*>(&ss[lrow[i] * kRouteLd + lk[i]]) = sv[i];
+    }
+    __syncthreads();
+    if (k0 + kRouteK < d) load(k0 + kRouteK);   // in flight during this step's FMAs
+#pragma unroll 8
+    for (int kk4 = 0; kk4 < kRouteK; kk4 += 4) {
+      float4 a[2], bb[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const float4*>(&qs[(tr + 16 * i) * kRouteLd + kk4]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bb[j] = *reinterpret_cast<const float4*>(&ss[(tc + 16 * j) * kRouteLd + kk4]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          acc[i][j] = fmaf(a[i].x, bb[j].x, acc[i][j]);
+          acc[i][j] = fmaf(a[i].y, bb[j].y, acc[i][j]);
+          acc[i][j] = fmaf(a[i].z, bb[j].z, acc[i][j]);
+          acc[i][j] = fmaf(a[i].w, bb[j].w, acc[i][j]);
         }
-      }
-      // bc is the same in every lane; C >= 1 guarantees a candidate exists for r < C.
-      if (lane == 0) {
-        taken[bc] = 1;
-        order[r] = bc;
-      }
-      __builtin_amdgcn_wave_barrier();
     }
   }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = row0 + tr + 16 * i;
+    if (row >= rend) continue;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = cb0 + tc + 16 * j;
+      if (c < C) w_dense[(long long)row * ldw + c] = acc[i][j];
+    }
+  }
+}
+
+constexpr int kSelectWaves = 4;
+
+__global__ __launch_bounds__(kSelectWaves * kWave) void route_rows_select_kernel(
+    int M, const int* __restrict__ chunk_ptr, const int* __restrict__ row_ptr, int G, int top_k,
+    float route_temp, float* __restrict__ w_dense, int ldw, int* __restrict__ idx,
+    float* __restrict__ w_sel, int kk) {
+  extern __shared__ float lds[];   // per wave: dots[ldw] | taken[ldw] | order[ldw]
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const int m = blockIdx.x * kSelectWaves + wv;
+  if (m >= M) return;
+  float* dots = lds + (size_t)wv * 3 * ldw;
+  int* taken = reinterpret_cast<int*>(dots + ldw);
+  int* order = taken + ldw;
+  const int g = find_tile_group(row_ptr, G, m);   // row_ptr is non-decreasing: same search
+  const int c0 = chunk_ptr[g];
+  const int C = min(chunk_ptr[g + 1] - c0, ldw);
+  float* wrow = w_dense + (long long)m * ldw;
+  for (int c = lane; c < C; c += kWave) dots[c] = wrow[c];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
-
-  // Softmax over the kept logits (logit = dot * route_temp, as the reference scales first).
-  float lmax = -INFINITY;
-  for (int r = lane; r < nsel; r += kWave) lmax = fmaxf(lmax, dots[order[r]] * route_temp);
-  lmax = wave_max(lmax);
-  float part = 0.f;
-  for (int r = lane; r < nsel; r += kWave) part += expf(dots[order[r]] * route_temp - lmax);
-  const float inv = 1.f / wave_sum(part);
-  int* irow = idx + (long long)m * kk;
-  float* selrow = w_sel + (long long)m * kk;
-  for (int r = lane; r < nsel; r += kWave) {
-    const int c = order[r];
-    const float wr = expf(dots[c] * route_temp - lmax) * inv;
-    irow[r] = c;
-    selrow[r] = wr;
-    wrow[c] = wr;
-  }
-  for (int r = nsel + lane; r < kk; r += kWave) {
-    irow[r] = -1;
-    selrow[r] = 0.f;
-  }
+  for (int c = lane; c < ldw; c += kWave) wrow[c] = 0.f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  select_topk_softmax(dots, taken, order, C, top_k, kk, route_temp, wrow, idx + (long long)m * kk,
+                      w_sel + (long long)m * kk, lane);
 }
 
 }  // namespace xenc
@@ -172,5 +308,27 @@ extern "C" int xenc_route_topk(const float* q, long long ldq, int M, int d, cons
     default:
       return XENC_EINVAL;
   }
+  return check_launch();
+}
+
+extern "C" int xenc_route_topk_rows(const float* q, long long ldq, int M, int d, const float* S,
+                                    const int* chunk_ptr, const int* row_ptr, const int* tile_ptr,
+                                    int G, int n_tiles, int top_k, float route_temp,
+                                    float* w_dense, long long ldw, int* idx, float* w_sel, int kk,
+                                    void* stream) {
+  if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || ldw <= 0 || n_tiles < 0) return XENC_EINVAL;
+  if (d % 8 != 0 || ldq < d || ldq % 4 != 0) return XENC_EINVAL;
+  const size_t lds = (size_t)kSelectWaves * 3 * ldw * sizeof(float);
+  if (lds > 64 * 1024) return XENC_EINVAL;  // up to 1365 chunks per library
+  if (M == 0) return XENC_OK;
+  if (!q || !S || !chunk_ptr || !row_ptr || !tile_ptr || !w_dense || !idx || !w_sel) return XENC_ENULL;
+  if (!aligned16(q) || !aligned16(S)) return XENC_EALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (n_tiles > 0)
+    hipLaunchKernelGGL(route_rows_logits_kernel, dim3(n_tiles), dim3(256), 0, st, q, ldq, d, S,
+                       chunk_ptr, row_ptr, tile_ptr, G, w_dense, ldw);
+  hipLaunchKernelGGL(route_rows_select_kernel, dim3((M + kSelectWaves - 1) / kSelectWaves),
+                     dim3(kSelectWaves * kWave), lds, st, M, chunk_ptr, row_ptr, G, top_k,
+                     route_temp, w_dense, (int)ldw, idx, w_sel, kk);
   return check_launch();
 }

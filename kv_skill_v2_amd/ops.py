@@ -310,6 +310,8 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
 # ---------------------------------------------------------------------------------------------
 # Prefill / registration read (MFMA) and the autograd of routing + read
 ROWS_SCORES, ROWS_READOUT, ROWS_ROUTE_BWD = 128, 128, 16
+ROUTE_TILE = 32            # rows and chunks per tile of the many-row routing kernel
+ROUTE_ROWS_MIN = 64        # from this many rows RouteFn uses the many-row routing kernel
 
 
 def _prefix(counts) -> list[int]:
@@ -332,6 +334,8 @@ class RowPlan:
     n_readout: int
     route_tiles: torch.Tensor
     n_route: int
+    logit_tiles: torch.Tensor
+    n_logit: int
 
     @property
     def M(self) -> int:
@@ -347,8 +351,9 @@ def row_plan(lib_: PagedLibrary, rows_per_library) -> RowPlan:
     sc = _prefix(-(-t // ROWS_SCORES) * c for t, c in zip(rows, lib_.n_chunks))
     ro = _prefix(-(-t // ROWS_READOUT) * d_tiles for t in rows)
     rb = _prefix(-(-t // ROWS_ROUTE_BWD) for t in rows)
+    lg = _prefix(-(-t // ROUTE_TILE) * -(-c // ROUTE_TILE) for t, c in zip(rows, lib_.n_chunks))
     return RowPlan(rows, _i32(_prefix(rows), dev), _i32(sc, dev), sc[-1], _i32(ro, dev), ro[-1],
-                   _i32(rb, dev), rb[-1])
+                   _i32(rb, dev), rb[-1], _i32(lg, dev), lg[-1])
 
 
 def cast_f16(x: torch.Tensor) -> torch.Tensor:
@@ -439,6 +444,29 @@ def route_backward(w: torch.Tensor, dw: torch.Tensor, lib_: PagedLibrary, plan: 
     return dq
 
 
+def route_topk_rows(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int = 0,
+                    route_temp: float = 10.0):
+    """route_topk for query rows grouped by library as in `plan` (rows of library g contiguous):
+    the q . S dots as 32 x 32 fp32 GEMM tiles, then the same wave top-k / softmax per row.
+    HIP kernels route_rows_logits_kernel + route_rows_select_kernel."""
+    q = _query(q, lib_.d)
+    M = q.shape[0]
+    if M != plan.M:
+        raise ValueError(f"q must have {plan.M} rows")
+    kk = lib_.kept(int(top_k))
+    dev = q.device
+    w = torch.empty(M, lib_.cmax, dtype=torch.float32, device=dev)
+    idx = torch.empty(M, kk, dtype=torch.int32, device=dev)
+    wsel = torch.empty(M, kk, dtype=torch.float32, device=dev)
+    if M == 0:
+        return w, idx, wsel
+    check(lib().xenc_route_topk_rows(ptr(q), q.stride(0), M, lib_.d, ptr(lib_.S), ptr(lib_.chunk_ptr),
+                                     ptr(plan.row_ptr), ptr(plan.logit_tiles), lib_.n_libraries, plan.n_logit,
+                                     int(top_k), float(route_temp), ptr(w), w.stride(0), ptr(idx), ptr(wsel),
+                                     kk, stream_handle(dev)), "xenc_route_topk_rows")
+    return w, idx, wsel
+
+
 def _plan_groups(plan: RowPlan) -> torch.Tensor:
     g = torch.repeat_interleave(torch.arange(len(plan.rows)), torch.tensor(plan.rows))
     return g.to(torch.int32)
@@ -449,8 +477,11 @@ class RouteFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, lib_, plan, top_k, route_temp):
-        qg = _plan_groups(plan).to(q.device)
-        w, idx, wsel = route_topk(q.detach(), lib_, qg, top_k=top_k, route_temp=route_temp)
+        if plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
+            w, idx, wsel = route_topk_rows(q.detach(), lib_, plan, top_k=top_k, route_temp=route_temp)
+        else:
+            qg = _plan_groups(plan).to(q.device)
+            w, idx, wsel = route_topk(q.detach(), lib_, qg, top_k=top_k, route_temp=route_temp)
         ctx.save_for_backward(w)
         ctx.lib, ctx.plan, ctx.route_temp = lib_, plan, route_temp
         ctx.mark_non_differentiable(idx, wsel)
@@ -552,5 +583,5 @@ def branch_read(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, read_temp: 
 
 
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
-           "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "RouteFn", "ReadFn",
+           "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "RouteFn", "ReadFn",
            "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS"]

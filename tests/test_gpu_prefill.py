@@ -134,3 +134,28 @@ def test_prefill_variants_fwd_bwd(dev, variant):
     assert rn <= 1e-2 and (r.detach().cpu().double() - ref[0].detach()).abs().max() <= 2e-3, (rn, rm)
     rn, rm = _rel(qd.grad, qo.grad[0])
     assert rn <= 1e-2 and rm <= 1e-2, (rn, rm)
+
+
+@pytest.mark.parametrize("counts,rows,top_k", [([32, 7, 130], [300, 64, 129], 0), ([32, 7, 130], [300, 0, 65], 5),
+                                               ([1, 64], [70, 1], 1)])
+def test_route_rows_matches_per_row_kernel(dev, counts, rows, top_k):
+    """The many-row routing kernel gives the per-row kernel's routing: identical kept chunks
+    (rows whose fp64 top-k gap is below 1e-5 are exempt) and weights within 1e-6."""
+    say("route rows", dict(counts=counts, rows=rows, top_k=top_k))
+    d = 256
+    P = synth.pool(counts, 64, d, device="cpu", tail_lo=1)
+    lib = _lib(P, dev)
+    plan = ops.row_plan(lib, rows)
+    q = synth.queries(sum(rows), d, device="cpu", seed=31)
+    qg = ops._plan_groups(plan)
+    w1, i1, s1 = ops.route_topk(q.to(dev), lib, qg.to(dev), top_k=top_k)
+    w2, i2, s2 = ops.route_topk_rows(q.to(dev), lib, plan, top_k=top_k)
+    assert (w1 - w2).abs().max().item() <= 1e-6
+    i1, i2 = i1.cpu(), i2.cpu()
+    off = 0
+    for g, T in enumerate(rows):
+        K, M, S = P.library(g)
+        gap = O.boundary_gap(q[off:off + T].double(), S.double(), top_k)
+        ok = gap > 1e-5
+        assert torch.equal(i1[off:off + T][ok], i2[off:off + T][ok]), g
+        off += T
