@@ -248,9 +248,12 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
 }
 
 constexpr int kSelectWaves = 4;
+constexpr int kSplitRouteRows = 256;   // below this many rows xenc_route_topk splits rows over waves
 
+// Library of row m: q_group[m] (clamped) when given, else the g with row_ptr[g] <= m < row_ptr[g+1].
 __global__ __launch_bounds__(kSelectWaves * kWave) void route_rows_select_kernel(
-    int M, const int* __restrict__ chunk_ptr, const int* __restrict__ row_ptr, int G, int top_k,
+    int M, const int* __restrict__ chunk_ptr, const int* __restrict__ row_ptr,
+    const int* __restrict__ q_group, int G, int top_k,
     float route_temp, float* __restrict__ w_dense, int ldw, int* __restrict__ idx,
     float* __restrict__ w_sel, int kk) {
   extern __shared__ float lds[];   // per wave: dots[ldw] | taken[ldw] | order[ldw]
@@ -261,7 +264,8 @@ __global__ __launch_bounds__(kSelectWaves * kWave) void route_rows_select_kernel
   float* dots = lds + (size_t)wv * 3 * ldw;
   int* taken = reinterpret_cast<int*>(dots + ldw);
   int* order = taken + ldw;
-  const int g = find_tile_group(row_ptr, G, m);   // row_ptr is non-decreasing: same search
+  const int g = q_group ? min(max(q_group[m], 0), G - 1)
+                        : find_tile_group(row_ptr, G, m);   // row_ptr is non-decreasing: same search
   const int c0 = chunk_ptr[g];
   const int C = min(chunk_ptr[g + 1] - c0, ldw);
   float* wrow = w_dense + (long long)m * ldw;
@@ -273,6 +277,48 @@ __global__ __launch_bounds__(kSelectWaves * kWave) void route_rows_select_kernel
   __builtin_amdgcn_wave_barrier();
   select_topk_softmax(dots, taken, order, C, top_k, kk, route_temp, wrow, idx + (long long)m * kk,
                       w_sel + (long long)m * kk, lane);
+}
+
+
+// Few query rows: one wave per (row, chunk) instead of one workgroup per row, so a handful of
+// rows still spreads over the whole GPU.  Each dot uses exactly the per-row kernel's arithmetic
+// (lane-owned float4 columns accumulated in block order, then the same xor butterfly), so the
+// dots, and hence the routing, are bit-identical to route_topk_kernel's.  Dots land in w_dense;
+// route_rows_select_kernel (with q_group) finishes.  Grid: (M, ceil(ldw / 8)); waves whose chunk
+// is past the row's library exit.
+template <int CB4>
+__global__ __launch_bounds__(8 * kWave) void route_dots_kernel(
+    const float* __restrict__ q, long long ldq, int d, const float* __restrict__ S,
+    const int* __restrict__ chunk_ptr, const int* __restrict__ q_group, int G,
+    float* __restrict__ w_dense, int ldw) {
+  const int m = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int c = blockIdx.y * 8 + (int)(threadIdx.x / kWave);
+  const int g = min(max(q_group[m], 0), G - 1);
+  const int c0 = chunk_ptr[g];
+  const int C = min(chunk_ptr[g + 1] - c0, ldw);
+  if (c >= C) return;
+  const float* qrow = q + (long long)m * ldq;
+  const float* srow = S + (long long)(c0 + c) * d;
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  float4 qv[CB4];
+  f32x4 sv[CB4];
+#pragma unroll
+  for (int cb = 0; cb < CB4; ++cb) {
+    const int i = (cb * kWave + lane) * 4;
+    qv[cb] = i < d ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    sv[cb] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(srow + min(i, d - 4)));
+  }
+  float a = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < CB4; ++cb) {
+    a = fmaf(qv[cb].x, sv[cb].x, a);
+    a = fmaf(qv[cb].y, sv[cb].y, a);
+    a = fmaf(qv[cb].z, sv[cb].z, a);
+    a = fmaf(qv[cb].w, sv[cb].w, a);
+  }
+  a = wave_sum(a);
+  if (lane == 0) w_dense[(long long)m * ldw + c] = a;
 }
 
 }  // namespace xenc
@@ -294,6 +340,28 @@ extern "C" int xenc_route_topk(const float* q, long long ldq, int M, int d, cons
   constexpr int NW = 8;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int cb4 = (d + 255) / 256;
+  // Fewer rows than about one per CU: one wave per (row, chunk), then the wave top-k per row.
+  const size_t sel_lds = (size_t)kSelectWaves * 3 * ldw * sizeof(float);
+  if (M < kSplitRouteRows && sel_lds <= 64 * 1024) {
+    const dim3 grid(M, (unsigned)((ldw + 7) / 8));
+    switch (cb4) {
+#define XENC_DOTS(N)                                                                             \
+  case N:                                                                                        \
+    hipLaunchKernelGGL(route_dots_kernel<N>, grid, dim3(NW * kWave), 0, st, q, ldq, d, S,        \
+                       chunk_ptr, q_group, G, w_dense, (int)ldw);                                \
+    break;
+      XENC_DOTS(1) XENC_DOTS(2) XENC_DOTS(3) XENC_DOTS(4) XENC_DOTS(5) XENC_DOTS(6)
+      XENC_DOTS(7) XENC_DOTS(8) XENC_DOTS(9) XENC_DOTS(10) XENC_DOTS(11) XENC_DOTS(12)
+      XENC_DOTS(13) XENC_DOTS(14) XENC_DOTS(15) XENC_DOTS(16)
+#undef XENC_DOTS
+      default:
+        return XENC_EINVAL;
+    }
+    hipLaunchKernelGGL(route_rows_select_kernel, dim3((M + kSelectWaves - 1) / kSelectWaves),
+                       dim3(kSelectWaves * kWave), sel_lds, st, M, chunk_ptr, nullptr, q_group, G,
+                       top_k, route_temp, w_dense, (int)ldw, idx, w_sel, kk);
+    return check_launch();
+  }
   switch (cb4) {
 #define XENC_CASE(N)                                                                           \
   case N:                                                                                      \
@@ -328,7 +396,7 @@ extern "C" int xenc_route_topk_rows(const float* q, long long ldq, int M, int d,
     hipLaunchKernelGGL(route_rows_logits_kernel, dim3(n_tiles), dim3(256), 0, st, q, ldq, d, S,
                        chunk_ptr, row_ptr, tile_ptr, G, w_dense, ldw);
   hipLaunchKernelGGL(route_rows_select_kernel, dim3((M + kSelectWaves - 1) / kSelectWaves),
-                     dim3(kSelectWaves * kWave), lds, st, M, chunk_ptr, row_ptr, G, top_k,
+                     dim3(kSelectWaves * kWave), lds, st, M, chunk_ptr, row_ptr, nullptr, G, top_k,
                      route_temp, w_dense, (int)ldw, idx, w_sel, kk);
   return check_launch();
 }

@@ -223,3 +223,20 @@ def test_graph_capture_and_replay(dev):
         ref = step()
         torch.cuda.synchronize()
         assert torch.equal(got, ref), rep
+
+
+@pytest.mark.parametrize("d,top_k", [(2048, 8), (40, 0), (2560, 3)])
+def test_route_paths_bit_identical(dev, d, top_k):
+    """Below 256 rows xenc_route_topk spreads the dots over one wave per (row, chunk); from 256
+    rows one workgroup scores a row.  Both use the same arithmetic: identical w, idx, w_sel."""
+    print("[case] route paths", d, top_k, flush=True)
+    counts = synth.batched_chunk_counts(9, 3, 70, seed=11)
+    P = synth.pool(counts, 64, d, device="cpu")
+    lib = _to_lib(P, dev)
+    M = 300
+    qg = torch.randint(0, len(counts), (M,), generator=torch.Generator().manual_seed(5)).int()
+    q = synth.queries(M, d, device="cpu", seed=9)
+    w_big, i_big, s_big = ops.route_topk(q.to(dev), lib, qg.to(dev), top_k=top_k)
+    for lo, hi in ((0, 100), (100, 300 - 45), (255, 300)):
+        w, i, s = ops.route_topk(q[lo:hi].to(dev), lib, qg[lo:hi].to(dev), top_k=top_k)
+        assert torch.equal(w, w_big[lo:hi]) and torch.equal(i, i_big[lo:hi]) and torch.equal(s, s_big[lo:hi])
