@@ -475,8 +475,10 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
   }
 
   // Publish this partial device-wide, then count it; the last workgroup of query m merges.
-  // The barrier orders every wave's partial stores before thread 0's agent-scope release (one
-  // L2 write-back per workgroup, not per wave); only the last workgroup pays the acquire.
+  // Every store of the partial comes from wave 0 (thread 0's wave): its agent-scope release
+  // (L2 write-back, then a wait for the wave's own stores) covers them, one write-back per
+  // workgroup.  The barrier does not wait for other waves' stores, so no other wave may write
+  // any part of the partial.  Only the last workgroup pays the acquire.
   __syncthreads();
   if (threadIdx.x == 0) {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
