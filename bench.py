@@ -36,6 +36,7 @@ def parse():
     ap.add_argument("--nsplit", type=int, default=None)
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
+    ap.add_argument("--no-graph", action="store_true", help="multi_depth: time the eager step only")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the timed loop, copy a buffer of this size 3 times (a plain copy "
                          "kernel of known bytes, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -256,7 +257,37 @@ def bench_multi_depth(args):
     for _ in range(args.steps):
         step()
     torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ms_eager = (time.perf_counter() - t0) * 1e3 / args.steps
+
+    # The step is ~20 small launches: capture it once in a HIP graph and replay it.  Every replay
+    # is checked against the eager result (bit for bit) with eager work and synchronisation in
+    # between; on any mismatch the eager time is reported.
+    ms_graph, graph_ok = None, False
+    if not args.no_graph:
+        ref_out = step()[0].clone()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            step()
+        torch.cuda.current_stream().wait_stream(s)
+        gph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gph):
+            g_out = step()[0]
+        graph_ok = True
+        for _ in range(3):
+            gph.replay()
+            torch.cuda.synchronize()
+            graph_ok &= bool(torch.equal(g_out, ref_out))
+            step()
+            torch.cuda.synchronize()
+        if graph_ok:
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                gph.replay()
+            torch.cuda.synchronize()
+            ms_graph = (time.perf_counter() - t0) * 1e3 / args.steps
+            graph_ok &= bool(torch.equal(g_out, ref_out))
+    ms_step = ms_graph if graph_ok else ms_eager
     achieved = bytes_step / (ms_step * 1e-3) / 1e9
 
     cpu = None
@@ -287,7 +318,8 @@ def bench_multi_depth(args):
         "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
         "config": {"workload": "multi_depth", "depths": L, "chunks_per_depth": c["chunks"],
                    "slots_per_page": c["N"], "d_s": d, "d_reader": dr, "batch": B,
-                   "selector_top_k": c["k_sel"], "top_k": k, "B_dtype": "fp32", "accumulate": "fp32"},
+                   "selector_top_k": c["k_sel"], "top_k": k, "B_dtype": "fp32", "accumulate": "fp32",
+                   "hip_graph": bool(graph_ok), "ms_per_step_eager": ms_eager},
         "roofline": {"bound": "hbm", "kernel": "whole step (route + read + B GEMM + epilogue)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
