@@ -416,7 +416,7 @@ def main():
                    "slots_per_page": P.pages.shape[1], "top_k": top_k, "read_temp": read_temp,
                    "route_temp": route_temp, "accumulate": "fp32", "page_table": "seeded shuffle",
                    "nsplit": args.nsplit or ops.default_nsplit(B * idx_h.shape[1], P.pages.shape[1])},
-        "roofline": {"bound": "hbm", "kernel": "decode_read_kernel",
+        "roofline": {"bound": "hbm", "kernel": "decode_read_kernel (+ merge_kernel when two-pass)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic["bytes_per_launch"] if traffic else None,

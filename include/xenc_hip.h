@@ -79,8 +79,9 @@ int xenc_route_topk_rows(const float* q, long long ldq, int M, int d, const floa
  * over the valid slots n of the routed chunks c_j = idx[m,j] (entries < 0 are skipped).
  * Each slot row is read from HBM once for both the score and the value.  Page slots are
  * split into nsplit ranges of ceil(slots_per_page/nsplit) slots (nsplit in 1..64).
- * r is fp32 [M, ldr].  One kernel launch: the last workgroup of each query merges that
- * query's partials in a fixed order, so results are deterministic.
+ * r is fp32 [M, ldr].  The partials of a query are merged in a fixed order, so results are
+ * deterministic: launches of >= 256 (query, page, split) units merge in a second kernel, smaller
+ * ones in the last workgroup of each query (same merge, bit-identical results).
  * Workspace: xenc_decode_workspace_bytes(max_rows, kk, nsplit, d) bytes for calls of up to
  * max_rows query rows (pass the same max_rows to every call); its first max_rows ints are
  * arrival counters that must be zero before the first call (xenc_decode_workspace_init does that
