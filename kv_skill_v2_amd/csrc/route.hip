@@ -20,11 +20,85 @@ namespace xenc {
 // (logit = dot * route_temp, scaled before the softmax as the reference does).  dots[0..C) hold
 // the raw dot products; taken / order are scratch of C entries.  Writes the kept weights into
 // wrow (which the caller has zeroed), and idx / w_sel rows (-1 / 0 past the kept count).
+// Register variant for C <= 64 * R chunks and <= 64 kept: lane l holds chunks l, l + 64, ...;
+// each round is a wave argmax (value, then lower index) by xor butterfly, the winner's owner
+// retires it, and lane r keeps round r's winner for the softmax.  Same selection and arithmetic
+// as the LDS variant below.
+template <int R>
+__device__ void select_topk_softmax_reg(const float* dots, int C, int top_k, int kk,
+                                        float route_temp, float* wrow, int* irow, float* selrow,
+                                        int lane) {
+  const bool dense = top_k <= 0 || top_k >= C;
+  const int nsel = min(dense ? C : top_k, kk);
+  float v[R];
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int c = lane + kWave * i;
+    v[i] = c < C ? dots[c] : -INFINITY;
+  }
+  int mine_c = -1;        // lane r: chunk chosen in round r
+  float mine_v = 0.f;
+  if (dense) {            // keep every chunk, in chunk order (nsel = C <= 64 here)
+    mine_c = lane < nsel ? lane : -1;
+    mine_v = v[0];
+  } else {
+    for (int r = 0; r < nsel; ++r) {
+      float bv = -INFINITY;
+      int bc = 0x7fffffff;
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int c = lane + kWave * i;
+        if (c < C && v[i] != -INFINITY && (bc == 0x7fffffff || ranks_before(v[i], c, bv, bc))) {
+          bv = v[i];
+          bc = c;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = shfl_xor(bv, o);
+        const int oc = shfl_xor(bc, o);
+        if (oc != 0x7fffffff && (bc == 0x7fffffff || ranks_before(ov, oc, bv, bc))) {
+          bv = ov;
+          bc = oc;
+        }
+      }
+      if ((bc & (kWave - 1)) == lane) v[bc / kWave] = -INFINITY;   // retire the winner
+      if (lane == r) {
+        mine_c = bc;
+        mine_v = bv;
+      }
+    }
+  }
+  const bool has = mine_c >= 0;
+  const float lg = has ? mine_v * route_temp : -INFINITY;
+  const float lmax = wave_max(lg);
+  const float e = has ? expf(lg - lmax) : 0.f;
+  const float inv = 1.f / wave_sum(e);
+  if (has) {
+    const float wr = e * inv;
+    irow[lane] = mine_c;
+    selrow[lane] = wr;
+    wrow[mine_c] = wr;
+  }
+  for (int r = nsel + lane; r < kk; r += kWave) {
+    irow[r] = -1;
+    selrow[r] = 0.f;
+  }
+}
+
 __device__ void select_topk_softmax(const float* dots, int* taken, int* order, int C, int top_k,
                                     int kk, float route_temp, float* wrow, int* irow, float* selrow,
                                     int lane) {
   const bool dense = top_k <= 0 || top_k >= C;
   const int nsel = min(dense ? C : top_k, kk);
+  if (nsel <= kWave && C <= kWave) {
+    select_topk_softmax_reg<1>(dots, C, top_k, kk, route_temp, wrow, irow, selrow, lane);
+    return;
+  }
+  if (nsel <= kWave && C <= 4 * kWave && !dense) {
+    select_topk_softmax_reg<4>(dots, C, top_k, kk, route_temp, wrow, irow, selrow, lane);
+    return;
+  }
   if (dense) {
     for (int r = lane; r < nsel; r += kWave) order[r] = r;
   } else {
