@@ -134,3 +134,12 @@ def test_decode_reader_rejects_bad_inputs(dev):
     bad[2] = bad[2].half()
     with pytest.raises(ValueError):
         dec(*bad, 0.1)
+
+
+def test_decode_reader_zero_rows(dev):
+    say("op B zero rows")
+    dec = DecodeReader(4, 8, 2, 64, max_keys=128, device=dev)
+    args = [a.to(dev) for a in _case(1, 8, 2, 64, 16, 10, 10, 0, torch.bfloat16, op_blocks=4, own_blocks=4)]
+    args[0] = args[0][:0]
+    out = dec(*args, 0.1)
+    assert out.shape == (0, 8, 64)

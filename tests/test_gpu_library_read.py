@@ -79,6 +79,8 @@ CASES = [
     (2560, 128, [10, 4], 8, 2, True),
     (256, 64, [4, 7, 1], 2, 2, False),
     (2048, 64, [12], 20, 1, False),
+    # the limits: d = 4096 (8 column blocks), a 1000-slot page split 64 ways, dense over 12 chunks
+    (4096, 1000, [3, 12], 0, 64, True),
 ]
 
 
@@ -240,3 +242,22 @@ def test_route_paths_bit_identical(dev, d, top_k):
     for lo, hi in ((0, 100), (100, 300 - 45), (255, 300)):
         w, i, s = ops.route_topk(q[lo:hi].to(dev), lib, qg[lo:hi].to(dev), top_k=top_k)
         assert torch.equal(w, w_big[lo:hi]) and torch.equal(i, i_big[lo:hi]) and torch.equal(s, s_big[lo:hi])
+
+
+def test_empty_inputs(dev):
+    """Zero query rows: every entry point returns empty results without launching."""
+    say("empty inputs")
+    P = synth.pool([3, 2], 64, 128, device="cpu")
+    lib = _to_lib(P, dev)
+    q = torch.zeros(0, 128, device=dev)
+    qg = torch.zeros(0, dtype=torch.int32, device=dev)
+    w, idx, wsel = ops.route_topk(q, lib, qg, top_k=2)
+    assert w.shape == (0, 3) and idx.shape == (0, 2) and wsel.shape == (0, 2)
+    r = ops.library_read_decode(q, lib, idx, wsel, qg)
+    assert r.shape == (0, 128)
+    plan = ops.row_plan(lib, [0, 0])
+    w2, _, _ = ops.route_topk_rows(q, lib, plan, top_k=2)
+    assert w2.shape == (0, 3)
+    r2, p = ops.prefill_forward(q, torch.zeros(0, 3, device=dev), lib, plan)
+    assert r2.shape == (0, 128) and p.shape == (3 * 64 // 8, 0, 8)
+    torch.cuda.synchronize()

@@ -159,3 +159,26 @@ def test_route_rows_matches_per_row_kernel(dev, counts, rows, top_k):
         ok = gap > 1e-5
         assert torch.equal(i1[off:off + T][ok], i2[off:off + T][ok]), g
         off += T
+
+
+def test_prefill_single_slot_chunks(dev):
+    """Chunks of 1 and 3 valid slots next to a full one, softmax and linear, forward and dQ."""
+    say("prefill 1-slot chunks")
+    d, N, T = 128, 64, 40
+    g = torch.Generator().manual_seed(41)
+    rows = [torch.nn.functional.normalize(torch.randn(n, d, generator=g), dim=-1) for n in (1, 64, 3)]
+    K, M, S = O.library_tensors(rows)
+    lib = ops.PagedLibrary.from_padded(K, M, S, device=dev, pad_to=64)
+    q = synth.queries(T, d, device="cpu", seed=43)
+    g_up = torch.randn(T, d, generator=g)
+    for soft in (True, False):
+        qd = q.to(dev).requires_grad_(True)
+        r, w = ops.library_read(qd, lib, lib.plan([T]), top_k=2, read_softmax=soft)
+        (r * g_up.to(dev)).sum().backward()
+        qo = q.double().view(1, T, d).requires_grad_(True)
+        ref, _ = O.branch_read(qo, K.double(), M, S.double(), top_k=2, read_softmax=soft)
+        (ref[0] * g_up.double()).sum().backward()
+        rn, _ = _rel(r.detach(), ref[0].detach())
+        assert rn <= 1e-2 and (r.detach().cpu().double() - ref[0].detach()).abs().max() <= 2e-3, soft
+        rn, rm = _rel(qd.grad, qo.grad[0])
+        assert rn <= 1e-2 and rm <= 1e-2, (soft, rn, rm)
