@@ -35,20 +35,13 @@
 #ifndef XENC_DECODE_SPT_WIDE
 #define XENC_DECODE_SPT_WIDE 2
 #endif
-// 1: two register tiles per wave, the next one loading while the current one is consumed.
-#ifndef XENC_DECODE_PIPELINE
-#define XENC_DECODE_PIPELINE 0
-#endif
-// Score dot products with q rounded to fp16 and v_dot2_f32_f16 (fp32 accumulate).  Measured no
-// faster (the kernel is HBM-bound) and it moves scores by ~1e-5, so it is off.
-#ifndef XENC_DECODE_QF16
-#define XENC_DECODE_QF16 0
-#endif
+// Measured and not kept (B = 64 batched decode, same box): two register tiles per wave with the
+// next one loading while the current one is consumed (184-185 us, no change), and score dots with
+// q rounded to fp16 through v_dot2_f32_f16 (no faster; moves scores by ~1e-5).
 
 namespace xenc {
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // Buffer descriptor word 3 for CDNA (raw buffer, 32-bit format fields unused by b128 loads).
@@ -81,12 +74,13 @@ __device__ __forceinline__ void wave_reduce_scatter(float (&v)[SPT], int lane) {
 }
 
 struct DecodeWorkspace {
-  int* counters;    // [M]        arrivals per query (0 between calls)
+  int* counters;    // [max_rows] arrivals per query (0 between calls; in-kernel merge only)
   float2* part_ml;  // [units]    (max in log2 units, sum) per partial; sum 0 = empty
   float* part_acc;  // [units, d] un-normalised value sums
 };
 
-// Merge the k*nsplit partials of query m into r[m] (run by the last workgroup of the query).
+// Merge the k*nsplit partials of query m into r[m] (run by merge_kernel, or by the last
+// workgroup of the query in the in-kernel merge).
 // LDS: [m | l | coefficient | unit] per partial (4 * nu words).  Every step is parallel over the
 // partials; the value sum runs over the live partials in (chunk, split) order with 8 loads in
 // flight, so the result is independent of arrival order.
@@ -205,19 +199,11 @@ __device__ __forceinline__ void load_tile(u32x4 (&kv)[SPT][CB], const TileCtx<CB
   __builtin_amdgcn_sched_barrier(0);
 }
 
-#if XENC_DECODE_QF16
-#define QV_PARAM const half8_t (&qh)[CB],
-#define QV_ARG qh,
-#else
-#define QV_PARAM
-#define QV_ARG
-#endif
-
 // Score the SPT rows of a loaded tile, update the wave's online softmax and accumulate the
 // rows into acc with the same registers (each row is read from HBM once).
 template <int SPT, int CB>
 __device__ __forceinline__ void consume_tile(u32x4 (&kv)[SPT][CB], const TileCtx<CB>& c, int t0,
-                                             const float (&qv)[CB][8], QV_PARAM float (&acc)[CB][8],
+                                             const float (&qv)[CB][8], float (&acc)[CB][8],
                                              float& mrun, float& lrun) {
   float part[SPT];
 #pragma unroll
@@ -226,17 +212,8 @@ __device__ __forceinline__ void consume_tile(u32x4 (&kv)[SPT][CB], const TileCtx
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb) {
       const half8_t h = __builtin_bit_cast(half8_t, kv[j][cb]);
-#if XENC_DECODE_QF16
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const half2_t kp = {h[2 * i], h[2 * i + 1]};
-        const half2_t qp = {qh[cb][2 * i], qh[cb][2 * i + 1]};
-        p = __builtin_amdgcn_fdot2(kp, qp, p, false);
-      }
-#else
 #pragma unroll
       for (int i = 0; i < 8; ++i) p = fmaf(qv[cb][i], (float)h[i], p);
-#endif
     }
     part[j] = p;
   }
@@ -340,13 +317,6 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
         for (int i = 0; i < 8; ++i) qv[cb][i] = 0.f;
       }
     }
-#if XENC_DECODE_QF16
-    half8_t qh[CB];
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) qh[cb][i] = (_Float16)qv[cb][i];
-#endif
 
     float acc[CB][8];
 #pragma unroll
@@ -371,37 +341,15 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
     ctx.lin_scale = lin_scale;
     ctx.softmax = softmax;
     ctx.lane = lane;
-    // With XENC_DECODE_PIPELINE the tile after the one being consumed is already in flight; the
-    // steady-state loop has no branch around a load, so every wait is an exact vmcnt.
+    // Wave wv takes slot rows first, first + step, ... (SPT rows each) of the split.
     const int step = NW * SPT;
     const int first = s0 + wv * SPT;
     const int ntile = first < s1 ? (s1 - first + step - 1) / step : 0;
-#if XENC_DECODE_PIPELINE
-    if (ntile > 0) {
-      u32x4 ka[SPT][CB], kb[SPT][CB];
-      load_tile<SPT, CB>(ka, ctx, first);
-      int i = 0;
-      for (; i + 2 < ntile; i += 2) {
-        load_tile<SPT, CB>(kb, ctx, first + (i + 1) * step);
-        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
-        load_tile<SPT, CB>(ka, ctx, first + (i + 2) * step);
-        consume_tile<SPT, CB>(kb, ctx, first + (i + 1) * step, qv, QV_ARG acc, mrun, lrun);
-      }
-      if (i + 1 < ntile) {
-        load_tile<SPT, CB>(kb, ctx, first + (i + 1) * step);
-        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
-        consume_tile<SPT, CB>(kb, ctx, first + (i + 1) * step, qv, QV_ARG acc, mrun, lrun);
-      } else {
-        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
-      }
-    }
-#else
     for (int i = 0; i < ntile; ++i) {
       u32x4 ka[SPT][CB];
       load_tile<SPT, CB>(ka, ctx, first + i * step);
-      consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, QV_ARG acc, mrun, lrun);
+      consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, acc, mrun, lrun);
     }
-#endif
 
     // Merge the NW waves of this workgroup: rescale each wave to the common max, then a tree
     // over LDS (round h: waves h..2h-1 hand their sums to waves 0..h-1) — a fixed order, so
