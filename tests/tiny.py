@@ -67,11 +67,12 @@ def x_in(d: int, T: int = 7, B: int = 2, seed: int = 1) -> torch.Tensor:
 
 def oracle_forward(model: nn.Module, x: torch.Tensor, itf, tensors: dict, *, top_k: int = 0,
                    read_temp: float = 12.0, route_temp: float = 10.0, read_softmax: bool = True,
-                   selector=None, grad: bool = False):
+                   selector=None, grad: bool = False, call=None):
     """Run a CPU fp64 copy of `model` with one hook per injection layer computing the reference
     branch with oracle functions.  tensors: {li: (K, M, S[, V])}.  selector: a LayerSelector whose
-    parameters are copied (weights from its u at the first candidate layer).  Returns
-    (output, copies) where copies = (interface copy, selector copy) for gradient comparisons."""
+    parameters are copied (weights from its u at the first candidate layer).  call(m, x) runs the
+    copy (default: m(x) on fp64 x).  Returns (output, copies) where copies = (interface copy,
+    selector copy) for gradient comparisons."""
     m = copy.deepcopy(model).cpu().double()
     for mod in m.modules():          # the copy must not run hooks an injector put on `model`
         mod._forward_hooks.clear()
@@ -102,7 +103,7 @@ def oracle_forward(model: nn.Module, x: torch.Tensor, itf, tensors: dict, *, top
     for li in it.inject_layers:
         blocks[li].register_forward_hook(make(li))
     with torch.set_grad_enabled(grad):
-        y = m(x.cpu().double())
+        y = call(m, x.cpu()) if call is not None else m(x.cpu().double())
     return y, (it, sel)
 
 
