@@ -148,6 +148,25 @@ int xenc_route_backward(const float* w, long long ldw, const float* dw_read, lon
                         void* stream);
 
 /*
+ * ---- Library pool build from a document cache
+ * rows fp16 [R, d] holds the slot rows of C chunks back to back: chunk c is rows
+ * row_off[c] .. row_off[c+1]-1 (int64 [C+1], device).  For each chunk, on fp32 values:
+ *   x_n      = row n, or L2(row n - mu) = (row - mu) / (|row - mu| + 1e-6) when mu (fp32 [d]) is given
+ *   page c   = x_0 .. x_{n_c-1} then zero rows up to slots_per_page, each zero-padded to d_pad,
+ *              stored fp16 at pages + c * page_stride (halves)
+ *   S[c]     = m / (|m| + 1e-6), m = sum_n x_n / max(n_c, 1), fp32 at S + c * lds (d_pad floats)
+ *   nvalid[c] = n_c
+ * The caller guarantees n_c <= slots_per_page (a longer chunk is cut to slots_per_page rows).
+ * d % 8 == 0, d <= d_pad <= 4096, d_pad % 8 == 0, page_stride >= slots_per_page * d_pad.
+ * Deterministic: the column sums merge in a fixed order.
+ * Replaces the padding, centring and summaries of Library.__init__ / _summaries
+ * (xenc/library.py:47-74) over the cache that load_doc_cache returns (xenc/depth_skill.py:299-311).
+ */
+int xenc_build_pages(const void* rows, const long long* row_off, int C, int d, const float* mu,
+                     int slots_per_page, int d_pad, void* pages, long long page_stride, float* S,
+                     long long lds, int* nvalid, void* stream);
+
+/*
  * ---- Op B: joint decode read over a document operator's pages and the request's own pages
  * For query row n < N and query head hq_i = h*G + g (G = hq / hkv, 1 <= G <= 8):
  *   keys/values = [op pool rows 0..op_len[n]-1 ; own pool rows 0..own_len[n]-1]

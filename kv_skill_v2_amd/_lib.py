@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lock = threading.Lock()
 _lib = None
@@ -48,6 +48,8 @@ SIGNATURES = {
         c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_rows, stream
     "xenc_cast_rows_f16": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p]),
     "xenc_fragment_pages": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "xenc_build_pages": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p,
+                                 c_longlong, c_void_p, c_longlong, c_void_p, c_void_p]),
     "xenc_prefill_scores": (c_int, [
         c_int, c_void_p, c_int, c_void_p, c_void_p,  # mode, x, d, row_ptr, tile_ptr
         c_int, c_int, c_void_p, c_int, c_longlong,   # G, n_tiles, pages_a, slots_per_page, page_stride

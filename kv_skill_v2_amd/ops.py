@@ -129,6 +129,82 @@ class PagedLibrary:
                             n_chunks=nch, nvalid=nv,
                             values=torch.cat(vals).contiguous() if untied else None, d_valid=d)
 
+    @staticmethod
+    def from_doc_caches(caches, rho: float, device, center: dict | None = None,
+                        slots_per_page: int | None = None, pad_to: int = 64) -> "PagedLibrary":
+        """The pool of depth rho for one or more document caches (the dicts load_doc_cache
+        returns: {"chunks": [{"K": {rho: fp16 [n_c, d]}, ["V": {...}], ...}], ...}), one library
+        per cache, built on the device by xenc_build_pages: the chunk rows go up in one copy and
+        one kernel writes the zero-padded fp16 pages, the fp32 summary keys S = L2(masked mean)
+        and the valid counts, centring the rows as L2(row - mu) when center = {rho: mu} is given
+        (the math of Library.__init__ / _summaries, xenc/library.py:47-74, at the Library's fp32
+        precision before the fp16 store).  Untied values are copied uncentred, as the reference
+        does."""
+        from .depth import rho_key
+
+        device = torch.device(device)
+        _require_device(torch.empty(0, device=device), "device")
+        if isinstance(caches, dict):
+            caches = [caches]
+        if not caches:
+            raise ValueError("from_doc_caches needs at least one cache")
+        rows, vrows, nch = [], [], []
+        for cache in caches:
+            chunks = cache["chunks"]
+            if not chunks:
+                raise ValueError("Library needs at least one chunk")
+            nch.append(len(chunks))
+            for ch in chunks:
+                k = ch["K"]
+                rows.append(k[rho_key(k, rho)])
+                v = ch.get("V") if isinstance(ch, dict) else None
+                vrows.append(None if v is None else v[rho_key(v, rho)])
+                if vrows[-1] is not None and vrows[-1].shape != rows[-1].shape:
+                    raise ValueError("untied values must match the key rows' shape")
+        d = int(rows[0].shape[-1])
+        n = [int(r.shape[0]) for r in rows]
+        if min(n) < 1:
+            raise ValueError("every chunk needs at least one slot row")
+        if any(r.dim() != 2 or r.shape[-1] != d for r in rows):
+            raise ValueError(f"chunk rows must all be [n_c, {d}]")
+        rnd = lambda x: -(-x // pad_to) * pad_to  # noqa: E731
+        N = rnd(slots_per_page or max(n))
+        if N < max(n):
+            raise ValueError(f"slots_per_page={N} is below the longest chunk ({max(n)} slots)")
+        dp = rnd(d)
+        if d % 8 or dp > 4096:
+            raise ValueError(f"d={d} must be a multiple of 8 and pad to at most 4096")
+        mu = None
+        if center is not None:
+            mu = center[rho_key(center, rho)].to(device=device, dtype=torch.float32).contiguous()
+            if mu.shape != (d,):
+                raise ValueError(f"centre must be [{d}], got {tuple(mu.shape)}")
+        Ctot = len(rows)
+        off = [0]
+        for c in n:
+            off.append(off[-1] + c)
+        off_d = torch.tensor(off, dtype=torch.int64, device=device)
+        stream = stream_handle(device)
+
+        def build(src, centre):
+            flat = torch.cat([r.to(torch.float16) for r in src]).to(device).contiguous()
+            pages = torch.empty(Ctot, N, dp, dtype=torch.float16, device=device)
+            S = torch.empty(Ctot, dp, dtype=torch.float32, device=device)
+            nv = torch.empty(Ctot, dtype=torch.int32, device=device)
+            check(lib().xenc_build_pages(ptr(flat), ptr(off_d), Ctot, d, ptr(centre), N, dp, ptr(pages),
+                                         N * dp, ptr(S), dp, ptr(nv), stream), "xenc_build_pages")
+            return pages, S, nv
+
+        pages, S, nv = build(rows, mu)
+        values = None
+        if any(v is not None for v in vrows):
+            values = build([v if v is not None else k for v, k in zip(vrows, rows)], None)[0]
+        ptr_ = [0]
+        for c in nch:
+            ptr_.append(ptr_[-1] + c)
+        return PagedLibrary(pages, torch.arange(Ctot, dtype=torch.int32, device=device), nv,
+                            _i32(ptr_, device), S, n_chunks=nch, nvalid=n, values=values, d_valid=d)
+
     # ------------------------------------------------------------------ properties
     @property
     def d(self) -> int:

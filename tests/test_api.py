@@ -132,6 +132,41 @@ def test_from_doc_cache():
     assert lib.chunk_meta[0]["doc_id"] == "dd"
 
 
+def test_doc_cache_file_roundtrip(tmp_path):
+    """save_doc_cache stores K (and V) as fp16 CPU tensors keyed by float depth; load_doc_cache
+    reads it back with weights_only; a Library from the file equals one from the fp16 rows; the
+    device pool build refuses a CPU device (no CPU path)."""
+    from kv_skill_v2_amd.depth import load_doc_cache, save_doc_cache
+    from kv_skill_v2_amd.ops import PagedLibrary
+
+    g = torch.Generator().manual_seed(3)
+    chunks = [{"K": {r: torch.randn(n, 16, generator=g) for r in DEPTHS},
+               "V": {r: torch.randn(n, 16, generator=g) for r in DEPTHS}, "start": 0, "n_tokens": n}
+              for n in (5, 9)]
+    cache = {"depths": DEPTHS, "chunks": chunks, "doc_id": "x", "encoder": "e", "chunk_tokens": 512}
+    path = tmp_path / "sub" / "c.pt"
+    save_doc_cache(cache, str(path))
+    assert sorted(p.name for p in path.parent.iterdir()) == ["c.pt"]   # no temporary left behind
+    back = load_doc_cache(str(path))
+    assert back["doc_id"] == "x" and back["chunk_tokens"] == 512 and len(back["chunks"]) == 2
+    for c0, c1 in zip(chunks, back["chunks"]):
+        for f in ("K", "V"):
+            assert sorted(c1[f]) == sorted(float(r) for r in DEPTHS)
+            for r in DEPTHS:
+                t = c1[f][float(r)]
+                assert t.dtype == torch.float16 and t.device.type == "cpu" and t.is_contiguous()
+                assert torch.equal(t, c0[f][r].half())
+    reader = TinyLM(d=40, n_layers=8)
+    a = Library.from_doc_cache(back, reader)
+    fp16 = {**cache, "chunks": [{**c, "K": {r: t.half() for r, t in c["K"].items()},
+                                 "V": {r: t.half() for r, t in c["V"].items()}} for c in chunks]}
+    b = Library.from_doc_cache(fp16, reader)
+    for li in a.layers:
+        assert torch.equal(a.K[li], b.K[li]) and torch.equal(a.V[li], b.V[li]) and torch.equal(a.S[li], b.S[li])
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        PagedLibrary.from_doc_caches(back, 0.25, "cpu")
+
+
 # ----------------------------------------------------------------------------- selector
 D, CAND = 40, [3, 5, 7, 9, 11, 13, 15, 17]
 
