@@ -32,7 +32,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="batched_paged_decode",
-                    choices=["batched_paged_decode", "single_decode", "prefill", "multi_depth"])
+                    choices=["batched_paged_decode", "single_decode", "prefill", "multi_depth",
+                             "pool_build"])
     ap.add_argument("--nsplit", type=int, default=None)
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -330,6 +331,91 @@ def bench_multi_depth(args):
     print(json.dumps(out), flush=True)
 
 
+def bench_pool_build(args):
+    """Library pool build from document caches: the batched-decode page set (64 documents of
+    U{8..64} chunks x 512 slots, ragged tails, d_s = 2048) as back-to-back fp16 slot rows already
+    in HBM, centred by a seeded mu; one step = one xenc_build_pages launch writing the fp16 pages,
+    fp32 summary keys and valid counts.  Algorithmic bytes per launch: the slot rows read once
+    (R x d x 2) plus the pages (C x 512 x d x 2, zero tails included), S (C x d x 4) and counts."""
+    from kv_skill_v2_amd import ops, synth
+
+    dev = torch.device("cuda:0")
+    P, _, _, _ = synth.decode_workload("batched_paged_decode", device=dev)
+    C, N, d = len(P.nvalid), P.pages.shape[1], P.pages.shape[2]
+    by_chunk = P.pages[P.chunk_page.long()]                   # chunk order
+    keep = torch.arange(N, device=dev).view(1, N) < P.chunk_nvalid.view(-1, 1)
+    rows = by_chunk[keep].contiguous()                         # [R, d] fp16, chunks back to back
+    off = torch.zeros(C + 1, dtype=torch.int64, device=dev)
+    off[1:] = torch.cumsum(P.chunk_nvalid.long(), 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(11)
+    mu = (0.05 * torch.randn(d, generator=gen, device=dev)).contiguous()
+    del by_chunk, keep
+    R = rows.shape[0]
+    alg_bytes = R * d * 2 + C * N * d * 2 + C * d * 4 + C * 4 + (C + 1) * 8 + d * 4
+    for _ in range(args.warmup):
+        out = ops.build_pages(rows, off, d, N, d, mu)
+    del out
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        ev[i][0].record(stream)
+        out = ops.build_pages(rows, off, d, N, d, mu)
+        ev[i][1].record(stream)
+        del out
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    k_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    achieved = alg_bytes / (k_ms * 1e-3) / 1e9
+    # Read + write ceiling for reference: torch's device copy of the slot rows (same order of
+    # bytes read and written as the build).
+    dst = torch.empty_like(rows)
+    cev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(5)]
+    for a, b in cev:
+        a.record(stream)
+        dst.copy_(rows)
+        b.record(stream)
+    torch.cuda.synchronize()
+    copy_gbs = 2 * rows.numel() * 2 / (statistics.mean(a.elapsed_time(b) for a, b in cev[1:]) * 1e-3) / 1e9
+    del dst
+
+    cpu = None
+    if args.cpu_sample > 0:
+        import oracle as O
+        torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+        nc = sum(P.n_chunks[:8])
+        r_cpu = rows[: int(off[nc])].cpu()
+        o = off[: nc + 1].cpu().tolist()
+        chunk_rows = [r_cpu[o[c]:o[c + 1]] for c in range(nc)]
+        mu_c = mu.cpu()
+        t0 = time.perf_counter()
+        for g in range(8):
+            a, b = sum(P.n_chunks[:g]), sum(P.n_chunks[:g + 1])
+            O.library_tensors(chunk_rows[a:b], dtype=torch.float32, center_mu=mu_c)
+        cpu_s = time.perf_counter() - t0
+        cpu = {"value": nc / cpu_s, "unit": "chunks/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": (f"documents 0-7 ({nc} chunks x {N} slots x {d}), fp32 Library padding + "
+                          f"centring + summaries in the reference's operation order, one pass "
+                          f"({cpu_s:.2f} s); CPU oracle on {cpu_model()}")}
+    out = {
+        "metric": "Library pool build from document caches: chunks/s and HBM GB/s (% peak)",
+        "value": C / (k_ms * 1e-3), "unit": "chunks/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32 (fp16 in/out)", "data": "synthetic",
+        "config": {"workload": "pool_build", "documents": len(P.n_chunks), "chunks": C,
+                   "slot_rows": R, "slots_per_page": N, "d_s": d, "centred": True},
+        "roofline": {"bound": "hbm", "kernel": "build_pages_kernel", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": None, "algorithmic_bytes": alg_bytes, "avg_launch_ms": k_ms,
+                     "device_copy_gbs": copy_gbs},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -343,6 +429,8 @@ def main():
         return bench_prefill(args)
     if args.workload == "multi_depth":
         return bench_multi_depth(args)
+    if args.workload == "pool_build":
+        return bench_pool_build(args)
     from kv_skill_v2_amd import ops, synth
 
     dev = torch.device("cuda:0")

@@ -17,6 +17,11 @@ namespace {
 constexpr int kPoolWaves = 8;
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 
+// Rows per wave per step, their loads issued together: more for narrow rows, fewer where the
+// registers of wide rows would spill.
+template <int CB>
+constexpr int pool_rows() { return CB <= 2 ? 4 : (CB <= 6 ? 2 : 1); }
+
 template <int CB>
 __global__ __launch_bounds__(kPoolWaves * kWave) void build_pages_kernel(
     const _Float16* __restrict__ rows, const long long* __restrict__ row_off, int d,
@@ -39,40 +44,59 @@ __global__ __launch_bounds__(kPoolWaves * kWave) void build_pages_kernel(
     }
   }
   _Float16* page = pages + (long long)c * page_stride;
-  for (int t = wv; t < N; t += kPoolWaves) {
-    float x[CB][8];
-    const bool valid = t < n;
+  constexpr int kRows = pool_rows<CB>();
+  // kRows rows per wave per step (t, t + kPoolWaves, ...): all their loads are issued before any
+  // is used, multiplying the bytes in flight.  Rows are read once and pages written once, so both
+  // go around the caches (nontemporal).
+  for (int t0 = wv; t0 < N; t0 += kRows * kPoolWaves) {
+    half8_t h[kRows][CB];
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const int d0 = (cb * kWave + lane) * 8;
-      half8_t h = {};
-      if (valid && d0 < d) h = *reinterpret_cast<const half8_t*>(rows + (r0 + t) * d + d0);
+    for (int u = 0; u < kRows; ++u) {
+      const int t = t0 + u * kPoolWaves;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[cb][e] = (valid && d0 + e < d) ? (float)h[e] - mv[cb][e] : 0.f;
-    }
-    if (mu) {   // centre and renormalise the valid row
-      float ss = 0.f;
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss = fmaf(x[cb][e], x[cb][e], ss);
-      const float inv = 1.f / (sqrtf(wave_sum(ss)) + 1e-6f);
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[cb][e] *= inv;
+      for (int cb = 0; cb < CB; ++cb) {
+        const int d0 = (cb * kWave + lane) * 8;
+        h[u][cb] = half8_t{};
+        if (t < n && d0 < d)
+          h[u][cb] = __builtin_nontemporal_load(reinterpret_cast<const half8_t*>(rows + (r0 + t) * d + d0));
+      }
     }
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb) {
-      const int d0 = (cb * kWave + lane) * 8;
-      if (d0 < d_pad) {
-        half8_t o;
+    for (int u = 0; u < kRows; ++u) {
+      const int t = t0 + u * kPoolWaves;
+      if (t >= N) break;   // wave-uniform
+      float x[CB][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          o[e] = (_Float16)x[cb][e];
-          sum[cb][e] += x[cb][e];
+      for (int cb = 0; cb < CB; ++cb) {
+        const int d0 = (cb * kWave + lane) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          x[cb][e] = (t < n && d0 + e < d) ? (float)h[u][cb][e] - mv[cb][e] : 0.f;
+      }
+      if (mu) {   // centre and renormalise the valid row
+        float ss = 0.f;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = fmaf(x[cb][e], x[cb][e], ss);
+        const float inv = 1.f / (sqrtf(wave_sum(ss)) + 1e-6f);
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[cb][e] *= inv;
+      }
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        const int d0 = (cb * kWave + lane) * 8;
+        if (d0 < d_pad) {
+          half8_t o;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            o[e] = (_Float16)x[cb][e];
+            sum[cb][e] += x[cb][e];
+          }
+          __builtin_nontemporal_store(o, reinterpret_cast<half8_t*>(page + (long long)t * d_pad + d0));
         }
-        *reinterpret_cast<half8_t*>(page + (long long)t * d_pad + d0) = o;
       }
     }
   }

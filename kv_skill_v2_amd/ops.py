@@ -29,6 +29,31 @@ def _i32(x, device) -> torch.Tensor:
     return torch.as_tensor(x, dtype=torch.int32, device=device).contiguous()
 
 
+def build_pages(rows: torch.Tensor, row_off: torch.Tensor, d: int, slots_per_page: int, d_pad: int,
+                mu: torch.Tensor | None = None):
+    """xenc_build_pages on device-resident input: rows fp16 [R, d] (chunk c = rows
+    row_off[c] .. row_off[c+1]-1, row_off int64 [C+1]) -> (pages fp16 [C, slots_per_page, d_pad],
+    S fp32 [C, d_pad], nvalid int32 [C]), centring by mu fp32 [d] when given.  The caller
+    guarantees every chunk has 1 .. slots_per_page rows."""
+    for t, name in ((rows, "rows"), (row_off, "row_off")):
+        _require_device(t, name)
+    if rows.dtype != torch.float16 or rows.dim() != 2 or rows.shape[1] != d or not rows.is_contiguous():
+        raise ValueError(f"rows must be contiguous fp16 [R, {d}]")
+    if row_off.dtype != torch.int64 or row_off.dim() != 1 or not row_off.is_contiguous():
+        raise ValueError("row_off must be contiguous int64 [C+1]")
+    if mu is not None and (mu.dtype != torch.float32 or mu.shape != (d,) or not mu.is_contiguous()):
+        raise ValueError(f"mu must be contiguous fp32 [{d}]")
+    C = row_off.numel() - 1
+    dev = rows.device
+    pages = torch.empty(C, slots_per_page, d_pad, dtype=torch.float16, device=dev)
+    S = torch.empty(C, d_pad, dtype=torch.float32, device=dev)
+    nv = torch.empty(C, dtype=torch.int32, device=dev)
+    check(lib().xenc_build_pages(ptr(rows), ptr(row_off), C, d, ptr(mu), slots_per_page, d_pad,
+                                 ptr(pages), slots_per_page * d_pad, ptr(S), d_pad, ptr(nv),
+                                 stream_handle(dev)), "xenc_build_pages")
+    return pages, S, nv
+
+
 @dataclass
 class PagedLibrary:
     """Device layout of one or more Libraries (see include/xenc_hip.h)."""
@@ -184,21 +209,15 @@ class PagedLibrary:
         for c in n:
             off.append(off[-1] + c)
         off_d = torch.tensor(off, dtype=torch.int64, device=device)
-        stream = stream_handle(device)
 
-        def build(src, centre):
-            flat = torch.cat([r.to(torch.float16) for r in src]).to(device).contiguous()
-            pages = torch.empty(Ctot, N, dp, dtype=torch.float16, device=device)
-            S = torch.empty(Ctot, dp, dtype=torch.float32, device=device)
-            nv = torch.empty(Ctot, dtype=torch.int32, device=device)
-            check(lib().xenc_build_pages(ptr(flat), ptr(off_d), Ctot, d, ptr(centre), N, dp, ptr(pages),
-                                         N * dp, ptr(S), dp, ptr(nv), stream), "xenc_build_pages")
-            return pages, S, nv
+        def flat(src):
+            return torch.cat([r.to(torch.float16) for r in src]).to(device).contiguous()
 
-        pages, S, nv = build(rows, mu)
+        pages, S, nv = build_pages(flat(rows), off_d, d, N, dp, mu)
         values = None
         if any(v is not None for v in vrows):
-            values = build([v if v is not None else k for v, k in zip(vrows, rows)], None)[0]
+            values = build_pages(flat([v if v is not None else k for v, k in zip(vrows, rows)]), off_d,
+                                 d, N, dp)[0]
         ptr_ = [0]
         for c in nch:
             ptr_.append(ptr_[-1] + c)
