@@ -138,7 +138,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
     const int* __restrict__ chunk_nvalid, float temp, const float* __restrict__ w, long long ldw,
     _Float16* __restrict__ P, long long p_rows, _Float16* __restrict__ dS,
     float* __restrict__ gamma, long long ldg) {
-  __shared__ _Float16 lB[2][kRowsPerTile * BK];  // X tile [128][64], two stages (32 KiB)
+  __shared__ _Float16 lB[3][kRowsPerTile * BK];  // X tile [128][64], three stages (48 KiB)
   __shared__ float red[8][kRowsPerTile];          // per-wave row statistics
 
   const int b = xcd_remap(blockIdx.x, gridDim.x);
@@ -200,13 +200,21 @@ __global__ __launch_bounds__(512) void scores_kernel(
   // One k-step on LDS stage st.  The scheduling barriers keep every global load where it is
   // written: the compiler otherwise sinks them next to their first use and each k-step waits
   // out a full memory latency.
+  // fb0: the first k16 step's B fragments of the coming k-step, read from LDS before the barrier
+  // that ends the previous k-step, so the MFMAs start as soon as the barrier releases.
+  half8_t fb0[4];
+  auto read_fb0 = [&](int st) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+      fb0[nt] = *reinterpret_cast<const half8_t*>(&lB[st][swz(nt * 32 + l32, hl)]);
+  };
   auto compute = [&](int st, int knext) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       half8_t fb[4];
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
-        fb[nt] = *reinterpret_cast<const half8_t*>(&lB[st][swz(nt * 32 + l32, ks * 2 + hl)]);
+        fb[nt] = ks == 0 ? fb0[nt] : *reinterpret_cast<const half8_t*>(&lB[st][swz(nt * 32 + l32, ks * 2 + hl)]);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -224,15 +232,23 @@ __global__ __launch_bounds__(512) void scores_kernel(
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) fa[mt][ks] = *reinterpret_cast<const half8_t*>(abase[mt] + ks * 512);
+  // Three LDS stages: k-step k reads stage k % 3 while the rows of step k + 2 are stored into
+  // stage (k + 2) % 3 (last read in step k - 1, before the barrier that ended it) and the first
+  // fragments of step k + 1 are read from stage (k + 1) % 3 (stored in step k - 1, before that
+  // same barrier).  One barrier per k-step.
   load_b(0);
   store_b(0);
+  load_b(min(1, nk - 1) * BK);
+  store_b(1);
   __syncthreads();
+  read_fb0(0);
   for (int k = 0; k < nk; ++k) {
     const int k1 = min(k + 1, nk - 1) * BK;
-    load_b(k1);
+    load_b(min(k + 2, nk - 1) * BK);
     __builtin_amdgcn_sched_barrier(0);
-    compute(k & 1, k1);
-    store_b((k + 1) & 1);  // that stage was last read before the previous barrier
+    compute(k % 3, k1);
+    store_b((k + 2) % 3);
+    read_fb0((k + 1) % 3);
     __syncthreads();
   }
 
@@ -401,7 +417,7 @@ __global__ __launch_bounds__(256) void readout_kernel(
     long long page_stride, const int* __restrict__ chunk_ptr, const int* __restrict__ chunk_page,
     const float* __restrict__ w, long long ldw, float* __restrict__ out, long long ldo) {
   constexpr int RT = kReadoutRows;
-  __shared__ _Float16 lA[2][RT * BK];
+  __shared__ _Float16 lA[3][RT * BK];
 
   const int b = xcd_remap(blockIdx.x, gridDim.x);
   const int g = find_group(tile_ptr, G, b);
@@ -467,12 +483,21 @@ __global__ __launch_bounds__(256) void readout_kernel(
   for (int mt = 0; mt < NA; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = (f32x16){};
+  // fa0: the first k16 step's A fragments of the coming k-step, read before the barrier that
+  // ends the previous k-step (as in the scores kernel).
+  half8_t fa0[NA];
+  auto read_fa0 = [&](int st) {
+#pragma unroll
+    for (int mt = 0; mt < NA; ++mt)
+      fa0[mt] = *reinterpret_cast<const half8_t*>(&lA[st][swz(mt * 32 + l32, hl)]);
+  };
   auto compute = [&](int st, const _Float16* kbn, int nbn) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
 #pragma unroll
       for (int mt = 0; mt < NA; ++mt) {
-        const half8_t fa = *reinterpret_cast<const half8_t*>(&lA[st][swz(mt * 32 + l32, ks * 2 + hl)]);
+        const half8_t fa =
+            ks == 0 ? fa0[mt] : *reinterpret_cast<const half8_t*>(&lA[st][swz(mt * 32 + l32, ks * 2 + hl)]);
 #pragma unroll
         for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(fa, fb[nt][ks], acc[mt][nt]);
       }
@@ -493,16 +518,27 @@ __global__ __launch_bounds__(256) void readout_kernel(
       for (int ks = 0; ks < 4; ++ks)
         fb[nt][ks] = *reinterpret_cast<const half8_t*>(kb0 + ((long long)dbk[nt] * (N / 16) + ks) * 512);
   }
+  // Three LDS stages, as in the scores kernel: step it reads stage it % 3, stores the rows of
+  // step it + 2 into stage (it + 2) % 3 and reads the first fragments of step it + 1 from stage
+  // (it + 1) % 3 before its barrier.
   load_a(0, 0);
   store_a(0);
+  {
+    const int n1 = min(1, total - 1);
+    load_a(n1 / kpc, (n1 % kpc) * BK);
+    store_a(1);
+  }
   __syncthreads();
+  read_fa0(0);
   for (int it = 0; it < total; ++it) {
     const int nx = min(it + 1, total - 1);  // the prefetch past the last step re-reads it
     const int cn = nx / kpc, nn = (nx % kpc) * BK;
-    load_a(cn, nn);
+    const int n2 = min(it + 2, total - 1);
+    load_a(n2 / kpc, (n2 % kpc) * BK);
     __builtin_amdgcn_sched_barrier(0);
-    compute(it & 1, kb_base(cn), nn / 16);
-    store_a((it + 1) & 1);
+    compute(it % 3, kb_base(cn), nn / 16);
+    store_a((it + 2) % 3);
+    read_fa0((it + 1) % 3);
     __syncthreads();
   }
   // acc[mt][nt][r] = out[row0 + 32mt + 8(r/4) + 4hl + r%4][d0 + 64w + 32nt + l32]
