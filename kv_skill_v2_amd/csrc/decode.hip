@@ -15,6 +15,12 @@
 // keeps its own online-softmax state (max, sum, acc[8*CB]); the NW waves merge through LDS and
 // the workgroup writes one partial (acc[d], max, sum).
 //
+// Shared libraries (more query rows than libraries): the (row, routed chunk) entries are first
+// ranked by page (page_order_kernel) and the units run in that order, XCD-major: the rows that
+// routed the same page then read it on the same XCD at the same time, and all but the first
+// reader are served by that XCD's L2.  Partials keep their logical index, so the merge and the
+// result do not depend on the order.
+//
 // Merge (merge_query): the k*nsplit partials of a query are combined by log-sum-exp, chunk j
 // scaled by w[j] / l_j, and summed in (j, s) order — a fixed order, so results are
 // deterministic.  Launches of >= kTwoPassUnits workgroups run it as a second kernel, one
@@ -75,6 +81,7 @@ __device__ __forceinline__ void wave_reduce_scatter(float (&v)[SPT], int lane) {
 
 struct DecodeWorkspace {
   int* counters;    // [max_rows] arrivals per query (0 between calls; in-kernel merge only)
+  int* order;       // [M * kk]   (row, routed chunk) entries ranked by page (page-grouped runs)
   float2* part_ml;  // [units]    (max in log2 units, sum) per partial; sum 0 = empty
   float* part_acc;  // [units, d] un-normalised value sums
 };
@@ -273,14 +280,18 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
     const int* __restrict__ chunk_nvalid, const int* __restrict__ chunk_ptr,
     const int* __restrict__ q_group, int G, const int* __restrict__ idx,
     const float* __restrict__ w_sel, int kk, int nsplit, int split_slots, float scale2,
-    int softmax, float* __restrict__ r, long long ldr, DecodeWorkspace ws, int fused_merge) {
+    int softmax, float* __restrict__ r, long long ldr, DecodeWorkspace ws, int fused_merge,
+    int grouped) {
   extern __shared__ float red[];  // [NW/2][d] wave-merge tree; reused by the merge
   __shared__ float wml[NW][2];
   __shared__ int is_last;
 
-  const int unit = blockIdx.x;
-  const int s = unit % nsplit;
-  const int mj = unit / nsplit;
+  // Launch position -> logical unit: in page-grouped runs the XCD-major position indexes the
+  // page-ranked entries; otherwise the unit is the block index.
+  const int pos = grouped ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
+  const int s = pos % nsplit;
+  const int mj = grouped ? ws.order[pos / nsplit] : pos / nsplit;
+  const int unit = mj * nsplit + s;
   const int m = mj / kk;
   const int lane = threadIdx.x & (kWave - 1);
   // Wave index as a provably uniform value, so row offsets stay in SGPRs (buffer soffset).
@@ -446,6 +457,33 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
   if (threadIdx.x == 0) atomicExch(&ws.counters[m], 0);  // re-arm for the next call
 }
 
+// Page-grouped runs: entry i = (row i / kk, routed chunk i % kk) of the n = M * kk entries gets
+// its rank among the entries ordered by (page, i); unrouted entries sort last.  One workgroup;
+// n <= kOrderMax, so each thread ranks at most one entry by a scan over the LDS keys.
+constexpr int kOrderMax = 1024;
+__global__ __launch_bounds__(kOrderMax) void page_order_kernel(
+    const int* __restrict__ idx, const int* __restrict__ q_group, const int* __restrict__ chunk_ptr,
+    const int* __restrict__ chunk_page, int G, int kk, int n, int* __restrict__ order) {
+  __shared__ int key[kOrderMax];
+  const int i = threadIdx.x;
+  if (i < n) {
+    const int g = min(max(q_group[i / kk], 0), G - 1);
+    const int cbeg = chunk_ptr[g];
+    const int cl = idx[i];
+    key[i] = (cl >= 0 && cl < chunk_ptr[g + 1] - cbeg) ? chunk_page[cbeg + cl] : 0x7fffffff;
+  }
+  __syncthreads();
+  if (i < n) {
+    const int ki = key[i];
+    int rank = 0;
+    for (int j = 0; j < n; ++j) {
+      const int kj = key[j];
+      rank += (kj < ki || (kj == ki && j < i)) ? 1 : 0;
+    }
+    order[rank] = i;
+  }
+}
+
 // Second pass of a large launch: one workgroup per query row merges its partials (the same
 // merge_query, so the result is bit-identical to the in-kernel merge).
 __global__ __launch_bounds__(512) void merge_kernel(DecodeWorkspace ws, const int* __restrict__ idx,
@@ -462,7 +500,8 @@ __global__ void fill_zero_kernel(int* p, int n) {
 
 static size_t host_align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Workspace: [counters: max_rows ints, 256-B aligned | (m, l) per partial | acc per partial].
+// Workspace: [counters: max_rows ints | page order: M * kk ints | (m, l) per partial | acc per
+// partial], each region 256-B aligned.
 // The counter region depends only on the capacity max_rows, never on the call's row count, so
 // counters zeroed once stay in place (and zero) whatever sizes later calls use.
 static DecodeWorkspace carve(void* base, int max_rows, int M, int kk, int nsplit) {
@@ -471,6 +510,8 @@ static DecodeWorkspace carve(void* base, int max_rows, int M, int kk, int nsplit
   DecodeWorkspace ws;
   ws.counters = reinterpret_cast<int*>(p);
   p += host_align256((size_t)max_rows * sizeof(int));
+  ws.order = reinterpret_cast<int*>(p);
+  p += host_align256((size_t)M * kk * sizeof(int));
   ws.part_ml = reinterpret_cast<float2*>(p);
   p += host_align256(units * sizeof(float2));
   ws.part_acc = reinterpret_cast<float*>(p);
@@ -483,12 +524,13 @@ static void launch_read(dim3 grid, size_t lds, hipStream_t st, const float* q, l
                         const int* chunk_page, const int* chunk_nvalid, const int* chunk_ptr,
                         const int* q_group, int G, const int* idx, const float* w_sel, int kk,
                         int nsplit, int split_slots, float scale2, int softmax, float* r,
-                        long long ldr, const DecodeWorkspace& ws, int fused_merge) {
+                        long long ldr, const DecodeWorkspace& ws, int fused_merge, int grouped) {
   constexpr int NW = XENC_DECODE_NW;
   constexpr int SPT = CB <= 4 ? XENC_DECODE_SPT : (CB == 5 ? XENC_DECODE_SPT_WIDE : 1);
   hipLaunchKernelGGL((decode_read_kernel<CB, SPT, NW>), grid, dim3(NW * kWave), lds, st, q, ldq,
                      d, pages, page_stride, spp, chunk_page, chunk_nvalid, chunk_ptr, q_group, G,
-                     idx, w_sel, kk, nsplit, split_slots, scale2, softmax, r, ldr, ws, fused_merge);
+                     idx, w_sel, kk, nsplit, split_slots, scale2, softmax, r, ldr, ws, fused_merge,
+                     grouped);
 }
 
 // Launches of at least this many workgroups merge in a second kernel; smaller ones (few query
@@ -499,14 +541,14 @@ constexpr long long kTwoPassUnits = 256;
 
 using namespace xenc;
 
-static size_t workspace_need(int max_rows, long long units, int d) {
-  return host_align256((size_t)max_rows * sizeof(int)) + host_align256(units * sizeof(float2)) +
-         host_align256(units * d * sizeof(float));
+static size_t workspace_need(int max_rows, long long entries, long long units, int d) {
+  return host_align256((size_t)max_rows * sizeof(int)) + host_align256(entries * sizeof(int)) +
+         host_align256(units * sizeof(float2)) + host_align256(units * d * sizeof(float));
 }
 
 extern "C" size_t xenc_decode_workspace_bytes(int max_rows, int kk, int nsplit, int d) {
   if (max_rows <= 0 || kk <= 0 || nsplit <= 0 || d <= 0) return 0;
-  return workspace_need(max_rows, (long long)max_rows * kk * nsplit, d);
+  return workspace_need(max_rows, (long long)max_rows * kk, (long long)max_rows * kk * nsplit, d);
 }
 
 extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int max_rows,
@@ -544,7 +586,7 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
     return XENC_EALIGN;
   const long long units = (long long)M * kk * nsplit;
   if (units > 0x7fffffffLL) return XENC_EINVAL;
-  if (workspace_bytes < workspace_need(max_rows, units, d)) return XENC_EWORKSPACE;
+  if (workspace_bytes < workspace_need(max_rows, (long long)M * kk, units, d)) return XENC_EWORKSPACE;
   // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
   const size_t lds =
       std::max((size_t)std::max(XENC_DECODE_NW / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
@@ -552,10 +594,16 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
 
   const DecodeWorkspace ws = carve(workspace, max_rows, M, kk, nsplit);
   const int fused = units < kTwoPassUnits ? 1 : 0;
+  // Page-grouped runs when rows share libraries and there are enough entries to matter.
+  const long long entries = (long long)M * kk;
+  const int grouped = (M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
   const int split_slots = (slots_per_page + nsplit - 1) / nsplit;
   const float scale2 = read_temp * kLog2e;
   const _Float16* pg = static_cast<const _Float16*>(pages);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (grouped)
+    hipLaunchKernelGGL(page_order_kernel, dim3(1), dim3(kOrderMax), 0, st, idx, q_group,
+                       chunk_ptr, chunk_page, G, kk, (int)entries, ws.order);
   const dim3 grid((unsigned)units);
   const int cb = (d + 511) / 512;
   switch (cb) {
@@ -563,7 +611,7 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
   case N:                                                                                      \
     launch_read<N>(grid, lds, st, q, ldq, d, pg, page_stride, slots_per_page, chunk_page,      \
                    chunk_nvalid, chunk_ptr, q_group, G, idx, w_sel, kk, nsplit, split_slots,   \
-                   scale2, softmax, r, ldr, ws, fused);                                        \
+                   scale2, softmax, r, ldr, ws, fused, grouped);                               \
     break;
     XENC_CASE(1) XENC_CASE(2) XENC_CASE(3) XENC_CASE(4)
     XENC_CASE(5) XENC_CASE(6) XENC_CASE(7) XENC_CASE(8)

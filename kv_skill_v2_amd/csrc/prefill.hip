@@ -51,17 +51,6 @@ __device__ __forceinline__ f32x16 mfma32(const half8_t& a, const half8_t& b, con
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Tile b is
-// remapped so that XCD x runs a contiguous range of logical tiles; the logical order then puts
-// tiles that share operands next to each other, so the workgroups resident on one XCD at a time
-// hit in that XCD's L2 instead of re-reading HBM.  A bijection on [0, n).
-constexpr int kXcds = 8;
-__device__ __forceinline__ int xcd_remap(int b, int n) {
-  const int x = b % kXcds, j = b / kXcds;
-  const int per = (n + kXcds - 1) / kXcds, rem = n % kXcds;
-  const int start = rem == 0 ? x * per : x * per - max(0, x - rem);
-  return start + j;
-}
 constexpr int kChunkGroup = 4;  // scores tiles: chunks per group, all row tiles of a group adjacent
 
 // Library g of tile b: tile_ptr[g] <= b < tile_ptr[g+1] (binary search; G is small).

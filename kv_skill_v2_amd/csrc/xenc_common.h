@@ -51,4 +51,16 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Tile b is
+// remapped so that XCD x runs a contiguous range of logical tiles; the logical order then puts
+// tiles that share operands next to each other, so the workgroups resident on one XCD at a time
+// hit in that XCD's L2 instead of re-reading HBM.  A bijection on [0, n).
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_remap(int b, int n) {
+  const int x = b % kXcds, j = b / kXcds;
+  const int per = (n + kXcds - 1) / kXcds, rem = n % kXcds;
+  const int start = rem == 0 ? x * per : x * per - max(0, x - rem);
+  return start + j;
+}
+
 }  // namespace xenc

@@ -129,6 +129,40 @@ def test_nsplit_invariance_and_page_relabel(dev):
     assert torch.equal(r2, rs[1]), "page relabelling must not change a single bit"
 
 
+@pytest.mark.parametrize("M,top_k,nsplit", [(40, 6, 2), (100, 8, 1), (24, 8, 3)])
+def test_page_grouped_runs(dev, M, top_k, nsplit):
+    """Rows sharing libraries with >= 128 (row, chunk) entries run page-grouped (entries ranked
+    by page, XCD-major).  The result must match the oracle and be bit-identical to the same rows
+    read one call per row (never grouped) and to a relabelled page pool (a different order)."""
+    say("page-grouped", dict(M=M, top_k=top_k, nsplit=nsplit))
+    d = 512
+    P = synth.pool([24, 16], 128, d, device="cpu", tail_lo=1)
+    lib = _to_lib(P, dev)
+    groups = [m % 2 for m in range(M)]
+    q = synth.queries(M, d, device="cpu", seed=21)
+    qg = torch.tensor(groups, dtype=torch.int32, device=dev)
+    _, idx, wsel = ops.route_topk(q.to(dev), lib, qg, top_k=top_k)
+    r = ops.library_read_decode(q.to(dev), lib, idx, wsel, qg, nsplit=nsplit)
+    single = torch.stack([ops.library_read_decode(q[m:m + 1].to(dev), lib, idx[m:m + 1], wsel[m:m + 1],
+                                                  qg[m:m + 1], nsplit=nsplit)[0] for m in range(M)])
+    assert torch.equal(r, single)
+    perm = torch.randperm(P.pages.shape[0], generator=torch.Generator().manual_seed(2))
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(perm.numel())
+    lib2 = ops.PagedLibrary(lib.pages[perm.to(dev)].contiguous(),
+                            inv.to(dev).int()[lib.chunk_page.long()].contiguous(), lib.chunk_nvalid,
+                            lib.chunk_ptr, lib.S, n_chunks=lib.n_chunks, nvalid=lib.nvalid)
+    assert torch.equal(ops.library_read_decode(q.to(dev), lib2, idx, wsel, qg, nsplit=nsplit), r)
+    idx_c, wsel_c = idx.cpu(), wsel.cpu()
+    for m, g in enumerate(groups):
+        K, Mk, _ = P.library(g)
+        kept = [c for c in idx_c[m].tolist() if c >= 0]
+        w = torch.zeros(1, 1, K.shape[0], dtype=torch.float64)
+        w[0, 0, kept] = wsel_c[m, :len(kept)].double()
+        ref, _ = O.read(q[m].view(1, 1, -1).double(), K.double(), Mk, w, 12.0)
+        _check_close(r[m], ref.view(-1), f"row {m} (library {g})")
+
+
 def test_read_is_linear_in_route_weights(dev):
     say("linearity in w", dict(d=256))
     P = synth.pool([5, 5], 64, 256, device="cpu")
