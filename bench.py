@@ -199,7 +199,8 @@ def bench_multi_depth(args):
     of 32 tokens; the selector keeps the top-2 depths per token (seeded logits), so 64 (token,
     depth) query rows are routed (top-8 chunks of their depth) and read in ONE route and ONE read
     launch (the depth is the row's library).  Each read is written back through its depth's
-    B [5120, 2560] fp32 (one padded batched GEMM reads every B once), times gate and gain, then
+    B [5120, 2560] fp32 with gate and gain folded in (one xenc_write_back launch streams the B of
+    every selected depth once), then
     rescaled to the selector's matched norm and weighted.  The unselected depths are not read (the
     reference reads all 8 and multiplies 6 by zero).  Step = everything after the selector logits;
     the two updates of a token (one per selected depth, applied at different layers in a model)
@@ -212,6 +213,8 @@ def bench_multi_depth(args):
     c = synth.MULTI_DEPTH
     dev = torch.device("cuda:0")
     P, z, q_all, h, BwT = synth.multi_depth_workload(dev)
+    Bw = BwT.transpose(1, 2).contiguous()                            # [L, d_r, d] out-major rows
+    del BwT
     lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
                            n_chunks=P.n_chunks, nvalid=P.nvalid)
     B, L, d, dr, k = c["B"], c["depths"], c["d"], c["d_r"], c["top_k"]
@@ -231,11 +234,8 @@ def bench_multi_depth(args):
             qr = q_all[ql, bidx]                                      # [64, d]
             _, idx, wsel = ops.route_topk(qr, lib, qg, top_k=k)
             r = ops.library_read_decode(qr, lib, idx, wsel, qg)
-            rp = torch.zeros(L, B, d, device=dev)
-            rp[ql, bidx] = r
-            dl = torch.bmm(rp, BwT)[ql, bidx]                         # [64, d_r]
-            g = torch.sigmoid(hn[bidx] @ gate_w + gate_b[ql]).unsqueeze(-1)
-            dl = torch.exp(log_gain[ql]).unsqueeze(-1) * g * dl
+            g = torch.sigmoid(hn[bidx] @ gate_w + gate_b[ql])
+            dl = ops.write_back(r, Bw, qg, None, torch.exp(log_gain[ql]) * g)   # [64, d_r]
             hb = h[bidx]
             rel = dl.norm(dim=-1, keepdim=True) / (hb.norm(dim=-1, keepdim=True) + 1e-6)
             dl = dl / (rel + 1e-6) * sel.log_alpha.exp() * wsl[bidx, ql].unsqueeze(-1)
@@ -298,7 +298,7 @@ def bench_multi_depth(args):
         K, M, S = P.library(0)
         K, M, S = K.cpu(), M.cpu(), S.cpu()
         ql0 = q_all[0].cpu().view(B, 1, d)
-        Bw0 = BwT[0].cpu().t().contiguous()
+        Bw0 = Bw[0].cpu()
         hc = h.cpu().view(B, 1, dr)
         O.branch_read(ql0[:1], K, M, S, top_k=k)                       # warm-up
         t0 = time.perf_counter()
@@ -321,7 +321,7 @@ def bench_multi_depth(args):
                    "slots_per_page": c["N"], "d_s": d, "d_reader": dr, "batch": B,
                    "selector_top_k": c["k_sel"], "top_k": k, "B_dtype": "fp32", "accumulate": "fp32",
                    "hip_graph": bool(graph_ok), "ms_per_step_eager": ms_eager},
-        "roofline": {"bound": "hbm", "kernel": "whole step (route + read + B GEMM + epilogue)",
+        "roofline": {"bound": "hbm", "kernel": "whole step (route + read + write-back + epilogue)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "algorithmic_bytes": bytes_step, "unique_routed_pages": len(pages),

@@ -148,6 +148,26 @@ int xenc_route_backward(const float* w, long long ldw, const float* dw_read, lon
                         void* stream);
 
 /*
+ * ---- Write-back through the interface's B (decode path)
+ *   out[m, o] = row_scale[m] * (sum_k W_g[o, k] r[m, k] + bias_g[o]),  g = row_group[m]
+ * r fp32 [M, ldr] (the read, d columns); W fp32: library g's [d_out, d] weight (out-major rows
+ * of ldw floats) at W + g * w_group_stride; bias (optional) fp32 d_out floats at
+ * bias + g * bias_group_stride (0 = one bias for all libraries); row_scale (optional) fp32 [M]:
+ * gain_scale * exp(log_gain) * gate of each row; row_group (optional, NULL = all rows in
+ * library 0) int32 [M], clamped to [0, G).  out fp32 [M, ldo].  M <= 4096, G <= 1024,
+ * d % 4 == 0, ldr and ldw multiples of 4, r and W 16-byte aligned.  Each used library's W is
+ * streamed from HBM once per call: its rows are taken in batches of 8 whose workgroups read the
+ * same W rows side by side on one XCD (the later ones from L2); libraries with no rows are not
+ * read.  Deterministic.
+ * Replaces itf_write and the delta product of LibraryInjector._branch
+ * (xenc/injector.py:71-74, 266-267) on the decode path.
+ */
+int xenc_write_back(const float* r, long long ldr, int M, int d, const int* row_group, int G,
+                    const float* W, long long w_group_stride, long long ldw, int d_out,
+                    const float* bias, long long bias_group_stride, const float* row_scale,
+                    float* out, long long ldo, void* stream);
+
+/*
  * ---- Library pool build from a document cache
  * rows fp16 [R, d] holds the slot rows of C chunks back to back: chunk c is rows
  * row_off[c] .. row_off[c+1]-1 (int64 [C+1], device).  For each chunk, on fp32 values:

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lock = threading.Lock()
 _lib = None
@@ -50,6 +50,11 @@ SIGNATURES = {
     "xenc_fragment_pages": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p]),
     "xenc_build_pages": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p,
                                  c_longlong, c_void_p, c_longlong, c_void_p, c_void_p]),
+    "xenc_write_back": (c_int, [
+        c_void_p, c_longlong, c_int, c_int, c_void_p, c_int,  # r, ldr, M, d, row_group, G
+        c_void_p, c_longlong, c_longlong, c_int,     # W, w_group_stride, ldw, d_out
+        c_void_p, c_longlong, c_void_p,              # bias, bias_group_stride, row_scale
+        c_void_p, c_longlong, c_void_p]),            # out, ldo, stream
     "xenc_prefill_scores": (c_int, [
         c_int, c_void_p, c_int, c_void_p, c_void_p,  # mode, x, d, row_ptr, tile_ptr
         c_int, c_int, c_void_p, c_int, c_longlong,   # G, n_tiles, pages_a, slots_per_page, page_stride

@@ -56,29 +56,6 @@ constexpr int kBufferWord3 = 0x00020000;
 // against 6.2 TB/s without on MI355X.
 constexpr int kLoadNT = 2;
 
-// Reduce SPT per-lane partial values over the 64 lanes.  On return v[0] holds, in every lane,
-// the full sum for slot j = lane / (64 / SPT).  Step with lane bit MASK: lanes with the bit set
-// keep the upper half of the remaining values, send the lower half to their partner and add
-// what they receive.  Written as compile-time recursion so every array index is a constant.
-template <int SPT, int CNT = SPT, int MASK = 32>
-__device__ __forceinline__ void wave_reduce_scatter(float (&v)[SPT], int lane) {
-  static_assert(SPT >= 1 && SPT <= 64 && (SPT & (SPT - 1)) == 0, "SPT must be a power of 2");
-  if constexpr (CNT > 1) {
-    constexpr int H = CNT / 2;
-    const bool hi = (lane & MASK) != 0;
-#pragma unroll
-    for (int i = 0; i < H; ++i) {
-      const float send = hi ? v[i] : v[i + H];
-      const float keep = hi ? v[i + H] : v[i];
-      v[i] = keep + shfl_xor(send, MASK);
-    }
-    wave_reduce_scatter<SPT, H, MASK / 2>(v, lane);
-  } else if constexpr (MASK >= 1) {
-    v[0] += shfl_xor(v[0], MASK);
-    wave_reduce_scatter<SPT, 1, MASK / 2>(v, lane);
-  }
-}
-
 struct DecodeWorkspace {
   int* counters;    // [max_rows] arrivals per query (0 between calls; in-kernel merge only)
   int* order;       // [M * kk]   (row, routed chunk) entries ranked by page (page-grouped runs)
@@ -459,26 +436,40 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
 
 // Page-grouped runs: entry i = (row i / kk, routed chunk i % kk) of the n = M * kk entries gets
 // its rank among the entries ordered by (page, i); unrouted entries sort last.  One workgroup;
-// n <= kOrderMax, so each thread ranks at most one entry by a scan over the LDS keys.
+// n <= kOrderMax, so each thread ranks at most one entry by a scan over the LDS keys, read 16
+// keys per step (four 16-byte loads in flight).  Keys past n are padded with the largest key:
+// they rank after every entry, so they never count.
 constexpr int kOrderMax = 1024;
 __global__ __launch_bounds__(kOrderMax) void page_order_kernel(
     const int* __restrict__ idx, const int* __restrict__ q_group, const int* __restrict__ chunk_ptr,
     const int* __restrict__ chunk_page, int G, int kk, int n, int* __restrict__ order) {
-  __shared__ int key[kOrderMax];
+  __shared__ __align__(16) int key[kOrderMax];
   const int i = threadIdx.x;
+  int ki = 0x7fffffff;
   if (i < n) {
     const int g = min(max(q_group[i / kk], 0), G - 1);
     const int cbeg = chunk_ptr[g];
     const int cl = idx[i];
-    key[i] = (cl >= 0 && cl < chunk_ptr[g + 1] - cbeg) ? chunk_page[cbeg + cl] : 0x7fffffff;
+    if (cl >= 0 && cl < chunk_ptr[g + 1] - cbeg) ki = chunk_page[cbeg + cl];
   }
+  key[i] = ki;
   __syncthreads();
   if (i < n) {
-    const int ki = key[i];
+    const int n16 = (n + 15) & ~15;
+    const int4* k4 = reinterpret_cast<const int4*>(key);
     int rank = 0;
-    for (int j = 0; j < n; ++j) {
-      const int kj = key[j];
-      rank += (kj < ki || (kj == ki && j < i)) ? 1 : 0;
+    for (int j0 = 0; j0 < n16; j0 += 16) {
+      int4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = k4[j0 / 4 + u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int j = j0 + 4 * u;
+        rank += (v[u].x < ki || (v[u].x == ki && j + 0 < i)) ? 1 : 0;
+        rank += (v[u].y < ki || (v[u].y == ki && j + 1 < i)) ? 1 : 0;
+        rank += (v[u].z < ki || (v[u].z == ki && j + 2 < i)) ? 1 : 0;
+        rank += (v[u].w < ki || (v[u].w == ki && j + 3 < i)) ? 1 : 0;
+      }
     }
     order[rank] = i;
   }

@@ -44,6 +44,29 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Reduce SPT per-lane partial values over the 64 lanes.  On return v[0] holds, in every lane,
+// the full sum for slot j = lane / (64 / SPT).  Step with lane bit MASK: lanes with the bit set
+// keep the upper half of the remaining values, send the lower half to their partner and add
+// what they receive.  Written as compile-time recursion so every array index is a constant.
+template <int SPT, int CNT = SPT, int MASK = 32>
+__device__ __forceinline__ void wave_reduce_scatter(float (&v)[SPT], int lane) {
+  static_assert(SPT >= 1 && SPT <= 64 && (SPT & (SPT - 1)) == 0, "SPT must be a power of 2");
+  if constexpr (CNT > 1) {
+    constexpr int H = CNT / 2;
+    const bool hi = (lane & MASK) != 0;
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const float send = hi ? v[i] : v[i + H];
+      const float keep = hi ? v[i + H] : v[i];
+      v[i] = keep + shfl_xor(send, MASK);
+    }
+    wave_reduce_scatter<SPT, H, MASK / 2>(v, lane);
+  } else if constexpr (MASK >= 1) {
+    v[0] += shfl_xor(v[0], MASK);
+    wave_reduce_scatter<SPT, 1, MASK / 2>(v, lane);
+  }
+}
+
 // (value, index) order used by every top-k here: larger value first, then lower index.
 __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib) {
   return va > vb || (va == vb && ia < ib);

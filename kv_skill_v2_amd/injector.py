@@ -49,6 +49,35 @@ def _linear(mod: nn.Module, x: torch.Tensor) -> torch.Tensor:
     return F.linear(x, _on(mod.weight, x), b)
 
 
+# The fused write-back kernel serves the decode path (few rows, no autograd); many rows go to
+# the library GEMM, whose W reuse across rows the kernel does not have.
+_FUSED_WRITE_ROWS = 64
+
+
+def write_delta(itf, hn: torch.Tensor, r: torch.Tensor, li: int, gain_scale: float,
+                gcal=1.0) -> torch.Tensor:
+    """delta = gain_scale * gain * gcal * gate * B(r) (xenc/injector.py:266-267).  On the decode
+    path (a ModelInterface with an fp32 linear B, at most 64 rows, nothing requiring grad) the
+    product runs as one xenc_write_back launch: B streamed once with gate * gain folded into a
+    per-row scale."""
+    sc = gain_scale * itf_gain(itf, li, hn) * gcal * itf_gate(itf, hn, li)   # [..., 1] per row
+    Bm = getattr(itf, "B", None) if isinstance(itf, ModelInterface) else None
+    rows = r.numel() // r.shape[-1]
+    fused = (isinstance(Bm, nn.Linear) and r.is_cuda and r.dtype == torch.float32
+             and Bm.weight.dtype == torch.float32 and rows <= _FUSED_WRITE_ROWS
+             and r.shape[-1] % 4 == 0 and sc.shape[-1] == 1
+             and not (torch.is_grad_enabled() and (r.requires_grad or sc.requires_grad
+                                                    or Bm.weight.requires_grad
+                                                    or (Bm.bias is not None and Bm.bias.requires_grad))))
+    if not fused:
+        return sc * itf_write(itf, r)
+    scale = sc.expand(*r.shape[:-1], 1).reshape(-1).float().contiguous()
+    W = _on(Bm.weight, r).contiguous()
+    b = None if Bm.bias is None else _on(Bm.bias, r).float().contiguous()
+    out = ops.write_back(r.reshape(rows, r.shape[-1]).contiguous(), W, None, b, scale)
+    return out.view(*r.shape[:-1], W.shape[0])
+
+
 def itf_query(itf, hn: torch.Tensor) -> torch.Tensor:
     if not isinstance(itf, ModelInterface):
         return itf.query(hn)
@@ -179,8 +208,7 @@ class XEncInjector(SkillInjector):
             gcal = self.calib[li]["gain"]
             if isinstance(gcal, torch.Tensor):
                 gcal = _on(gcal, r)
-        g = itf_gate(self.itf, hn, li)
-        return self.gain_scale * itf_gain(self.itf, li, hn) * gcal * g * itf_write(self.itf, r)
+        return write_delta(self.itf, hn, r, li, self.gain_scale, gcal)
 
 
 class LibraryInjector(XEncInjector):
@@ -352,8 +380,7 @@ class LibraryInjector(XEncInjector):
                 if self.training_attn and torch.is_grad_enabled():
                     self.attn_terms.append(at.float())
             self._last_q = None
-            g = itf_gate(self.itf, hn, li)
-            delta = self.gain_scale * itf_gain(self.itf, li, hn) * g * itf_write(self.itf, r)
+            delta = write_delta(self.itf, hn, r, li, self.gain_scale)
             self.last_route = w.detach()
             if torch.is_grad_enabled():
                 self.route_terms.append((li, w))
@@ -363,4 +390,4 @@ class LibraryInjector(XEncInjector):
 
 
 __all__ = ["SkillInjector", "XEncInjector", "LibraryInjector", "itf_query", "itf_gate", "itf_gain",
-           "itf_write", "rms_norm"]
+           "itf_write", "write_delta", "rms_norm"]

@@ -409,6 +409,46 @@ ROUTE_TILE = 32            # rows and chunks per tile of the many-row routing ke
 ROUTE_ROWS_MIN = 64        # from this many rows RouteFn uses the many-row routing kernel
 
 
+def write_back(r: torch.Tensor, W: torch.Tensor, row_group: torch.Tensor | None = None,
+               bias: torch.Tensor | None = None, row_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """out[m] = row_scale[m] * (W[g_m] @ r[m] + bias[g_m]) on xenc_write_back: the write of the
+    decode path's epilogue (xenc/injector.py:71-74, 266-267).  r fp32 [M, d]; W fp32 [d_out, d]
+    (one library) or [G, d_out, d] (one weight per library / depth, selected by row_group int32
+    [M]); bias [d_out] or [G, d_out]; row_scale fp32 [M].  Returns fp32 [M, d_out]."""
+    _require_device(r, "r")
+    _require_device(W, "W")
+    if r.dtype != torch.float32 or r.dim() != 2 or r.stride(1) != 1:
+        raise ValueError("r must be fp32 [M, d] with unit column stride")
+    if W.dtype != torch.float32 or W.dim() not in (2, 3) or W.stride(-1) != 1:
+        raise ValueError("W must be fp32 [d_out, d] or [G, d_out, d] with unit column stride")
+    W3 = W if W.dim() == 3 else W.unsqueeze(0)
+    G, d_out, d = W3.shape
+    M = r.shape[0]
+    if r.shape[1] != d:
+        raise ValueError(f"r has {r.shape[1]} columns, W takes {d}")
+    if row_group is not None:
+        _require_device(row_group, "row_group")
+        if row_group.dtype != torch.int32 or row_group.shape != (M,) or not row_group.is_contiguous():
+            raise ValueError("row_group must be contiguous int32 [M]")
+    if bias is not None:
+        _require_device(bias, "bias")
+        b2 = bias if bias.dim() == 2 else bias.unsqueeze(0)
+        if bias.dtype != torch.float32 or b2.shape[-1] != d_out or b2.shape[0] not in (1, G) or b2.stride(-1) != 1:
+            raise ValueError(f"bias must be fp32 [{d_out}] or [{G}, {d_out}]")
+        if b2.shape[0] != G:
+            b2 = b2.expand(G, d_out)
+    if row_scale is not None:
+        _require_device(row_scale, "row_scale")
+        if row_scale.dtype != torch.float32 or row_scale.shape != (M,) or not row_scale.is_contiguous():
+            raise ValueError("row_scale must be contiguous fp32 [M]")
+    out = torch.empty(M, d_out, dtype=torch.float32, device=r.device)
+    check(lib().xenc_write_back(ptr(r), r.stride(0), M, d, ptr(row_group), G, ptr(W3), W3.stride(0),
+                                W3.stride(1), d_out, ptr(bias), b2.stride(0) if bias is not None else 0,
+                                ptr(row_scale), ptr(out), out.stride(0), stream_handle(r.device)),
+          "xenc_write_back")
+    return out
+
+
 def _prefix(counts) -> list[int]:
     out = [0]
     for c in counts:

@@ -242,8 +242,8 @@ def test_force_attn(dev):
     fa = torch.zeros(M.shape)
     fa[0, :2] = 0.5
     captured = []
-    orig = xi.itf_write
-    xi.itf_write = lambda itf_, r: (captured.append(r), orig(itf_, r))[1]
+    orig = xi.write_delta
+    xi.write_delta = lambda itf_, hn_, r, *a, **k: (captured.append(r), orig(itf_, hn_, r, *a, **k))[1]
     try:
         with torch.no_grad():
             inj.force_attn, inj.force_norm_match = fa, True
@@ -251,7 +251,7 @@ def test_force_attn(dev):
             inj.force_attn = None
             inj._branch(h, li)
     finally:
-        xi.itf_write = orig
+        xi.write_delta = orig
     r_forced, r_comp = captured
     assert torch.allclose(r_forced.norm(dim=-1), r_comp.norm(dim=-1), atol=1e-4)
     inj.detach()
