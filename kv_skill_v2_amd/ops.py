@@ -30,11 +30,12 @@ def _i32(x, device) -> torch.Tensor:
 
 
 def build_pages(rows: torch.Tensor, row_off: torch.Tensor, d: int, slots_per_page: int, d_pad: int,
-                mu: torch.Tensor | None = None):
+                mu: torch.Tensor | None = None, out=None):
     """xenc_build_pages on device-resident input: rows fp16 [R, d] (chunk c = rows
     row_off[c] .. row_off[c+1]-1, row_off int64 [C+1]) -> (pages fp16 [C, slots_per_page, d_pad],
-    S fp32 [C, d_pad], nvalid int32 [C]), centring by mu fp32 [d] when given.  The caller
-    guarantees every chunk has 1 .. slots_per_page rows."""
+    S fp32 [C, d_pad], nvalid int32 [C]), centring by mu fp32 [d] when given.  out = (pages, S,
+    nvalid) writes into existing contiguous tensors of those shapes (e.g. a range of a static
+    pool) instead of new ones.  The caller guarantees every chunk has 1 .. slots_per_page rows."""
     for t, name in ((rows, "rows"), (row_off, "row_off")):
         _require_device(t, name)
     if rows.dtype != torch.float16 or rows.dim() != 2 or rows.shape[1] != d or not rows.is_contiguous():
@@ -45,9 +46,17 @@ def build_pages(rows: torch.Tensor, row_off: torch.Tensor, d: int, slots_per_pag
         raise ValueError(f"mu must be contiguous fp32 [{d}]")
     C = row_off.numel() - 1
     dev = rows.device
-    pages = torch.empty(C, slots_per_page, d_pad, dtype=torch.float16, device=dev)
-    S = torch.empty(C, d_pad, dtype=torch.float32, device=dev)
-    nv = torch.empty(C, dtype=torch.int32, device=dev)
+    if out is None:
+        pages = torch.empty(C, slots_per_page, d_pad, dtype=torch.float16, device=dev)
+        S = torch.empty(C, d_pad, dtype=torch.float32, device=dev)
+        nv = torch.empty(C, dtype=torch.int32, device=dev)
+    else:
+        pages, S, nv = out
+        for t, shape, dt, name in ((pages, (C, slots_per_page, d_pad), torch.float16, "pages"),
+                                   (S, (C, d_pad), torch.float32, "S"), (nv, (C,), torch.int32, "nvalid")):
+            _require_device(t, name)
+            if tuple(t.shape) != shape or t.dtype != dt or not t.is_contiguous():
+                raise ValueError(f"out {name} must be contiguous {dt} {shape}")
     check(lib().xenc_build_pages(ptr(rows), ptr(row_off), C, d, ptr(mu), slots_per_page, d_pad,
                                  ptr(pages), slots_per_page * d_pad, ptr(S), d_pad, ptr(nv),
                                  stream_handle(dev)), "xenc_build_pages")

@@ -165,6 +165,9 @@ def test_doc_cache_file_roundtrip(tmp_path):
         assert torch.equal(a.K[li], b.K[li]) and torch.equal(a.V[li], b.V[li]) and torch.equal(a.S[li], b.S[li])
     with pytest.raises(RuntimeError, match="no CPU path"):
         PagedLibrary.from_doc_caches(back, 0.25, "cpu")
+    from kv_skill_v2_amd.pool import LibraryPool
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        LibraryPool(8, 64, 16, "cpu")
 
 
 # ----------------------------------------------------------------------------- selector
