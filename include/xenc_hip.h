@@ -219,6 +219,34 @@ int xenc_paged_decode_joint(int dtype, int N, int hq, int hkv, int d,
                             float* out, long long s_on, long long s_oh,
                             void* workspace, size_t workspace_bytes, int max_n, void* stream);
 
+/*
+ * ---- Op B serving step (per-request decode state on the device)
+ * slots int32 [n_slots][4] = {op_start block, op_tokens, own_len, unused} per request slot; slot s
+ * owns own-pool blocks [s * own_blocks, (s + 1) * own_blocks).  row_slot int32 [N]: the slot
+ * decoded by row i (< 0: a padded row); a slot appears in at most one row per call.
+ * xenc_decode_step, for each row i with slot s: p0 = slots[s].own_len;
+ *   write_pos[i] = s * own_blocks * block_size + p0 (int64; -1 when p0 reached the capacity or for
+ *   a padded row), own_len[i] = p0 + 1 (capped), slots[s].own_len = p0 + 1,
+ *   op_len[i] = slots[s].op_tokens, op_bt[i][j] = op_start + j for j < ceil(op_tokens /
+ *   block_size) else dummy_block (j < max_op_blocks), own_bt[i][j] = s * own_blocks + j.
+ *   Padded rows get op_len = own_len = 0, dummy op blocks and own block 0.
+ * xenc_own_rows_write: own pool rows write_pos[i] (block write_pos / block_size, slot
+ *   write_pos % block_size) of own_k / own_v ([num_blocks, block_size, hkv, d], element strides
+ *   sb, ss, sh, d contiguous) <- k_new / v_new [N, hkv, d] (strides s_n, s_h); 2-byte elements
+ *   (fp16 or bf16), d % 8 == 0, 16-byte aligned; rows with write_pos < 0 are skipped.
+ * Both allocate nothing and read nothing back, so a decode step (xenc_decode_step,
+ * xenc_own_rows_write, xenc_paged_decode_joint) captures into one graph and replays step after
+ * step.  Replaces the per-step host fill and copies of Static.fill / stage_step and the own-row
+ * index_copy_ of read_static (xenc/d23_vllm_plugin.py:241-264, 433-457, 486-487).
+ */
+int xenc_decode_step(int N, const int* row_slot, int* slots, int n_slots, int own_blocks,
+                     int block_size, int max_op_blocks, int dummy_block, int* op_bt,
+                     long long ld_op_bt, int* op_len, int* own_bt, long long ld_own_bt,
+                     int* own_len, long long* write_pos, void* stream);
+int xenc_own_rows_write(int N, int hkv, int d, const void* k_new, const void* v_new, long long s_n,
+                        long long s_h, void* own_k, void* own_v, long long sb, long long ss,
+                        long long sh, int block_size, const long long* write_pos, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lock = threading.Lock()
 _lib = None
@@ -78,6 +78,16 @@ SIGNATURES = {
         c_float, c_int, c_int,                       # scale, nsplit, chunk
         c_void_p, c_longlong, c_longlong,            # out, s_on, s_oh
         c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_n, stream
+    "xenc_decode_step": (c_int, [
+        c_int, c_void_p, c_void_p, c_int, c_int,     # N, row_slot, slots, n_slots, own_blocks
+        c_int, c_int, c_int, c_void_p, c_longlong,   # block_size, max_op_blocks, dummy_block, op_bt, ld
+        c_void_p, c_void_p, c_longlong, c_void_p,    # op_len, own_bt, ld, own_len
+        c_void_p, c_void_p]),                        # write_pos, stream
+    "xenc_own_rows_write": (c_int, [
+        c_int, c_int, c_int, c_void_p, c_void_p,     # N, hkv, d, k_new, v_new
+        c_longlong, c_longlong, c_void_p, c_void_p,  # s_n, s_h, own_k, own_v
+        c_longlong, c_longlong, c_longlong, c_int,   # sb, ss, sh, block_size
+        c_void_p, c_void_p]),                        # write_pos, stream
     "xenc_route_backward": (c_int, [
         c_void_p, c_longlong, c_void_p, c_longlong,  # w, ldw, dw_read, ldr
         c_void_p, c_longlong, c_void_p, c_void_p,    # dw_ext, lde, row_ptr, tile_ptr

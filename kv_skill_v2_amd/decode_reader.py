@@ -97,4 +97,103 @@ class DecodeReader:
         return out
 
 
-__all__ = ["DecodeReader"]
+class DecodeState:
+    """Device-resident decode state of the op-B serving step: per request slot {operator start
+    block, operator tokens, own rows so far} and per step row the slot it decodes.  `step()`
+    (xenc_decode_step) advances every live row's own position and writes the block tables and
+    lengths of the joint read into static buffers; `write_own()` (xenc_own_rows_write) puts the
+    step's new K/V rows into the own pool.  The reference rebuilds the same tables on the host and
+    copies them to the device each step (Static.fill and stage_step,
+    xenc/d23_vllm_plugin.py:241-264, 433-457); here the host only writes when a request is admitted
+    or released or the rows change, so a whole decode step (step, write_own, DecodeReader) can be
+    captured once and replayed.
+
+        st = DecodeState(max_n, n_slots, own_blocks, block, max_op_blocks, dummy_block, device)
+        st.admit(slot, op_start_block, op_tokens); st.set_rows([slot, ...])
+        st.step(); st.write_own(k_new, v_new, own_k, own_v)
+        out = reader(q, op_k, op_v, st.op_bt, st.op_len, own_k, own_v, st.own_bt, st.own_len, scale)
+
+    Slot s owns own-pool blocks [s * own_blocks, (s + 1) * own_blocks); the own pool needs at
+    least n_slots * own_blocks blocks.  Padded rows (slot -1) read nothing and write nothing."""
+
+    def __init__(self, max_n: int, n_slots: int, own_blocks: int, block_size: int, max_op_blocks: int,
+                 dummy_block: int, device):
+        device = torch.device(device)
+        if device.type != "cuda":
+            raise RuntimeError("DecodeState lives on a ROCm GPU (there is no CPU path)")
+        if min(max_n, n_slots, own_blocks, block_size, max_op_blocks) < 1 or dummy_block < 0:
+            raise ValueError("sizes must be >= 1 and dummy_block >= 0")
+        self.max_n, self.n_slots, self.own_blocks = int(max_n), int(n_slots), int(own_blocks)
+        self.block_size, self.max_op_blocks, self.dummy_block = int(block_size), int(max_op_blocks), int(dummy_block)
+        self.device = device
+        i32 = dict(dtype=torch.int32, device=device)
+        self.slots = torch.zeros(self.n_slots, 4, **i32)
+        self.row_slot = torch.full((self.max_n,), -1, **i32)
+        self.op_bt = torch.full((self.max_n, self.max_op_blocks), self.dummy_block, **i32)
+        self.op_len = torch.zeros(self.max_n, **i32)
+        self.own_bt = torch.zeros(self.max_n, self.own_blocks, **i32)
+        self.own_len = torch.zeros(self.max_n, **i32)
+        self.write_pos = torch.full((self.max_n,), -1, dtype=torch.int64, device=device)
+        self.n = 0
+
+    def admit(self, slot: int, op_start: int, op_tokens: int, own_len: int = 0) -> None:
+        """A request enters `slot`: its document operator is op_tokens rows in the operator pool's
+        blocks op_start.. (contiguous, as the plugin's static pool lays documents out)."""
+        if not 0 <= slot < self.n_slots:
+            raise ValueError(f"slot {slot} outside [0, {self.n_slots})")
+        if op_tokens < 0 or -(-op_tokens // self.block_size) > self.max_op_blocks:
+            raise ValueError(f"op_tokens={op_tokens} needs more than max_op_blocks={self.max_op_blocks} blocks")
+        if not 0 <= own_len <= self.own_blocks * self.block_size:
+            raise ValueError("own_len outside the slot's own rows")
+        self.slots[slot].copy_(torch.tensor([op_start, op_tokens, own_len, 0], dtype=torch.int32))
+
+    def release(self, slot: int) -> None:
+        self.slots[slot].zero_()
+
+    def set_rows(self, slots) -> None:
+        """Rows of the coming steps: row i decodes slot slots[i] (-1 = padded); each slot at most
+        once."""
+        slots = [int(x) for x in slots]
+        if len(slots) > self.max_n:
+            raise ValueError(f"{len(slots)} rows > max_n={self.max_n}")
+        live = [x for x in slots if x >= 0]
+        if len(set(live)) != len(live) or any(x >= self.n_slots for x in live):
+            raise ValueError("each row's slot must be distinct and < n_slots")
+        self.row_slot.fill_(-1)
+        if slots:
+            self.row_slot[:len(slots)].copy_(torch.tensor(slots, dtype=torch.int32))
+        self.n = len(slots)
+
+    def own_rows(self, slot: int) -> int:
+        """Own rows written so far for `slot` (reads the device state: a synchronising call)."""
+        return int(self.slots[slot, 2])
+
+    def step(self, N: int | None = None) -> None:
+        N = self.n if N is None else int(N)
+        check(lib().xenc_decode_step(N, ptr(self.row_slot), ptr(self.slots), self.n_slots, self.own_blocks,
+                                     self.block_size, self.max_op_blocks, self.dummy_block, ptr(self.op_bt),
+                                     self.op_bt.stride(0), ptr(self.op_len), ptr(self.own_bt),
+                                     self.own_bt.stride(0), ptr(self.own_len), ptr(self.write_pos),
+                                     stream_handle(self.device)), "xenc_decode_step")
+
+    def write_own(self, k_new: torch.Tensor, v_new: torch.Tensor, own_k: torch.Tensor, own_v: torch.Tensor,
+                  N: int | None = None) -> None:
+        """Write the step's new rows k_new / v_new [N, hkv, d] at the positions step() assigned."""
+        N = self.n if N is None else int(N)
+        if k_new.shape != v_new.shape or k_new.stride() != v_new.stride() or k_new.dim() != 3:
+            raise ValueError("k_new and v_new must be [N, hkv, d] with equal strides")
+        if k_new.shape[0] < N or k_new.stride(-1) != 1:
+            raise ValueError("k_new must hold >= N rows with a contiguous last dim")
+        sb, ss, sh, bs = DecodeReader._pool(own_k, own_v, "own")
+        if bs != self.block_size or own_k.shape[0] < self.n_slots * self.own_blocks:
+            raise ValueError(f"own pool must have block size {self.block_size} and >= "
+                             f"{self.n_slots * self.own_blocks} blocks")
+        if own_k.shape[2:] != k_new.shape[1:] or own_k.dtype != k_new.dtype or own_k.element_size() != 2:
+            raise ValueError("new rows must match the own pool's [hkv, d] and 2-byte dtype")
+        check(lib().xenc_own_rows_write(N, k_new.shape[1], k_new.shape[2], ptr(k_new), ptr(v_new),
+                                        k_new.stride(0), k_new.stride(1), ptr(own_k), ptr(own_v), sb, ss, sh,
+                                        bs, ptr(self.write_pos), stream_handle(self.device)),
+              "xenc_own_rows_write")
+
+
+__all__ = ["DecodeReader", "DecodeState"]

@@ -168,6 +168,9 @@ def test_doc_cache_file_roundtrip(tmp_path):
     from kv_skill_v2_amd.pool import LibraryPool
     with pytest.raises(RuntimeError, match="no CPU path"):
         LibraryPool(8, 64, 16, "cpu")
+    from kv_skill_v2_amd.decode_reader import DecodeState
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        DecodeState(4, 2, 2, 16, 8, 0, "cpu")
 
 
 # ----------------------------------------------------------------------------- selector
