@@ -220,6 +220,31 @@ int xenc_paged_decode_joint(int dtype, int N, int hq, int hkv, int d,
                             void* workspace, size_t workspace_bytes, int max_n, void* stream);
 
 /*
+ * ---- Slot top-k selection read (D8)
+ * xenc_select_scores: scores[b, i] = pool over query heads h of <q[b, h], keys[i, h / G]>
+ *   (G = n_q / n_kv; pool_mean = 0: max, 1: mean), -inf where valid[i] == 0 (valid may be NULL).
+ *   q fp32 [B, n_q, hd], keys fp32 [S, n_kv, hd], scores fp32 [B, ld_s].
+ *   Replaces TopKSelector.head_scores + pool_scores at the last position
+ *   (xenc/topk_read.py:205-226).
+ * xenc_topk_rows: idx[b, :k] = the k largest scores[b, :S] in descending order, ties to the lower
+ *   index; vals (optional) their scores.  k <= S, k <= 1024.  Replaces the top-k of
+ *   TopKSelector.select_from_input (xenc/topk_read.py:237-240).
+ * xenc_gather_pages: out[g, j] = the slot row of flat index idx[g, j] (chunk idx / n_flat, slot
+ *   idx % n_flat; chunk c on page chunk_page[c]) for j < k, zero rows for k <= j < kpad;
+ *   out fp16 [G, kpad, d].  Out-of-range indices give zero rows.  The gathered pages form a
+ *   one-chunk library per set whose read (route weight 1) is the read over the selected slots
+ *   (xenc/topk_read.py:383-414).
+ */
+int xenc_select_scores(const float* q, int B, int n_q, int n_kv, int hd, const float* keys, int S,
+                       const unsigned char* valid, int pool_mean, float* scores, long long ld_s,
+                       void* stream);
+int xenc_topk_rows(const float* scores, long long ld_s, int B, int S, int k, int* idx, float* vals,
+                   long long ld_o, void* stream);
+int xenc_gather_pages(const void* pages, int slots_per_page, long long page_stride, int d,
+                      const int* chunk_page, int n_chunks, int n_flat, const int* idx,
+                      long long ld_idx, int G, int k, int kpad, void* out, void* stream);
+
+/*
  * ---- Op B serving step (per-request decode state on the device)
  * slots int32 [n_slots][4] = {op_start block, op_tokens, own_len, unused} per request slot; slot s
  * owns own-pool blocks [s * own_blocks, (s + 1) * own_blocks).  row_slot int32 [N]: the slot

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lock = threading.Lock()
 _lib = None
@@ -78,6 +78,17 @@ SIGNATURES = {
         c_float, c_int, c_int,                       # scale, nsplit, chunk
         c_void_p, c_longlong, c_longlong,            # out, s_on, s_oh
         c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_n, stream
+    "xenc_select_scores": (c_int, [
+        c_void_p, c_int, c_int, c_int, c_int,        # q, B, n_q, n_kv, hd
+        c_void_p, c_int, c_void_p, c_int,            # keys, S, valid, pool_mean
+        c_void_p, c_longlong, c_void_p]),            # scores, ld_s, stream
+    "xenc_topk_rows": (c_int, [
+        c_void_p, c_longlong, c_int, c_int, c_int,   # scores, ld_s, B, S, k
+        c_void_p, c_void_p, c_longlong, c_void_p]),  # idx, vals, ld_o, stream
+    "xenc_gather_pages": (c_int, [
+        c_void_p, c_int, c_longlong, c_int,          # pages, slots_per_page, page_stride, d
+        c_void_p, c_int, c_int, c_void_p, c_longlong,  # chunk_page, n_chunks, n_flat, idx, ld_idx
+        c_int, c_int, c_int, c_void_p, c_void_p]),   # G, k, kpad, out, stream
     "xenc_decode_step": (c_int, [
         c_int, c_void_p, c_void_p, c_int, c_int,     # N, row_slot, slots, n_slots, own_blocks
         c_int, c_int, c_int, c_void_p, c_longlong,   # block_size, max_op_blocks, dummy_block, op_bt, ld

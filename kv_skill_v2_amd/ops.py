@@ -458,6 +458,80 @@ def write_back(r: torch.Tensor, W: torch.Tensor, row_group: torch.Tensor | None 
     return out
 
 
+def select_scores(q: torch.Tensor, keys: torch.Tensor, valid: torch.Tensor | None = None,
+                  pool: str = "max") -> torch.Tensor:
+    """Pooled selection scores [B, S] on xenc_select_scores: q fp32 [B, n_q, hd] (one position),
+    keys fp32 [S, n_kv, hd], valid bool [S] (xenc/topk_read.py:205-226)."""
+    for t, n in ((q, "q"), (keys, "keys")):
+        _require_device(t, n)
+    if q.dtype != torch.float32 or keys.dtype != torch.float32 or q.dim() != 3 or keys.dim() != 3:
+        raise ValueError("q [B, n_q, hd] and keys [S, n_kv, hd] must be fp32")
+    B, n_q, hd = q.shape
+    S, n_kv, hk = keys.shape
+    if hk != hd or n_q % n_kv:
+        raise ValueError(f"head dims {hd} / {hk} or groups {n_q} / {n_kv} do not match")
+    if pool not in ("max", "mean"):
+        raise ValueError(f"unknown pool {pool!r}")
+    q, keys = q.contiguous(), keys.contiguous()
+    vb = None
+    if valid is not None:
+        _require_device(valid, "valid")
+        if valid.numel() != S:
+            raise ValueError(f"valid must have {S} entries")
+        vb = valid.reshape(-1).to(torch.uint8).contiguous()
+    out = torch.empty(B, S, dtype=torch.float32, device=q.device)
+    check(lib().xenc_select_scores(ptr(q), B, n_q, n_kv, hd, ptr(keys), S, ptr(vb), int(pool == "mean"),
+                                   ptr(out), out.stride(0), stream_handle(q.device)), "xenc_select_scores")
+    return out
+
+
+def topk_rows(scores: torch.Tensor, k: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(idx int32 [B, k], values [B, k]): the k largest entries of each row of scores fp32 [B, S]
+    in descending order, ties to the lower index, on xenc_topk_rows."""
+    _require_device(scores, "scores")
+    if scores.dtype != torch.float32 or scores.dim() != 2 or scores.stride(1) != 1:
+        raise ValueError("scores must be fp32 [B, S] with unit column stride")
+    B, S = scores.shape
+    idx = torch.empty(B, k, dtype=torch.int32, device=scores.device)
+    vals = torch.empty(B, k, dtype=torch.float32, device=scores.device)
+    check(lib().xenc_topk_rows(ptr(scores), scores.stride(0), B, S, int(k), ptr(idx), ptr(vals), k,
+                               stream_handle(scores.device)), "xenc_topk_rows")
+    return idx, vals
+
+
+def gather_library(lib_: PagedLibrary, idx: torch.Tensor, n_flat: int, pad_to: int = 64) -> PagedLibrary:
+    """One-chunk libraries of the selected slots: set g's chunk holds the slot rows of the flat
+    indices idx[g, :k] (chunk f // n_flat, slot f % n_flat of lib_'s single library), in
+    selection order, zero-padded to a multiple of pad_to slots; values are gathered the same way
+    when lib_ carries untied values.  Reading it with route weight 1 is the read over the selected
+    slots (xenc/topk_read.py:390-410)."""
+    _single(lib_)
+    _require_device(idx, "idx")
+    if idx.dim() != 2:
+        raise ValueError("idx must be [G, k]")
+    G, k = idx.shape
+    if k < 1:
+        raise ValueError("select at least one slot")
+    kpad = -(-k // pad_to) * pad_to
+    ii = idx.to(torch.int32).contiguous()
+    dev = lib_.device
+
+    def gather(src):
+        out = torch.empty(G, kpad, lib_.d, dtype=torch.float16, device=dev)
+        check(lib().xenc_gather_pages(ptr(src), lib_.slots_per_page, lib_.slots_per_page * lib_.d, lib_.d,
+                                      ptr(lib_.chunk_page), lib_.chunk_page.numel(), int(n_flat), ptr(ii), k,
+                                      G, k, kpad, ptr(out), stream_handle(dev)), "xenc_gather_pages")
+        return out
+
+    pages = gather(lib_.pages)
+    values = gather(lib_.values) if lib_.values is not None else None
+    return PagedLibrary(pages, torch.arange(G, dtype=torch.int32, device=dev),
+                        torch.full((G,), k, dtype=torch.int32, device=dev),
+                        torch.arange(G + 1, dtype=torch.int32, device=dev),
+                        torch.zeros(G, lib_.d, dtype=torch.float32, device=dev),
+                        n_chunks=[1] * G, nvalid=[k] * G, values=values, d_valid=lib_.d_valid)
+
+
 def _prefix(counts) -> list[int]:
     out = [0]
     for c in counts:
@@ -728,4 +802,5 @@ def branch_read(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, read_temp: 
 
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
            "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "RouteFn", "ReadFn",
-           "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS"]
+           "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS",
+           "build_pages", "write_back", "select_scores", "topk_rows", "gather_library"]

@@ -19,6 +19,9 @@ Pins (each function is checked by tests/test_oracle.py against something other t
                                (tests/test_selector.py:25-55)
   decode_read_ref / ref_varlen two-part LSE merge == joint softmax (tests/test_d23_kernels.py:38-48),
                                pure-Python loop restatement on tiny inputs
+  select_scores / topk_read    pure-Python loops over heads and slots on tiny inputs; the read
+                               over every slot of a one-chunk library == read (the reference's
+                               own equivalence, tests/test_topk_read.py:150-170)
   epilogue                     parity unpinned for rms_norm's eps and ModelInterface internals
                                (deltaskill is absent); fixed here as documented parameters.
 """

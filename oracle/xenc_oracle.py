@@ -269,4 +269,38 @@ def batched_decode(q: torch.Tensor, libs, route_temp=10.0, read_temp=12.0, top_k
     return torch.stack(rs), ws
 
 
+# ----------------------------------------------------------------------------- D8 slot top-k read ((f)4)
+def select_scores(q: torch.Tensor, keys: torch.Tensor, valid: torch.Tensor | None = None,
+                  pool: str = "max") -> torch.Tensor:
+    """Pooled selection scores [B, S] at one query position — TopKSelector.head_scores +
+    pool_scores (query "last"), xenc/topk_read.py:205-226: per query head h,
+    s_h[i] = q_h . K[i, h // G] (GQA, G = n_q / n_kv, no RoPE), then max (or mean) over the
+    heads; invalid slots -inf.  q [B, n_q, hd], keys [S, n_kv, hd]."""
+    B, n_q, hd = q.shape
+    n_kv = keys.shape[1]
+    G = n_q // n_kv
+    qh = q.reshape(B, n_kv, G, hd)
+    s = torch.einsum("bkgd,skd->bkgs", qh, keys.to(q.dtype)).reshape(B, n_q, -1)
+    s = s.amax(1) if pool == "max" else s.mean(1)
+    if valid is not None:
+        s = s.masked_fill(~valid.bool().view(1, -1), float("-inf"))
+    return s
+
+
+def topk_read(q: torch.Tensor, K: torch.Tensor, idx: torch.Tensor, read_temp: float = 12.0,
+              read_softmax: bool = True, V: torch.Tensor | None = None) -> torch.Tensor:
+    """The D8 read over the selected slots — TopKLibraryInjector._branch, xenc/topk_read.py:390-410:
+    Ks, Vs = K.flat[idx], V.flat[idx]; a = q . Ks; a = softmax(read_temp * a) (or a / sqrt(k));
+    r = a . Vs.  q [B, T, d]; K, V [C, N, d]; idx [B, k] flat indices into [C * N] (a single row
+    is shared by every batch row)."""
+    Kf = K.reshape(-1, K.shape[-1])
+    Vf = (K if V is None else V).reshape(-1, K.shape[-1])
+    if idx.shape[0] != q.shape[0]:
+        idx = idx[:1].expand(q.shape[0], -1)
+    Ks, Vs = Kf[idx], Vf[idx]
+    a = torch.einsum("btd,bkd->btk", q, Ks)
+    a = torch.softmax(a * read_temp, -1) if read_softmax else a / (idx.shape[-1] ** 0.5)
+    return torch.einsum("btk,bkd->btd", a, Vs)
+
+
 __all__ = [n for n in dir() if not n.startswith("_") and n not in ("math", "torch", "annotations")]

@@ -312,3 +312,50 @@ def test_decode_ref_pure_python_loop():
             for j in range(3):
                 ref = sum(ei / z * float(v[kvh, j]) for ei, (_, v) in zip(e, keys))
                 assert abs(float(out[n, h, j]) - ref) < 1e-5
+
+
+# ---------------------------------------------------------------- D8 slot top-k read ((f)4)
+def test_select_scores_pure_python_loop():
+    """select_scores against explicit loops over query heads and slots (GQA: head h reads kv
+    head h // G), for max and mean pooling, with invalid slots at -inf."""
+    g = torch.Generator().manual_seed(41)
+    B, n_q, n_kv, hd, S = 2, 6, 3, 5, 9
+    q = torch.randn(B, n_q, hd, generator=g, dtype=torch.float64)
+    keys = torch.randn(S, n_kv, hd, generator=g, dtype=torch.float64)
+    valid = torch.tensor([1, 1, 0, 1, 1, 1, 0, 1, 1], dtype=torch.bool)
+    G = n_q // n_kv
+    for pool in ("max", "mean"):
+        s = O.select_scores(q, keys, valid, pool)
+        for b in range(B):
+            for i in range(S):
+                per_head = [sum(q[b, h, e].item() * keys[i, h // G, e].item() for e in range(hd)) for h in range(n_q)]
+                want = (max(per_head) if pool == "max" else sum(per_head) / n_q) if valid[i] else -math.inf
+                assert (s[b, i].item() == want) if want == -math.inf else abs(s[b, i].item() - want) < 1e-12
+
+
+def test_topk_read_pure_python_and_one_chunk_equivalence():
+    """topk_read against explicit loops; and with every slot of a one-chunk library selected it
+    equals the standard read of that chunk (the reference's own equivalence,
+    tests/test_topk_read.py:150-170)."""
+    g = torch.Generator().manual_seed(43)
+    C, N, d, T, k = 3, 4, 5, 2, 4
+    K = torch.randn(C, N, d, generator=g, dtype=torch.float64)
+    q = torch.randn(1, T, d, generator=g, dtype=torch.float64)
+    idx = torch.tensor([[7, 0, 11, 5]])
+    r = O.topk_read(q, K, idx, 12.0)
+    Kf = K.reshape(-1, d)
+    for t in range(T):
+        sc = [sum(q[0, t, e].item() * Kf[f, e].item() for e in range(d)) * 12.0 for f in idx[0].tolist()]
+        m = max(sc)
+        ex = [math.exp(x - m) for x in sc]
+        z = sum(ex)
+        for e in range(d):
+            want = sum(ex[j] / z * Kf[f, e].item() for j, f in enumerate(idx[0].tolist()))
+            assert abs(r[0, t, e].item() - want) < 1e-12
+    rl = O.topk_read(q, K, idx, read_softmax=False)
+    a = torch.einsum("td,kd->tk", q[0], Kf[idx[0]]) / 2.0
+    assert torch.allclose(rl[0], a @ Kf[idx[0]], atol=1e-12)
+    K1 = K[:1]
+    M1 = torch.ones(1, N, dtype=torch.bool)
+    ref, _ = O.read(q, K1, M1, torch.ones(1, T, 1, dtype=torch.float64), 12.0)
+    assert torch.allclose(O.topk_read(q, K1, torch.arange(N).view(1, -1), 12.0), ref, atol=1e-12)
