@@ -220,6 +220,29 @@ int xenc_paged_decode_joint(int dtype, int N, int hq, int hkv, int d,
                             void* workspace, size_t workspace_bytes, int max_n, void* stream);
 
 /*
+ * ---- LayerSelector and the epilogue's row scale
+ * xenc_selector_weights: per row b of z fp32 [B, ldz] (n candidates, n <= 256, k <= min(n, 64)):
+ *   keep the k largest (descending, ties to the lower index), w = softmax over them, 0 elsewhere;
+ *   writes w fp32 [B, ldw] (dense), idx int32 [B, ld_sel] and w_sel fp32 [B, ld_sel] (rank order).
+ *   Replaces LayerSelector._weights_from_logits (xenc/selector.py:59-67) without straight-through.
+ * xenc_selector_apply: out[b] = sum_{j<k} w_row[b*k+j] * exp(*log_alpha) * delta[b*k+j] / (rel + 1e-6),
+ *   rel = |delta[b*k+j]| / (|h[b]| + 1e-6); delta fp32 [B*k, ldd], h fp32 [B, ldh], out [B, ldo],
+ *   d columns, k <= 64; log_alpha is a device fp32 scalar (read by the kernel, no host sync).  k = 1 is LayerSelector.apply (xenc/selector.py:106-110); k > 1 sums the k
+ *   selected layers' updates of a token.
+ * xenc_gate_scale: scale[m] = gain_scale * exp(log_gain[p]) * sigmoid(<hn[t], gate_w> + gate_b[p]),
+ *   t = row_token[m] (NULL: m), p = row_pos[m] clamped to [0, n_pos) (NULL: 0); hn fp32 [*, ldh]
+ *   with d columns.  The per-row factor of delta (itf_gate, itf_gain, xenc/injector.py:59-69).
+ */
+int xenc_selector_weights(const float* z, long long ldz, int B, int n, int k, float* w, long long ldw,
+                          int* idx, float* w_sel, long long ld_sel, void* stream);
+int xenc_selector_apply(int B, int k, int d, const float* delta, long long ldd, const float* h,
+                        long long ldh, const float* w_row, const float* log_alpha, float* out,
+                        long long ldo, void* stream);
+int xenc_gate_scale(int M, int d, const float* hn, long long ldh, const int* row_token,
+                    const int* row_pos, int n_pos, const float* gate_w, const float* gate_b,
+                    const float* log_gain, float gain_scale, float* scale, void* stream);
+
+/*
  * ---- Slot top-k selection read (D8)
  * xenc_select_scores: scores[b, i] = pool over query heads h of <q[b, h], keys[i, h / G]>
  *   (G = n_q / n_kv; pool_mean = 0: max, 1: mean), -inf where valid[i] == 0 (valid may be NULL).

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lock = threading.Lock()
 _lib = None
@@ -78,6 +78,16 @@ SIGNATURES = {
         c_float, c_int, c_int,                       # scale, nsplit, chunk
         c_void_p, c_longlong, c_longlong,            # out, s_on, s_oh
         c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_n, stream
+    "xenc_selector_weights": (c_int, [
+        c_void_p, c_longlong, c_int, c_int, c_int,   # z, ldz, B, n, k
+        c_void_p, c_longlong, c_void_p, c_void_p, c_longlong, c_void_p]),  # w, ldw, idx, w_sel, ld, stream
+    "xenc_selector_apply": (c_int, [
+        c_int, c_int, c_int, c_void_p, c_longlong,   # B, k, d, delta, ldd
+        c_void_p, c_longlong, c_void_p, c_void_p,    # h, ldh, w_row, log_alpha (device scalar)
+        c_void_p, c_longlong, c_void_p]),            # out, ldo, stream
+    "xenc_gate_scale": (c_int, [
+        c_int, c_int, c_void_p, c_longlong, c_void_p, c_void_p, c_int,  # M, d, hn, ldh, row_token, row_pos, n_pos
+        c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p]),    # gate_w, gate_b, log_gain, gain_scale, scale, stream
     "xenc_select_scores": (c_int, [
         c_void_p, c_int, c_int, c_int, c_int,        # q, B, n_q, n_kv, hd
         c_void_p, c_int, c_void_p, c_int,            # keys, S, valid, pool_mean

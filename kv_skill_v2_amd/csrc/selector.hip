@@ -1,0 +1,231 @@
+// LayerSelector on the device (xenc/selector.py:59-110) and the gate * gain row scale of the
+// epilogue (xenc/injector.py:59-69):
+//
+//   selector_weights_kernel  per row b of logits z [B, n]: keep the top k (descending, ties to the
+//                            lower index), w = softmax over the kept logits, 0 elsewhere;
+//                            dense w [B, n] and the kept (index, weight) pairs in rank order
+//   selector_apply_kernel    out[b] = sum_{j<k} w[b,j] * alpha * delta[b*k+j] / (rel + 1e-6),
+//                            rel = |delta[b*k+j]| / (|h[b]| + 1e-6), alpha = exp(*log_alpha): the
+//                            matched-norm rescale and weighting of LayerSelector.apply, summed
+//                            over the k selected layers of a token (k = 1: apply itself)
+//   gate_scale_kernel        scale[m] = gain_scale * exp(log_gain[p]) *
+//                            sigmoid(<hn[t], gate_w> + gate_b[p]), t = row_token[m],
+//                            p = row_pos[m]: the per-row factor of delta = scale * B(r)
+// Every sum runs in a fixed order (deterministic).
+#include "xenc_common.h"
+
+namespace xenc {
+namespace {
+
+constexpr int kSelMaxN = 256;   // candidates per row (4 per lane)
+
+// One wave per row.
+__global__ __launch_bounds__(256) void selector_weights_kernel(
+    const float* __restrict__ z, long long ldz, int B, int n, int k, float* __restrict__ w,
+    long long ldw, int* __restrict__ idx, float* __restrict__ w_sel, long long lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int b = blockIdx.x * 4 + threadIdx.x / kWave;
+  if (b >= B) return;  // wave-uniform
+  const float* zr = z + (long long)b * ldz;
+  float v[4];
+  bool taken[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = lane + u * kWave;
+    v[u] = c < n ? zr[c] : -INFINITY;
+    taken[u] = c >= n;
+  }
+  // k rounds of wave arg-max over the untaken entries: (value desc, index asc).
+  float kept_v = -INFINITY;   // lane j < k ends with the j-th kept value and index
+  int kept_i = -1;
+  for (int r = 0; r < k; ++r) {
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int c = lane + u * kWave;
+      if (!taken[u] && ranks_before(v[u], c, bv, bi)) {
+        bv = v[u];
+        bi = c;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = shfl_xor(bv, o);
+      const int oi = shfl_xor(bi, o);
+      if (ranks_before(ov, oi, bv, bi)) {
+        bv = ov;
+        bi = oi;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+      if (lane + u * kWave == bi) taken[u] = true;
+    if (lane == r) {
+      kept_v = bv;
+      kept_i = bi;
+    }
+  }
+  // Softmax over the kept values (lanes 0..k-1).
+  const float m = wave_max(lane < k ? kept_v : -INFINITY);
+  const float e = lane < k ? __expf(kept_v - m) : 0.f;
+  const float s = wave_sum(e);
+  const float wk = e / s;
+  float* wr = w + (long long)b * ldw;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int c = lane + u * kWave;
+    if (c < n) wr[c] = 0.f;
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  if (lane < k) {
+    wr[kept_i] = wk;
+    idx[(long long)b * lds + lane] = kept_i;
+    w_sel[(long long)b * lds + lane] = wk;
+  }
+}
+
+// Workgroup sum of one float per thread (kRowThreads threads), fixed order.
+constexpr int kRowThreads = 256;
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  __syncthreads();
+  if (lane == 0) red[wv] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Sum over e < d of f(a[e], b[e]) by the workgroup: 16-byte loads when vec4 (d, both rows 16-byte
+// aligned), else scalar.  Each thread accumulates its elements in order; then a fixed-order
+// workgroup sum.
+template <typename F>
+__device__ __forceinline__ float row_dot(const float* a, const float* b, int d, bool vec4, float* red, F f) {
+  float acc = 0.f;
+  if (vec4) {
+    const int d4 = d / 4;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < d4; i += kRowThreads) {
+      const f32x4 x = reinterpret_cast<const f32x4*>(a)[i];
+      const f32x4 y = reinterpret_cast<const f32x4*>(b)[i];
+      acc = f(x[0], y[0], acc);
+      acc = f(x[1], y[1], acc);
+      acc = f(x[2], y[2], acc);
+      acc = f(x[3], y[3], acc);
+    }
+  } else {
+#pragma unroll 4
+    for (int e = threadIdx.x; e < d; e += kRowThreads) acc = f(a[e], b[e], acc);
+  }
+  return block_sum(acc, red);
+}
+
+struct Fma {
+  __device__ float operator()(float x, float y, float acc) const { return fmaf(x, y, acc); }
+};
+
+// One workgroup per output row b.
+__global__ __launch_bounds__(kRowThreads) void selector_apply_kernel(
+    int k, int d, const float* __restrict__ delta, long long ldd, const float* __restrict__ h,
+    long long ldh, const float* __restrict__ w_row, const float* __restrict__ log_alpha,
+    float* __restrict__ out, long long ldo, int vec4) {
+  __shared__ float red[kRowThreads / kWave];
+  __shared__ float coef_s[64];
+  const int b = blockIdx.x;
+  const float* hb = h + (long long)b * ldh;
+  const float hnorm = sqrtf(row_dot(hb, hb, d, vec4, red, Fma()));
+  const float alpha = __expf(*log_alpha);
+  for (int j = 0; j < k; ++j) {
+    const float* dr = delta + ((long long)b * k + j) * ldd;
+    const float dnorm = sqrtf(row_dot(dr, dr, d, vec4, red, Fma()));
+    if (threadIdx.x == 0) {
+      const float rel = dnorm / (hnorm + 1e-6f);
+      coef_s[j] = w_row[(long long)b * k + j] * alpha / (rel + 1e-6f);
+    }
+  }
+  __syncthreads();
+  float* o = out + (long long)b * ldo;
+  const float* d0 = delta + (long long)b * k * ldd;
+  if (vec4) {
+    for (int i = threadIdx.x; i < d / 4; i += kRowThreads) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < k; ++j) {
+        const f32x4 x = reinterpret_cast<const f32x4*>(d0 + (long long)j * ldd)[i];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[u] = fmaf(coef_s[j], x[u], acc[u]);
+      }
+      reinterpret_cast<f32x4*>(o)[i] = acc;
+    }
+  } else {
+    for (int e = threadIdx.x; e < d; e += kRowThreads) {
+      float acc = 0.f;
+      for (int j = 0; j < k; ++j) acc = fmaf(coef_s[j], d0[(long long)j * ldd + e], acc);
+      o[e] = acc;
+    }
+  }
+}
+
+// One workgroup per query row m.
+__global__ __launch_bounds__(kRowThreads) void gate_scale_kernel(
+    int M, int d, const float* __restrict__ hn, long long ldh, const int* __restrict__ row_token,
+    const int* __restrict__ row_pos, int n_pos, const float* __restrict__ gate_w,
+    const float* __restrict__ gate_b, const float* __restrict__ log_gain, float gain_scale,
+    float* __restrict__ scale, int vec4) {
+  __shared__ float red[kRowThreads / kWave];
+  const int m = blockIdx.x;
+  const int t = row_token ? row_token[m] : m;
+  const int p = min(max(row_pos ? row_pos[m] : 0, 0), n_pos - 1);
+  const float s = row_dot(hn + (long long)t * ldh, gate_w, d, vec4, red, Fma());
+  if (threadIdx.x == 0) {
+    const float g = 1.f / (1.f + __expf(-(s + gate_b[p])));
+    scale[m] = gain_scale * __expf(log_gain[p]) * g;
+  }
+}
+
+}  // namespace
+}  // namespace xenc
+
+using namespace xenc;
+
+extern "C" int xenc_selector_weights(const float* z, long long ldz, int B, int n, int k, float* w,
+                                     long long ldw, int* idx, float* w_sel, long long ld_sel,
+                                     void* stream) {
+  if (B < 0 || n <= 0 || n > kSelMaxN || k <= 0 || k > n || k > kWave || ldz < n || ldw < n ||
+      ld_sel < k)
+    return XENC_EINVAL;
+  if (B == 0) return XENC_OK;
+  if (!z || !w || !idx || !w_sel) return XENC_ENULL;
+  hipLaunchKernelGGL(selector_weights_kernel, dim3((B + 3) / 4), dim3(256), 0,
+                     reinterpret_cast<hipStream_t>(stream), z, ldz, B, n, k, w, ldw, idx, w_sel, ld_sel);
+  return check_launch();
+}
+
+extern "C" int xenc_selector_apply(int B, int k, int d, const float* delta, long long ldd,
+                                   const float* h, long long ldh, const float* w_row,
+                                   const float* log_alpha, float* out, long long ldo, void* stream) {
+  if (B < 0 || k <= 0 || k > 64 || d <= 0 || ldd < d || ldh < d || ldo < d) return XENC_EINVAL;
+  if (B == 0) return XENC_OK;
+  if (!delta || !h || !w_row || !log_alpha || !out) return XENC_ENULL;
+  const int vec4 = (d % 4 == 0 && ldd % 4 == 0 && ldh % 4 == 0 && ldo % 4 == 0 && aligned16(delta) &&
+                    aligned16(h) && aligned16(out)) ? 1 : 0;
+  hipLaunchKernelGGL(selector_apply_kernel, dim3(B), dim3(kRowThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), k, d, delta, ldd, h, ldh, w_row, log_alpha,
+                     out, ldo, vec4);
+  return check_launch();
+}
+
+extern "C" int xenc_gate_scale(int M, int d, const float* hn, long long ldh, const int* row_token,
+                               const int* row_pos, int n_pos, const float* gate_w, const float* gate_b,
+                               const float* log_gain, float gain_scale, float* scale, void* stream) {
+  if (M < 0 || d <= 0 || ldh < d || n_pos <= 0) return XENC_EINVAL;
+  if (M == 0) return XENC_OK;
+  if (!hn || !gate_w || !gate_b || !log_gain || !scale) return XENC_ENULL;
+  const int vec4 = (d % 4 == 0 && ldh % 4 == 0 && aligned16(hn) && aligned16(gate_w)) ? 1 : 0;
+  hipLaunchKernelGGL(gate_scale_kernel, dim3(M), dim3(kRowThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), M, d, hn, ldh, row_token, row_pos, n_pos,
+                     gate_w, gate_b, log_gain, gain_scale, scale, vec4);
+  return check_launch();
+}

@@ -60,18 +60,23 @@ def write_delta(itf, hn: torch.Tensor, r: torch.Tensor, li: int, gain_scale: flo
     path (a ModelInterface with an fp32 linear B, at most 64 rows, nothing requiring grad) the
     product runs as one xenc_write_back launch: B streamed once with gate * gain folded into a
     per-row scale."""
-    sc = gain_scale * itf_gain(itf, li, hn) * gcal * itf_gate(itf, hn, li)   # [..., 1] per row
     Bm = getattr(itf, "B", None) if isinstance(itf, ModelInterface) else None
     rows = r.numel() // r.shape[-1]
+    grad = torch.is_grad_enabled() and (
+        r.requires_grad or hn.requires_grad
+        or (isinstance(itf, nn.Module) and any(p.requires_grad for p in itf.parameters()))
+        or (isinstance(gcal, torch.Tensor) and gcal.requires_grad))
     fused = (isinstance(Bm, nn.Linear) and r.is_cuda and r.dtype == torch.float32
              and Bm.weight.dtype == torch.float32 and rows <= _FUSED_WRITE_ROWS
-             and r.shape[-1] % 4 == 0 and sc.shape[-1] == 1
-             and not (torch.is_grad_enabled() and (r.requires_grad or sc.requires_grad
-                                                    or Bm.weight.requires_grad
-                                                    or (Bm.bias is not None and Bm.bias.requires_grad))))
+             and r.shape[-1] % 4 == 0 and not grad and isinstance(gcal, (int, float)))
     if not fused:
-        return sc * itf_write(itf, r)
-    scale = sc.expand(*r.shape[:-1], 1).reshape(-1).float().contiguous()
+        return gain_scale * itf_gain(itf, li, hn) * gcal * itf_gate(itf, hn, li) * itf_write(itf, r)
+    # gain_scale * gcal * exp(log_gain[p]) * sigmoid(hn . gate_w + gate_b[p]) per row on
+    # xenc_gate_scale, then B streamed once with that scale folded in (xenc_write_back).
+    p = itf._pos[li]
+    scale = ops.gate_scale(hn.reshape(rows, hn.shape[-1]).float().contiguous(), _on(itf.gate_w, r),
+                           _on(itf.gate_b, r)[p:p + 1], _on(itf.log_gain, r)[p:p + 1],
+                           float(gain_scale) * float(gcal))
     W = _on(Bm.weight, r).contiguous()
     b = None if Bm.bias is None else _on(Bm.bias, r).float().contiguous()
     out = ops.write_back(r.reshape(rows, r.shape[-1]).contiguous(), W, None, b, scale)

@@ -458,6 +458,73 @@ def write_back(r: torch.Tensor, W: torch.Tensor, row_group: torch.Tensor | None 
     return out
 
 
+def selector_weights(z: torch.Tensor, k: int):
+    """(w [B, n] dense, idx int32 [B, k], w_sel [B, k]) on xenc_selector_weights: top-k of each
+    row of z fp32 [B, n] (descending, ties to the lower index), softmax over the kept logits
+    (LayerSelector._weights_from_logits, xenc/selector.py:59-67)."""
+    _require_device(z, "z")
+    if z.dtype != torch.float32 or z.dim() != 2 or z.stride(1) != 1:
+        raise ValueError("z must be fp32 [B, n] with unit column stride")
+    B, n = z.shape
+    w = torch.empty(B, n, dtype=torch.float32, device=z.device)
+    idx = torch.empty(B, k, dtype=torch.int32, device=z.device)
+    w_sel = torch.empty(B, k, dtype=torch.float32, device=z.device)
+    check(lib().xenc_selector_weights(ptr(z), z.stride(0), B, n, int(k), ptr(w), w.stride(0), ptr(idx),
+                                      ptr(w_sel), k, stream_handle(z.device)), "xenc_selector_weights")
+    return w, idx, w_sel
+
+
+def selector_apply(delta: torch.Tensor, h: torch.Tensor, w_row: torch.Tensor, log_alpha,
+                   k: int = 1) -> torch.Tensor:
+    """out [B, d] = sum over a token's k rows of w * exp(log_alpha) * delta / (|delta| / (|h| + 1e-6)
+    + 1e-6) on xenc_selector_apply (LayerSelector.apply, xenc/selector.py:106-110, summed over
+    the k selected layers).  delta fp32 [B * k, d] (the k rows of token b at b*k .. b*k+k-1),
+    h fp32 [B, d], w_row fp32 [B * k]; log_alpha a float or a device scalar tensor (read by the
+    kernel: no host synchronisation)."""
+    for t, n in ((delta, "delta"), (h, "h"), (w_row, "w_row")):
+        _require_device(t, n)
+    if delta.dtype != torch.float32 or h.dtype != torch.float32 or w_row.dtype != torch.float32:
+        raise ValueError("delta, h and w_row must be fp32")
+    if delta.dim() != 2 or h.dim() != 2 or delta.stride(1) != 1 or h.stride(1) != 1:
+        raise ValueError("delta and h must be 2-D with unit column stride")
+    B, d = h.shape
+    if delta.shape != (B * k, d) or w_row.numel() != B * k:
+        raise ValueError(f"delta must be [{B * k}, {d}] and w_row [{B * k}]")
+    w_row = w_row.reshape(-1).contiguous()
+    la = (log_alpha.detach().float().reshape(1).to(h.device) if isinstance(log_alpha, torch.Tensor)
+          else torch.full((1,), float(log_alpha), dtype=torch.float32, device=h.device))
+    out = torch.empty(B, d, dtype=torch.float32, device=h.device)
+    check(lib().xenc_selector_apply(B, int(k), d, ptr(delta), delta.stride(0), ptr(h), h.stride(0), ptr(w_row),
+                                    ptr(la), ptr(out), out.stride(0), stream_handle(h.device)),
+          "xenc_selector_apply")
+    return out
+
+
+def gate_scale(hn: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor, log_gain: torch.Tensor,
+               gain_scale: float = 1.0, row_token: torch.Tensor | None = None,
+               row_pos: torch.Tensor | None = None) -> torch.Tensor:
+    """scale [M] = gain_scale * exp(log_gain[p]) * sigmoid(hn[t] . gate_w + gate_b[p]) on
+    xenc_gate_scale (itf_gate, itf_gain, xenc/injector.py:59-69); t = row_token[m] (default m),
+    p = row_pos[m] (default 0).  hn fp32 [*, d]; gate_b, log_gain fp32 [n_pos]."""
+    for t, n in ((hn, "hn"), (gate_w, "gate_w"), (gate_b, "gate_b"), (log_gain, "log_gain")):
+        _require_device(t, n)
+    if hn.dtype != torch.float32 or hn.dim() != 2 or hn.stride(1) != 1:
+        raise ValueError("hn must be fp32 [rows, d] with unit column stride")
+    d = hn.shape[1]
+    gw, gb, lg = (t.detach().float().reshape(-1).contiguous() for t in (gate_w, gate_b, log_gain))
+    if gw.numel() != d or gb.numel() != lg.numel() or gb.numel() < 1:
+        raise ValueError("gate_w must have d entries and gate_b / log_gain one per position")
+    M = hn.shape[0] if row_token is None else row_token.numel()
+    rt = None if row_token is None else row_token.to(torch.int32).reshape(-1).contiguous()
+    rp = None if row_pos is None else row_pos.to(torch.int32).reshape(-1).contiguous()
+    if rp is not None and rp.numel() != M:
+        raise ValueError("row_pos must have one entry per row")
+    out = torch.empty(M, dtype=torch.float32, device=hn.device)
+    check(lib().xenc_gate_scale(M, d, ptr(hn), hn.stride(0), ptr(rt), ptr(rp), gb.numel(), ptr(gw), ptr(gb),
+                                ptr(lg), float(gain_scale), ptr(out), stream_handle(hn.device)), "xenc_gate_scale")
+    return out
+
+
 def select_scores(q: torch.Tensor, keys: torch.Tensor, valid: torch.Tensor | None = None,
                   pool: str = "max") -> torch.Tensor:
     """Pooled selection scores [B, S] on xenc_select_scores: q fp32 [B, n_q, hd] (one position),
@@ -803,4 +870,5 @@ def branch_read(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, read_temp: 
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
            "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "RouteFn", "ReadFn",
            "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS",
-           "build_pages", "write_back", "select_scores", "topk_rows", "gather_library"]
+           "build_pages", "write_back", "select_scores", "topk_rows", "gather_library", "selector_weights",
+           "selector_apply", "gate_scale"]

@@ -58,6 +58,11 @@ class LayerSelector(nn.Module):
 
     # ------------------------------------------------------------------ weights
     def _weights_from_logits(self, z: torch.Tensor) -> torch.Tensor:
+        if (z.is_cuda and z.dtype == torch.float32 and not self.straight_through and z.shape[-1] <= 256
+                and not (torch.is_grad_enabled() and z.requires_grad)):
+            from .ops import selector_weights   # xenc_selector_weights: ties to the lower index
+            w, _, _ = selector_weights(z.reshape(-1, z.shape[-1]).contiguous(), self.k)
+            return w.view(z.shape)
         top, idx = z.topk(self.k, dim=-1)
         sparse = torch.zeros_like(z).scatter(-1, idx, torch.softmax(top, dim=-1))
         if not self.straight_through:
@@ -112,6 +117,14 @@ class LayerSelector(nn.Module):
         """Matched-norm rescale of delta, times w[..., pos[li]]; returns delta's dtype."""
         p = self.pos[li]                     # KeyError for a non-candidate layer
         self._ensure(h, li)
+        if (delta.is_cuda and not (torch.is_grad_enabled() and (delta.requires_grad or self.log_alpha.requires_grad
+                                                                 or self._w.requires_grad))):
+            from .ops import selector_apply      # xenc_selector_apply (k = 1)
+            shp = delta.shape
+            d2 = delta.float().reshape(-1, shp[-1]).contiguous()
+            h2 = h.float().reshape(-1, shp[-1]).contiguous()
+            w2 = _on(self._w[..., p], d2).reshape(-1).float().contiguous()
+            return selector_apply(d2, h2, w2, self.log_alpha, k=1).view(shp).to(delta.dtype)
         d = delta.float()
         rel = d.norm(dim=-1, keepdim=True) / (h.float().norm(dim=-1, keepdim=True) + _EPS)
         d = d / (rel + _EPS) * _on(self.log_alpha, d).exp()

@@ -1,0 +1,99 @@
+"""GPU: the LayerSelector kernels and the epilogue row scale against the oracle:
+xenc_selector_weights vs selector_weights (xenc/selector.py:59-67; kept indices bit-exact incl.
+ties, weights to 1e-6), xenc_selector_apply vs selector_apply (xenc/selector.py:106-110) for one
+layer and summed over a token's selected layers, xenc_gate_scale vs the epilogue's gate * gain
+(xenc/injector.py:59-69, 266-267), and the guards."""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle as O
+from kv_skill_v2_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+@pytest.mark.parametrize("B,n,k,ties", [(37, 8, 2, False), (5, 200, 5, False), (64, 8, 2, True),
+                                        (9, 36, 1, True), (4, 256, 64, True)])
+def test_selector_weights(dev, B, n, k, ties):
+    say("selector weights", dict(B=B, n=n, k=k, ties=ties))
+    g = torch.Generator().manual_seed(B * n + k)
+    z = (torch.randint(-3, 4, (B, n), generator=g).float() if ties else torch.randn(B, n, generator=g))
+    w, idx, w_sel = ops.selector_weights(z.to(dev), k)
+    ref = O.selector_weights(z.double(), k)
+    order = O.topk_order(z, k)
+    assert torch.equal(idx.cpu().long(), order)
+    assert float((w.cpu().double() - ref).abs().max()) < 1e-6
+    assert float((w_sel.cpu().double() - ref.gather(1, order)).abs().max()) < 1e-6
+    assert int((w.cpu() != 0).sum(1).min()) == k
+
+
+def test_selector_apply_one_and_summed(dev):
+    say("selector apply")
+    g = torch.Generator().manual_seed(3)
+    B, d, k = 32, 5120, 2
+    h = torch.randn(B, d, generator=g)
+    delta = torch.randn(B * k, d, generator=g) * 0.01
+    w = torch.rand(B * k, generator=g)
+    la = -3.9
+    out1 = ops.selector_apply(delta[::2].contiguous().to(dev), h.to(dev), w[::2].contiguous().to(dev), la, k=1)
+    ref1 = O.selector_apply(delta[::2].double(), h.double(), w[::2].double(), la)
+    assert float((out1.cpu().double() - ref1).abs().max()) < 1e-6 * float(ref1.abs().max()) + 1e-9
+    out2 = ops.selector_apply(delta.to(dev), h.to(dev), w.to(dev), la, k=k)
+    ref2 = sum(O.selector_apply(delta[j::k].double(), h.double(), w[j::k].double(), la) for j in range(k))
+    assert float((out2.cpu().double() - ref2).abs().max()) < 1e-6 * float(ref2.abs().max()) + 1e-9
+    # the matched norm, closed form: with one layer and w = 1,
+    # ||out|| / ||h|| = alpha * rel / (rel + 1e-6) * (||h|| + 1e-6) / ||h||, rel = ||delta|| / (||h|| + 1e-6)
+    one = ops.selector_apply(delta[:B].contiguous().to(dev), h.to(dev), torch.ones(B, device=dev), la, k=1)
+    hn_, dn_ = h.double().norm(dim=-1), delta[:B].double().norm(dim=-1)
+    rel = dn_ / (hn_ + 1e-6)
+    want = torch.tensor(la, dtype=torch.float64).exp() * rel / (rel + 1e-6) * (hn_ + 1e-6) / hn_
+    ratio = one.cpu().double().norm(dim=-1) / hn_
+    assert torch.allclose(ratio, want, rtol=1e-5)
+
+
+def test_gate_scale_matches_epilogue(dev):
+    say("gate scale")
+    g = torch.Generator().manual_seed(5)
+    T, d, n_pos = 20, 5120, 8
+    hn = O.rms_norm(torch.randn(T, d, generator=g))
+    gate_w = torch.randn(d, generator=g) / 50
+    gate_b = torch.randn(n_pos, generator=g)
+    log_gain = torch.randn(n_pos, generator=g) * 0.2
+    row_token = torch.tensor([3, 3, 0, 19, 7, 7, 7])
+    row_pos = torch.tensor([0, 5, 2, 7, 1, 3, 6])
+    s = ops.gate_scale(hn.to(dev), gate_w.to(dev), gate_b.to(dev), log_gain.to(dev), 0.5,
+                       row_token.to(dev), row_pos.to(dev))
+    hd = hn.double()
+    ref = torch.stack([0.5 * torch.exp(log_gain[p].double()) * torch.sigmoid(hd[t] @ gate_w.double() + gate_b[p].double())
+                       for t, p in zip(row_token.tolist(), row_pos.tolist())])
+    assert float((s.cpu().double() - ref).abs().max()) < 1e-6
+    s_all = ops.gate_scale(hn.to(dev), gate_w.to(dev), gate_b[2:3].to(dev), log_gain[2:3].to(dev), 0.5)
+    ref_all = 0.5 * torch.exp(log_gain[2].double()) * torch.sigmoid(hd @ gate_w.double() + gate_b[2].double())
+    assert float((s_all.cpu().double() - ref_all).abs().max()) < 1e-6
+    # against the oracle epilogue itself (B = identity, d = 64): delta = scale * r
+    d2 = 64
+    hn2 = O.rms_norm(torch.randn(T, d2, generator=g)).double()
+    r2 = torch.randn(T, d2, generator=g).double()
+    gw2 = torch.randn(d2, generator=g).double() / 8
+    ep = O.epilogue(hn2, r2, torch.eye(d2, dtype=torch.float64), None, gw2, gate_b[4].double(),
+                    log_gain[4].double(), 0.7)
+    s2 = ops.gate_scale(hn2.float().to(dev), gw2.float().to(dev), gate_b[4:5].to(dev), log_gain[4:5].to(dev), 0.7)
+    assert float((s2.cpu().double().unsqueeze(-1) * r2 - ep).abs().max()) < 1e-5
+
+
+def test_selector_guards(dev):
+    say("selector guards")
+    with pytest.raises(ValueError):
+        ops.selector_weights(torch.randn(2, 300, device=dev), 2)      # n > 256
+    with pytest.raises(ValueError):
+        ops.selector_weights(torch.randn(2, 4, device=dev), 5)        # k > n
+    with pytest.raises(ValueError):
+        ops.selector_apply(torch.randn(3, 8, device=dev), torch.randn(2, 8, device=dev),
+                           torch.ones(4, device=dev), 0.0, k=2)
