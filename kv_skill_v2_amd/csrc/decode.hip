@@ -435,44 +435,39 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
 }
 
 // Page-grouped runs: entry i = (row i / kk, routed chunk i % kk) of the n = M * kk entries gets
-// its rank among the entries ordered by (page, i); unrouted entries sort last.  One workgroup;
-// n <= kOrderMax, so each thread ranks at most one entry by a scan over the LDS keys, read 16
-// keys per step (four 16-byte loads in flight).  Keys past n are padded with the largest key:
-// they rank after every entry, so they never count.
+// its rank among the entries ordered by (page, i); unrouted entries sort last.  Workgroup b
+// ranks entries [64b, 64b + 64): every workgroup builds all n keys in LDS, then 8 threads per
+// entry each count the keys before it in one eighth of the list, and an xor-shuffle over the 8
+// adds the counts (integers: the order of the adds does not matter).
 constexpr int kOrderMax = 1024;
-__global__ __launch_bounds__(kOrderMax) void page_order_kernel(
+constexpr int kOrderPerWg = 64;
+__global__ __launch_bounds__(512) void page_order_kernel(
     const int* __restrict__ idx, const int* __restrict__ q_group, const int* __restrict__ chunk_ptr,
     const int* __restrict__ chunk_page, int G, int kk, int n, int* __restrict__ order) {
-  __shared__ __align__(16) int key[kOrderMax];
-  const int i = threadIdx.x;
-  int ki = 0x7fffffff;
-  if (i < n) {
+  __shared__ int key[kOrderMax];
+  for (int i = threadIdx.x; i < n; i += blockDim.x) {
     const int g = min(max(q_group[i / kk], 0), G - 1);
     const int cbeg = chunk_ptr[g];
     const int cl = idx[i];
-    if (cl >= 0 && cl < chunk_ptr[g + 1] - cbeg) ki = chunk_page[cbeg + cl];
+    key[i] = (cl >= 0 && cl < chunk_ptr[g + 1] - cbeg) ? chunk_page[cbeg + cl] : 0x7fffffff;
   }
-  key[i] = ki;
   __syncthreads();
+  const int i = blockIdx.x * kOrderPerWg + threadIdx.x / 8;   // the entry this thread helps rank
+  const int part = threadIdx.x & 7;
+  int cnt = 0;
   if (i < n) {
-    const int n16 = (n + 15) & ~15;
-    const int4* k4 = reinterpret_cast<const int4*>(key);
-    int rank = 0;
-    for (int j0 = 0; j0 < n16; j0 += 16) {
-      int4 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = k4[j0 / 4 + u];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int j = j0 + 4 * u;
-        rank += (v[u].x < ki || (v[u].x == ki && j + 0 < i)) ? 1 : 0;
-        rank += (v[u].y < ki || (v[u].y == ki && j + 1 < i)) ? 1 : 0;
-        rank += (v[u].z < ki || (v[u].z == ki && j + 2 < i)) ? 1 : 0;
-        rank += (v[u].w < ki || (v[u].w == ki && j + 3 < i)) ? 1 : 0;
-      }
+    const int ki = key[i];
+    const int per = (n + 7) / 8;
+    const int j1 = min(n, (part + 1) * per);
+    for (int j = part * per; j < j1; ++j) {
+      const int kj = key[j];
+      cnt += (kj < ki || (kj == ki && j < i)) ? 1 : 0;
     }
-    order[rank] = i;
   }
+  cnt += __shfl_xor(cnt, 1, kWave);
+  cnt += __shfl_xor(cnt, 2, kWave);
+  cnt += __shfl_xor(cnt, 4, kWave);
+  if (i < n && part == 0) order[cnt] = i;
 }
 
 // Second pass of a large launch: one workgroup per query row merges its partials (the same
@@ -593,8 +588,9 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
   const _Float16* pg = static_cast<const _Float16*>(pages);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (grouped)
-    hipLaunchKernelGGL(page_order_kernel, dim3(1), dim3(kOrderMax), 0, st, idx, q_group,
-                       chunk_ptr, chunk_page, G, kk, (int)entries, ws.order);
+    hipLaunchKernelGGL(page_order_kernel, dim3((unsigned)((entries + kOrderPerWg - 1) / kOrderPerWg)),
+                       dim3(512), 0, st, idx, q_group, chunk_ptr, chunk_page, G, kk, (int)entries,
+                       ws.order);
   const dim3 grid((unsigned)units);
   const int cb = (d + 511) / 512;
   switch (cb) {
