@@ -47,7 +47,7 @@ int xenc_abi_version(void);
  * Routing: logit[m,c] = route_temp * <q[m], S[chunk_ptr[g]+c]>, g = q_group[m].
  * If 0 < top_k < C_g keep the top_k largest (ties -> lower chunk index), else keep all C_g.
  * w = softmax over the kept logits (the others are -inf, i.e. weight 0).
- * Outputs: w_dense [M, ldw] (columns >= C_g are 0; ldw >= max C_g),
+ * Outputs: w_dense [M, ldw] (columns >= C_g are 0; max C_g <= ldw <= 5460),
  *          idx [M, kk] int32 kept chunks, -1 past the kept count: in descending-logit order
  *          (ties -> lower index) under top-k, in chunk order 0..C_g-1 when all are kept,
  *          w_sel [M, kk] their weights (0 past the kept count).
@@ -65,7 +65,7 @@ int xenc_route_topk(const float* q, long long ldq, int M, int d,
  * row_ptr[g] .. row_ptr[g+1]-1; tile_ptr[g] = sum_{g'<g} ceil(T_g'/32) * ceil(C_g'/32) (G+1
  * entries, n_tiles = tile_ptr[G]).  Same outputs and top-k / softmax as xenc_route_topk; the dots
  * are computed as 32-row x 32-chunk fp32 tiles (each summary row read once per 32 query rows).
- * ldw <= 1365.  Replaces LibraryInjector.route (xenc/injector.py:220-229) for many tokens.
+ * ldw <= 1364.  Replaces LibraryInjector.route (xenc/injector.py:220-229) for many tokens.
  */
 int xenc_route_topk_rows(const float* q, long long ldq, int M, int d, const float* S,
                          const int* chunk_ptr, const int* row_ptr, const int* tile_ptr, int G,

@@ -11,21 +11,25 @@
 // scores CPI chunks per step (CPI * CB4 float4 loads in flight per lane), so the chunk rows of a
 // library stream in parallel instead of one dependent dot at a time.  Each dot is finished
 // with a fixed xor-butterfly: the fp32 summation order is the same on every call.  Dots land in
-// LDS; wave 0 then runs top_k rounds of a wave-wide argmax.
+// LDS; wave 0 then selects the top_k (a rank count up to 64 chunks, else wave arg-max rounds).
 #include "xenc_common.h"
 
 namespace xenc {
 
+// Per-row LDS of the top-k: dots | taken | order, ls words each.  ls >= 64 (the rank variant's
+// 64 keys of 8 bytes live in taken + order) and a multiple of 4 (16-byte aligned arrays).
+__host__ __device__ constexpr int select_lds_stride(int ldw) { return ((ldw > 64 ? ldw : 64) + 3) & ~3; }
+
 // Wave-level top-k (ties -> lower chunk index) and softmax over the kept logits
-// (logit = dot * route_temp, scaled before the softmax as the reference does).  dots[0..C) hold
-// the raw dot products; taken / order are scratch of C entries.  Writes the kept weights into
-// wrow (which the caller has zeroed), and idx / w_sel rows (-1 / 0 past the kept count).
+// (logit = dot * route_temp, ranked and scaled as the reference does).  dots[0..C) hold the raw
+// dot products; taken / order are scratch of select_lds_stride(C) words.  Writes the kept weights
+// into wrow (which the caller has zeroed), and idx / w_sel rows (-1 / 0 past the kept count).
 // Register variant for C <= 64 * R chunks and <= 64 kept: lane l holds chunks l, l + 64, ...;
 // each round is a wave argmax (value, then lower index) by xor butterfly, the winner's owner
 // retires it, and lane r keeps round r's winner for the softmax.  Same selection and arithmetic
 // as the LDS variant below.
 template <int R>
-__device__ void select_topk_softmax_reg(const float* dots, int C, int top_k, int kk,
+__device__ __forceinline__ void select_topk_softmax_reg(const float* dots, int C, int top_k, int kk,
                                         float route_temp, float* wrow, int* irow, float* selrow,
                                         int lane) {
   const bool dense = top_k <= 0 || top_k >= C;
@@ -34,7 +38,7 @@ __device__ void select_topk_softmax_reg(const float* dots, int C, int top_k, int
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int c = lane + kWave * i;
-    v[i] = c < C ? dots[c] : -INFINITY;
+    v[i] = c < C ? dots[c] * route_temp : -INFINITY;   // the logit the reference ranks
   }
   int mine_c = -1;        // lane r: chunk chosen in round r
   float mine_v = 0.f;
@@ -69,8 +73,14 @@ __device__ void select_topk_softmax_reg(const float* dots, int C, int top_k, int
       }
     }
   }
-  const bool has = mine_c >= 0;
-  const float lg = has ? mine_v * route_temp : -INFINITY;
+  // A round finds no candidate only when more than C - nsel logits are -inf: such a slot keeps
+  // index -1 and weight 0.
+  const bool has = mine_c >= 0 && mine_c < C;
+  if (!has && lane < nsel) {
+    irow[lane] = -1;
+    selrow[lane] = 0.f;
+  }
+  const float lg = has ? mine_v : -INFINITY;
   const float lmax = wave_max(lg);
   const float e = has ? expf(lg - lmax) : 0.f;
   const float inv = 1.f / wave_sum(e);
@@ -86,13 +96,92 @@ __device__ void select_topk_softmax_reg(const float* dots, int C, int top_k, int
   }
 }
 
-__device__ void select_topk_softmax(const float* dots, int* taken, int* order, int C, int top_k,
+// Order key of a logit: unsigned integers compare as the floats do, -0 is folded onto +0 (the
+// reference's == ties them) and every NaN onto one key above +inf (topk ranks NaN first).
+__device__ __forceinline__ unsigned order_key(float x) {
+  if (x == 0.f) x = 0.f;
+  if (x != x) x = __uint_as_float(0x7fc00000u);
+  const unsigned b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Rank variant for C <= 64 (one chunk per lane): the top-k is a rank count instead of k dependent
+// wave arg-max rounds.  Lane l publishes the 64-bit key (order_key(logit_l) << 32) | ~l, logit =
+// dot * route_temp as the reference ranks it: a larger key is a larger logit, or the same logit
+// at a lower index.  Every lane then counts the keys above its own (LDS broadcast reads, one
+// 64-bit compare per chunk, no branches): the ranks are a permutation of [0, C), and the lane of
+// rank r < nsel is round r of the arg-max variant.  The softmax max is the rank-0 logit (the
+// max over the kept lanes when dense); the exponentials go to LDS by position and are summed in
+// position order.  LDS: dots[64] (read, then reused for the exponentials), keys[64] (8-byte
+// aligned, in the taken / order scratch of at least 128 words).
+__device__ __forceinline__ void select_topk_softmax_rank(float* dots, unsigned long long* keys, int C,
+                                                         int top_k, int kk, float route_temp,
+                                                         float* wrow, int* irow, float* selrow,
+                                                         int lane) {
+  const bool dense = top_k <= 0 || top_k >= C;
+  const int nsel = min(dense ? C : top_k, kk);
+  const float x = lane < C ? dots[lane] * route_temp : 0.f;
+  const unsigned long long key =
+      lane < C ? ((unsigned long long)order_key(x) << 32) | (unsigned)~lane : 0ull;
+  const int C8 = (C + 7) & ~7;              // keys past C are 0: below every real key
+  if (lane < C8) keys[lane] = key;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int rank = 0;
+  for (int j = 0; j < C8; j += 8) {
+    unsigned long long kj[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) kj[u] = keys[j + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) rank += kj[u] > key ? 1 : 0;
+  }
+  const int pos = dense ? lane : rank;
+  const bool has = lane < C && pos < nsel;
+  // Softmax max: the top logit (position 0) under top-k; the max over the kept lanes when dense.
+  float* es = dots;                          // the kept exponentials by position, 0 up to nsel8
+  if (!dense && pos == 0 && lane < C) es[0] = x;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  const float lmax = dense ? wave_max(has ? x : -INFINITY) : es[0];
+  const float e = has ? expf(x - lmax) : 0.f;
+  const int nsel8 = (nsel + 7) & ~7;
+  __builtin_amdgcn_wave_barrier();           // every lane has read es[0]
+  if (has) es[pos] = e;
+  if (lane >= nsel && lane < nsel8) es[lane] = 0.f;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  float sum = 0.f;                           // position order
+  for (int r = 0; r < nsel8; r += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = es[r + u];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) sum += v[u];
+  }
+  const float inv = 1.f / sum;
+  if (has) {
+    const float wr = e * inv;
+    irow[pos] = lane;
+    selrow[pos] = wr;
+    wrow[lane] = wr;
+  }
+  for (int r = nsel + lane; r < kk; r += kWave) {
+    irow[r] = -1;
+    selrow[r] = 0.f;
+  }
+}
+
+__device__ __forceinline__ void select_topk_softmax(float* dots, int* taken, int* order, int C, int top_k,
                                     int kk, float route_temp, float* wrow, int* irow, float* selrow,
                                     int lane) {
   const bool dense = top_k <= 0 || top_k >= C;
   const int nsel = min(dense ? C : top_k, kk);
   if (nsel <= kWave && C <= kWave) {
-    select_topk_softmax_reg<1>(dots, C, top_k, kk, route_temp, wrow, irow, selrow, lane);
+    select_topk_softmax_rank(dots, reinterpret_cast<unsigned long long*>(taken), C,
+                             top_k, kk, route_temp, wrow, irow, selrow, lane);
     return;
   }
   if (nsel <= kWave && C <= 4 * kWave && !dense) {
@@ -110,7 +199,7 @@ __device__ void select_topk_softmax(const float* dots, int* taken, int* order, i
       int bc = 0x7fffffff;
       for (int c = lane; c < C; c += kWave) {
         if (!taken[c]) {
-          const float v = dots[c];
+          const float v = dots[c] * route_temp;
           if (bc == 0x7fffffff || ranks_before(v, c, bv, bc)) {
             bv = v;
             bc = c;
@@ -162,11 +251,12 @@ __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
     const int* __restrict__ chunk_ptr, const int* __restrict__ q_group, int G, int top_k,
     float route_temp, float* __restrict__ w_dense, int ldw, int* __restrict__ idx,
     float* __restrict__ w_sel, int kk) {
-  // LDS: dots[ldw] fp32 | taken[ldw] int | order[ldw] int
-  extern __shared__ float lds[];
+  // LDS: dots | taken | order, select_lds_stride(ldw) words each
+  extern __shared__ __align__(16) float lds[];
+  const int ls = select_lds_stride(ldw);
   float* dots = lds;
-  int* taken = reinterpret_cast<int*>(lds + ldw);
-  int* order = taken + ldw;
+  int* taken = reinterpret_cast<int*>(lds + ls);
+  int* order = taken + ls;
 
   const int m = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
@@ -330,14 +420,15 @@ __global__ __launch_bounds__(kSelectWaves * kWave) void route_rows_select_kernel
     const int* __restrict__ q_group, int G, int top_k,
     float route_temp, float* __restrict__ w_dense, int ldw, int* __restrict__ idx,
     float* __restrict__ w_sel, int kk) {
-  extern __shared__ float lds[];   // per wave: dots[ldw] | taken[ldw] | order[ldw]
+  extern __shared__ __align__(16) float lds[];   // per wave: dots | taken | order, ls words each
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
   const int m = blockIdx.x * kSelectWaves + wv;
   if (m >= M) return;
-  float* dots = lds + (size_t)wv * 3 * ldw;
-  int* taken = reinterpret_cast<int*>(dots + ldw);
-  int* order = taken + ldw;
+  const int ls = select_lds_stride(ldw);
+  float* dots = lds + (size_t)wv * 3 * ls;
+  int* taken = reinterpret_cast<int*>(dots + ls);
+  int* order = taken + ls;
   const int g = q_group ? min(max(q_group[m], 0), G - 1)
                         : find_tile_group(row_ptr, G, m);   // row_ptr is non-decreasing: same search
   const int c0 = chunk_ptr[g];
@@ -409,13 +500,13 @@ extern "C" int xenc_route_topk(const float* q, long long ldq, int M, int d, cons
   if (!q || !S || !chunk_ptr || !q_group || !w_dense || !idx || !w_sel) return XENC_ENULL;
   if (!aligned16(q) || !aligned16(S)) return XENC_EALIGN;
   if (d > 4096) return XENC_EINVAL;
-  const size_t lds = (size_t)ldw * 3 * sizeof(float);
-  if (lds > 64 * 1024) return XENC_EINVAL;  // up to 5461 chunks per library
+  const size_t lds = (size_t)select_lds_stride((int)ldw) * 3 * sizeof(float);
+  if (ldw > 5460 || lds > 64 * 1024) return XENC_EINVAL;  // up to 5460 chunks per library
   constexpr int NW = 8;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const int cb4 = (d + 255) / 256;
   // Fewer rows than about one per CU: one wave per (row, chunk), then the wave top-k per row.
-  const size_t sel_lds = (size_t)kSelectWaves * 3 * ldw * sizeof(float);
+  const size_t sel_lds = (size_t)kSelectWaves * 3 * select_lds_stride((int)ldw) * sizeof(float);
   if (M < kSplitRouteRows && sel_lds <= 64 * 1024) {
     const dim3 grid(M, (unsigned)((ldw + 7) / 8));
     switch (cb4) {
@@ -460,8 +551,8 @@ extern "C" int xenc_route_topk_rows(const float* q, long long ldq, int M, int d,
                                     void* stream) {
   if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || ldw <= 0 || n_tiles < 0) return XENC_EINVAL;
   if (d % 8 != 0 || ldq < d || ldq % 4 != 0) return XENC_EINVAL;
-  const size_t lds = (size_t)kSelectWaves * 3 * ldw * sizeof(float);
-  if (lds > 64 * 1024) return XENC_EINVAL;  // up to 1365 chunks per library
+  if (ldw > 1364) return XENC_EINVAL;  // up to 1364 chunks per library
+  const size_t lds = (size_t)kSelectWaves * 3 * select_lds_stride((int)ldw) * sizeof(float);
   if (M == 0) return XENC_OK;
   if (!q || !S || !chunk_ptr || !row_ptr || !tile_ptr || !w_dense || !idx || !w_sel) return XENC_ENULL;
   if (!aligned16(q) || !aligned16(S)) return XENC_EALIGN;

@@ -278,6 +278,82 @@ def test_route_paths_bit_identical(dev, d, top_k):
         assert torch.equal(w, w_big[lo:hi]) and torch.equal(i, i_big[lo:hi]) and torch.equal(s, s_big[lo:hi])
 
 
+def _exact_tie_case(counts, d, seed, dev):
+    """Summary keys in {-2..2}/4 and queries in {-1, 0, 1}: every q . S is a multiple of 1/4 below
+    2^7, exact in fp32 in any summation order, so equal logits are exact ties."""
+    g = torch.Generator().manual_seed(seed)
+    P = synth.pool(counts, 64, d, device="cpu")
+    S = torch.randint(-2, 3, tuple(P.S.shape), generator=g).float() / 4
+    lib = ops.PagedLibrary(P.pages.to(dev), P.chunk_page.to(dev), P.chunk_nvalid.to(dev),
+                           P.chunk_ptr.to(dev), S.to(dev), n_chunks=P.n_chunks, nvalid=P.nvalid)
+    return P, S, lib
+
+
+def _check_exact_route(P, S, q, groups, w, idx, wsel, top_k, route_temp):
+    """idx bit-exact against a stable descending sort of the fp32 logits (the reference's
+    topk with ties to the lower index); weights within 1e-6 of the fp64 softmax."""
+    w, idx, wsel = w.cpu(), idx.cpu(), wsel.cpu()
+    for m, gi in enumerate(groups):
+        a, b = int(P.chunk_ptr[gi]), int(P.chunk_ptr[gi + 1])
+        C = b - a
+        logit = (q[m:m + 1] @ S[a:b].T) * route_temp          # fp32, exact products of exact dots
+        if not top_k or top_k >= C:
+            order = torch.arange(C).view(1, C)
+        else:
+            order = O.topk_order(logit, top_k)
+        k = order.shape[-1]
+        assert torch.equal(idx[m, :k].long(), order[0]), f"row {m}: {idx[m, :k].tolist()} vs {order[0].tolist()}"
+        assert bool((idx[m, k:] == -1).all())
+        ref = O.route(q[m:m + 1].double(), S[a:b].double(), route_temp, top_k)[0]
+        assert float((w[m, :C].double() - ref).abs().max()) < 1e-6
+        assert float((wsel[m, :k].double() - ref[order[0]]).abs().max()) < 1e-6
+
+
+@pytest.mark.parametrize("counts,top_k", [([5, 64, 33], 3), ([64, 17], 8), ([64, 9], 0),
+                                          ([200, 70], 8), ([300, 129], 5), ([300, 40], 0)])
+@pytest.mark.parametrize("M", [7, 300])
+def test_route_exact_ties(dev, counts, top_k, M):
+    """Exact logit ties on every select variant (a rank count up to 64 chunks, register rounds up
+    to 256, LDS rounds beyond; dense keeps chunk order) and on both per-row paths (one wave per
+    dot below 256 rows, one workgroup per row from 256), plus the row-grouped GEMM path."""
+    say("route exact ties", counts, top_k, M)
+    d = 64
+    P, S, lib = _exact_tie_case(counts, d, 17 + M + sum(counts), dev)
+    g = torch.Generator().manual_seed(M)
+    q = torch.randint(-1, 2, (M, d), generator=g).float()
+    groups = sorted(torch.randint(0, len(counts), (M,), generator=g).tolist())
+    qg = torch.tensor(groups, dtype=torch.int32)
+    w, idx, wsel = ops.route_topk(q.to(dev), lib, qg.to(dev), top_k=top_k, route_temp=10.0)
+    _check_exact_route(P, S, q, groups, w, idx, wsel, top_k, 10.0)
+    plan = ops.row_plan(lib, [groups.count(i) for i in range(len(counts))])
+    w2, idx2, wsel2 = ops.route_topk_rows(q.to(dev), lib, plan, top_k=top_k, route_temp=10.0)
+    _check_exact_route(P, S, q, groups, w2, idx2, wsel2, top_k, 10.0)
+
+
+@pytest.mark.parametrize("M", [1, 300])
+def test_route_ranks_logits_not_dots(dev, M):
+    """Distinct fp32 dots whose logits round to the same value (dot * 1.1) are ties, broken to the
+    lower chunk index as the reference's topk over the logits does; ranking the raw dots would
+    keep the larger dot at the higher index instead."""
+    say("route logit collapse", M)
+    v, n = 1.819639801979065, 1.8196399211883545        # adjacent fp32 values, v * 1.1 == n * 1.1
+    assert torch.tensor(v) * 1.1 == torch.tensor(n) * 1.1 and torch.tensor(v) < torch.tensor(n)
+    d = 64
+    P = synth.pool([6], 64, d, device="cpu")
+    S = torch.zeros(6, d)
+    S[:, 0] = torch.tensor([1.0, v, n, 0.5, n, v])
+    lib = ops.PagedLibrary(P.pages.to(dev), P.chunk_page.to(dev), P.chunk_nvalid.to(dev),
+                           P.chunk_ptr.to(dev), S.to(dev), n_chunks=P.n_chunks, nvalid=P.nvalid)
+    q = torch.zeros(M, d)
+    q[:, 0] = 1.0
+    qg = torch.zeros(M, dtype=torch.int32)
+    for top_k in (1, 2, 3):
+        _, idx, _ = ops.route_topk(q.to(dev), lib, qg.to(dev), top_k=top_k, route_temp=1.1)
+        want = O.topk_order((q[:1] @ S.T) * 1.1, top_k)[0]
+        assert want.tolist() == [1, 2, 4][:top_k]
+        assert bool((idx.cpu().long() == want).all()), idx.cpu()[0].tolist()
+
+
 def test_empty_inputs(dev):
     """Zero query rows: every entry point returns empty results without launching."""
     say("empty inputs")
