@@ -76,18 +76,37 @@ def cpu_baseline(P, q, top_k, n_seq, reps):
     B = q.shape[0]
     n_seq = min(n_seq, B)
     qc = q.cpu()
-    times, slots = [], 0
+
+    def routed_only(qv, K, M, S):
+        # Route over every chunk, then read only the kept ones (the others carry weight 0): per
+        # kept chunk a masked softmax of K_c q and its weighted sum of K_c rows (views, no copies).
+        logit = (qv @ S.T) * 10.0
+        C = S.shape[0]
+        k = C if not top_k or top_k >= C else top_k
+        order = O.topk_order(logit, k)[0].tolist()
+        w = O.route(qv, S, 10.0, top_k)[0]
+        r = torch.zeros(K.shape[-1])
+        for c in order:
+            a = torch.softmax((K[c] @ qv[0] * 12.0).masked_fill(~M[c], float("-inf")), -1)
+            r += w[c] * (a @ K[c])
+        return r
+
+    def median_time(fn):
+        fn()                                                  # warm-up
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    times, times_routed, slots = [], [], 0
     for b in range(n_seq):
         K, M, S = P.library(b)
         K, M, S = K.cpu(), M.cpu(), S.cpu()
         qb = qc[b].view(1, 1, -1)
-        O.branch_read(qb, K, M, S, top_k=top_k)               # warm-up
-        ts = []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            O.branch_read(qb, K, M, S, top_k=top_k)
-            ts.append(time.perf_counter() - t0)
-        times.append(statistics.median(ts))
+        times.append(median_time(lambda: O.branch_read(qb, K, M, S, top_k=top_k)))
+        times_routed.append(median_time(lambda: routed_only(qc[b].view(1, -1), K, M, S)))
         slots += int(M.sum())
         del K, M, S
     total = sum(times)
@@ -95,7 +114,10 @@ def cpu_baseline(P, q, top_k, n_seq, reps):
             "kind": "port",
             "sample": (f"first {n_seq} of {B} sequences, one fp32 route+read call each over all of the "
                        f"sequence's chunks ({slots} slots), median of {reps} reps after 1 warm-up; "
-                       f"CPU oracle on {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
+                       f"CPU oracle on {cpu_model()}, os.cpu_count()={os.cpu_count()}"),
+            "routed_only": {"value": n_seq / sum(times_routed), "unit": "query tokens/s",
+                            "sample": (f"the same sequences: route over all chunks, then read only the "
+                                       f"top-{top_k} routed chunks, fp32")}}
 
 
 MFMA_FP16_PEAK_TFLOPS = 2500.0
