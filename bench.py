@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="batched_paged_decode",
                     choices=["batched_paged_decode", "single_decode", "prefill", "multi_depth",
-                             "pool_build"])
+                             "pool_build", "d18"])
     ap.add_argument("--nsplit", type=int, default=None)
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -441,6 +441,94 @@ def bench_pool_build(args):
     print(json.dumps(out), flush=True)
 
 
+def bench_d18(args):
+    """D18 multi-document read at a decode step of a Qwen3.5-shaped reader layer: one reader row,
+    6 document operators of 2048 rows each (bf16, Hkv = 2, hd = 256), 16 query heads (G = 8), 512
+    own rows before it; soft routing over the documents (skip 16).  One step = one xenc_d18_read
+    call (partials over (kv head, document | own rows, key split), then the merge + routing).
+    Algorithmic bytes: every operator row's K and V once per kv head, the own rows' K and V (fp32),
+    the rotated queries and the outputs."""
+    from kv_skill_v2_amd import ops
+    from kv_skill_v2_amd._lib import lib, ptr, stream_handle
+
+    dev = torch.device("cuda:0")
+    D, N, hkv, G, hd, P, T, skip = 6, 2048, 2, 8, 256, 512, 1, 16
+    hq = hkv * G
+    g = torch.Generator(device=dev)
+    g.manual_seed(18)
+    docs = [(torch.randn(hkv, N, hd, generator=g, device=dev).bfloat16(),
+             torch.randn(hkv, N, hd, generator=g, device=dev).bfloat16()) for _ in range(D)]
+    pk = ops.d18_pack(docs)
+    qd = torch.randn(D, T, hq, hd, generator=g, device=dev)
+    qo = torch.randn(T, hq, hd, generator=g, device=dev)
+    ko = torch.randn(hkv, P + T, hd, generator=g, device=dev)
+    vo = torch.randn(hkv, P + T, hd, generator=g, device=dev)
+    S = ops.d18_nsplit(T, hkv, pk.lengths, P + T) if args.nsplit is None else args.nsplit
+    out = torch.empty(T, hq, hd, device=dev)
+    w = torch.empty(hkv, G, T, D, device=dev)
+    r, rmax = torch.empty_like(w), torch.empty_like(w)
+    ws = torch.empty(int(lib().xenc_d18_workspace_bytes(T, hq, D, hd, S)), dtype=torch.uint8, device=dev)
+    st = stream_handle(dev)
+    scale = hd ** -0.5
+
+    def call():
+        rc = lib().xenc_d18_read(1, T, hq, hkv, hd, D, ptr(qd), ptr(qo), ptr(pk.K), ptr(pk.V), pk.K.stride(0),
+                                 pk.K.stride(1), ptr(pk.doc_ptr), ptr(ko), ptr(vo), ko.stride(0), ko.stride(1), P,
+                                 scale, skip, 1.0, 0, -1, None, S, ptr(out), ptr(w), ptr(r), ptr(rmax),
+                                 ptr(ws), ws.numel(), st)
+        if rc:
+            raise RuntimeError(f"xenc_d18_read failed: {rc}")
+
+    alg_bytes = (D * N * hkv * hd * 2 * 2 + (P + T) * hkv * hd * 2 * 4 + (D + 1) * T * hq * hd * 4
+                 + T * hq * hd * 4 + 3 * hkv * G * T * D * 4)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record(stream)
+        call()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    k_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    achieved = alg_bytes / (k_ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_sample > 0:
+        import oracle as O
+        torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+        qd_c = qd.cpu().permute(0, 2, 1, 3).reshape(D, hkv, G, T, hd)
+        qo_c = qo.cpu().permute(1, 0, 2).reshape(hkv, G, T, hd)
+        docs_c = [(K.cpu().float(), V.cpu().float()) for K, V in docs]
+        ko_c, vo_c = ko.cpu(), vo.cpu()
+        O.d18_core(qd_c, qo_c, docs_c, ko_c, vo_c, P, scale, skip)          # warm-up
+        ts = []
+        for _ in range(max(1, args.cpu_reps)):
+            t1 = time.perf_counter()
+            O.d18_core(qd_c, qo_c, docs_c, ko_c, vo_c, P, scale, skip)
+            ts.append(time.perf_counter() - t1)
+        cpu_s = statistics.median(ts)
+        cpu = {"value": 1.0 / cpu_s, "unit": "reader rows/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": (f"the same call: the reference's per-document loop (xenc/d18_library.py:63-90) in "
+                          f"fp32 on the CPU oracle, median of {max(1, args.cpu_reps)} reps after 1 warm-up; "
+                          f"{cpu_model()}")}
+    res = {
+        "metric": "D18 multi-document read: reader rows/s and HBM GB/s (% peak)",
+        "value": T / (k_ms * 1e-3), "unit": "reader rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32 (bf16 operators)", "data": "synthetic",
+        "config": {"workload": "d18", "documents": D, "rows_per_document": N, "hkv": hkv, "hq": hq,
+                   "head_dim": hd, "own_rows": P, "reader_rows": T, "skip": skip, "key_splits": S},
+        "roofline": {"bound": "hbm", "kernel": "d18_partials_kernel + d18_merge_kernel", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": alg_bytes, "avg_launch_ms": k_ms},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -456,6 +544,8 @@ def main():
         return bench_multi_depth(args)
     if args.workload == "pool_build":
         return bench_pool_build(args)
+    if args.workload == "d18":
+        return bench_d18(args)
     from kv_skill_v2_amd import ops, synth
 
     dev = torch.device("cuda:0")

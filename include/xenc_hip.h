@@ -295,6 +295,34 @@ int xenc_own_rows_write(int N, int hkv, int d, const void* k_new, const void* v_
                         long long s_h, void* own_k, void* own_v, long long sb, long long ss,
                         long long sh, int block_size, const long long* write_pos, void* stream);
 
+/*
+ * ---- D18 multi-document read: the attention core of lib_read (xenc/d18_library.py:63-90)
+ * For reader row t, kv head h and query head g of its G = hq / hkv (GQA):
+ *   document d (keys / values rows doc_ptr[d] .. doc_ptr[d+1]-1 of k_docs / v_docs [hkv][Ntot][hd],
+ *   element strides s_dh, s_dn; dtype 0 fp16, 1 bf16, 2 fp32):
+ *     s_d = scale * qd[d, t, hg] . K_d,   o_d = softmax([s_d ; s_own]) . [V_d ; V_own],
+ *     r_d = logsumexp(s_d[skip:]), rmax_d = max(s_d[skip:])   (all of s_d when N_d <= skip)
+ *   own rows (k_own / v_own fp32 [hkv][P + T][hd], strides s_oh, s_on): s_own = scale *
+ *     qo[t, hg] . K_own[0 .. P + t] (causal);
+ *   w = softmax_d(beta * r) over the top_k largest (top_k = 0 or >= D: all; ties to the lower
+ *     index), or one-hot at force (>= 0), or wfix [D] (device, when force < 0 and wfix != NULL);
+ *   out[t, hg, :] = sum_d w_d o_d.
+ * qd [D][T][hq][hd] and qo [T][hq][hd] fp32 contiguous (the caller's RoPE rotations: document d
+ * at N_d + P + t, own rows at P + t).  Outputs w, r, rmax [hkv][G][T][D] fp32, out [T][hq][hd]
+ * fp32.  Each document's keys and the own rows are read in nsplit ranges (1..32) by separate
+ * workgroups and merged in order.  Limits: 1 <= D <= 64, G <= 8, hd in {32, 64, 128, 256};
+ * strides multiples of 16 bytes; doc_ptr int32 [D + 1] on the device.  workspace >=
+ * xenc_d18_workspace_bytes(T, hq, D, hd, nsplit) bytes of device memory (no zeroing needed).
+ * Replaces the per-document loop of lib_read (xenc/d18_library.py:63-90).
+ */
+size_t xenc_d18_workspace_bytes(int T, int hq, int n_docs, int hd, int nsplit);
+int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_docs, const float* qd,
+                  const float* qo, const void* k_docs, const void* v_docs, long long s_dh,
+                  long long s_dn, const int* doc_ptr, const float* k_own, const float* v_own,
+                  long long s_oh, long long s_on, int P, float scale, int skip, float beta,
+                  int top_k, int force, const float* wfix, int nsplit, float* out, float* w,
+                  float* r, float* rmax, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

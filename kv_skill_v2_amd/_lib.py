@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lock = threading.Lock()
 _lib = None
@@ -95,6 +95,15 @@ SIGNATURES = {
     "xenc_topk_rows": (c_int, [
         c_void_p, c_longlong, c_int, c_int, c_int,   # scores, ld_s, B, S, k
         c_void_p, c_void_p, c_longlong, c_void_p]),  # idx, vals, ld_o, stream
+    "xenc_d18_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "xenc_d18_read": (c_int, [
+        c_int, c_int, c_int, c_int, c_int, c_int,    # dtype, T, hq, hkv, hd, n_docs
+        c_void_p, c_void_p,                          # qd, qo
+        c_void_p, c_void_p, c_longlong, c_longlong, c_void_p,  # k_docs, v_docs, s_dh, s_dn, doc_ptr
+        c_void_p, c_void_p, c_longlong, c_longlong, c_int,     # k_own, v_own, s_oh, s_on, P
+        c_float, c_int, c_float, c_int, c_int, c_void_p, c_int,  # scale, skip, beta, top_k, force, wfix, nsplit
+        c_void_p, c_void_p, c_void_p, c_void_p,      # out, w, r, rmax
+        c_void_p, c_size_t, c_void_p]),              # workspace, workspace_bytes, stream
     "xenc_gather_pages": (c_int, [
         c_void_p, c_int, c_longlong, c_int,          # pages, slots_per_page, page_stride, d
         c_void_p, c_int, c_int, c_void_p, c_longlong,  # chunk_page, n_chunks, n_flat, idx, ld_idx

@@ -1,0 +1,454 @@
+// D18: a library of D documents' operators read by the reader's own query in one pass
+// (lib_read, xenc/d18_library.py:34-96).  For reader row t, kv head h and its G query heads:
+//
+//   document d:  s_d = scale * qd[d] . K_d            (qd[d] rotated at N_d + P + t)
+//                o_d = softmax([s_d ; s_own]) . [V_d ; V_own]
+//                r_d = logsumexp(s_d[skip:]),  rmax_d = max(s_d[skip:])   (all of s_d if N_d <= skip)
+//   own rows:    s_own = scale * qo . K_own[0 .. P + t]   (qo rotated at P + t; causal)
+//   routing:     w = softmax_d(beta * r)  (top_k kept, ties to the lower index; or force / wfix)
+//   output:      o = sum_d w_d o_d                     (before the gate and o_proj)
+//
+// Two launches.  d18_partials_kernel: one workgroup per (row, kv head, unit, key split), the
+// units being the D documents and the own rows, each cut into S key ranges so that a few rows
+// (decode) still spread over the GPU; it streams its keys once for all G query heads (GQA) with
+// an online softmax in the log2 domain, and for a document also the max / sum of the keys past
+// `skip`.  A key row of hd elements is read by hd / EPL lanes (16-byte loads); lane groups merge
+// by shuffles and the 4 waves through LDS, in a fixed order.  d18_merge_kernel: one workgroup per
+// (row, query head) merges the splits, joins each document with the own rows (o_d), forms r, rmax
+// and the routing weights, and sums w_d o_d.  Deterministic: every sum runs in a fixed order.
+#include <algorithm>
+
+#include "xenc_common.h"
+
+namespace xenc {
+namespace {
+
+constexpr int kD18Threads = 256;
+constexpr int kD18Waves = kD18Threads / kWave;
+constexpr int kD18MaxG = 8;
+constexpr int kD18MaxHd = 256;
+constexpr int kD18MaxDocs = 64;
+constexpr int kD18MaxSplits = 32;
+constexpr float kLn2 = 0.6931471805599453f;
+
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T> struct D18Elem { static constexpr int EPL = 8; };   // 16-bit keys
+template <> struct D18Elem<float> { static constexpr int EPL = 4; };
+
+template <typename T>
+__device__ __forceinline__ void load_f32(const T* p, float (&f)[D18Elem<T>::EPL]);
+template <> __device__ __forceinline__ void load_f32<_Float16>(const _Float16* p, float (&f)[8]) {
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(v[i] & 0xffffu));
+    f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(v[i] >> 16));
+  }
+}
+template <> __device__ __forceinline__ void load_f32<__bf16>(const __bf16* p, float (&f)[8]) {
+  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(v[i] << 16);
+    f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void load_f32<float>(const float* p, float (&f)[4]) {
+  const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f[i] = v[i];
+}
+
+// 2^(m - M) with m = -inf (an empty state) -> 0, also when M = -inf.
+__device__ __forceinline__ float rescale(float m, float M) {
+  return m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
+}
+
+// Sum over each aligned group of TPR lanes (a power of two <= 64), every lane of the group ending
+// with the same bits.  Inside a 16-lane row the partner values come by DPP (quad xor 1, xor 2,
+// half-row mirror, row mirror), across rows by the gfx950 permlane swaps, so the VALU does the
+// whole reduction (no LDS-pipe permutes).  Each step adds the two halves in the same order in
+// both lanes of a pair.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+template <int TPR>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (TPR >= 2) v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+  if constexpr (TPR >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+  if constexpr (TPR >= 8) v += dpp_f<0x141>(v);   // row_half_mirror: the other quad of the 8
+  if constexpr (TPR >= 16) v += dpp_f<0x140>(v);  // row_mirror: the other 8 of the row
+  if constexpr (TPR >= 32) {                    // rows 2i, 2i+1: (even row) + (odd row) in both
+    const unsigned u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (TPR >= 64) {                    // lanes 0-31 + lanes 32-63 in both halves
+    const unsigned u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  return v;
+}
+
+// LDS of one unit: per wave and query head the state (m, l, mc, lc) and the accumulator.
+struct D18Lds {
+  float st[kD18Waves][kD18MaxG][4];
+  float acc[kD18Waves][kD18MaxG][kD18MaxHd];
+};
+
+// One key split (n keys, the first at index j_base of its unit; n <= 0: empty) for the G query
+// heads q[g * hd ...] of a kv head, hd = HD.  A key row is read by TPR = HD / EPL lanes; each lane
+// group keeps kD18Kif keys in flight (all their K / V loads issued before any is used).  Keys at
+// unit index >= skip_c (skip_c >= 0) also enter the content max / sum (mc, lc).  Writes
+// ml_out[g] = (m, l, mc, lc) (log2 domain, scores scaled by scale_log2) and acc_out[g * HD + e]
+// (unnormalised).
+constexpr int kD18Kif = 4;
+
+template <typename TK, int HD, int GP>
+__device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
+                                         const TK* __restrict__ K, const TK* __restrict__ V, long long s_n,
+                                         int n, int j_base, int skip_c, float scale_log2,
+                                         float4* __restrict__ ml_out, float* __restrict__ acc_out, D18Lds& lds) {
+  constexpr int EPL = D18Elem<TK>::EPL;
+  constexpr int TPR = HD / EPL;              // lanes per key row: a power of two <= 64
+  constexpr int KPW = kWave / TPR;           // keys per wave and load slot
+  constexpr int STEP = kD18Waves * KPW * kD18Kif;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = threadIdx.x / kWave;
+  const int grp = lane / TPR, e0 = (lane % TPR) * EPL;
+  float qv[GP][EPL];
+  float m[GP], l[GP], mc[GP], lc[GP], acc[GP][EPL];
+#pragma unroll
+  for (int g = 0; g < GP; ++g) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+      qv[g][e] = g < G ? q[g * HD + e0 + e] : 0.f;
+      acc[g][e] = 0.f;
+    }
+    m[g] = mc[g] = -INFINITY;
+    l[g] = lc[g] = 0.f;
+  }
+  for (int j0 = 0; j0 < n; j0 += STEP) {
+    float kf[kD18Kif][EPL], vf[kD18Kif][EPL];
+#pragma unroll
+    for (int i = 0; i < kD18Kif; ++i) {
+      const int j = j0 + (i * kD18Waves + wv) * KPW + grp;
+      const long long row = (long long)(j < n ? j : n - 1) * s_n + e0;   // n >= 1 inside the loop
+      load_f32<TK>(K + row, kf[i]);
+      load_f32<TK>(V + row, vf[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < kD18Kif; ++i) {
+      const int j = j0 + (i * kD18Waves + wv) * KPW + grp;
+      float p[GP];
+#pragma unroll
+      for (int g = 0; g < GP; ++g) {
+        p[g] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) p[g] = fmaf(qv[g][e], kf[i][e], p[g]);
+      }
+#pragma unroll
+      for (int g = 0; g < GP; ++g) p[g] = group_sum<TPR>(p[g]);
+      if (j < n) {
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+          const float s = p[g] * scale_log2;
+          const float mn = fmaxf(m[g], s);
+          const float a = rescale(m[g], mn), b = __builtin_amdgcn_exp2f(s - mn);
+          l[g] = l[g] * a + b;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(acc[g][e], a, b * vf[i][e]);
+          m[g] = mn;
+          if (skip_c >= 0 && j_base + j >= skip_c) {
+            const float mcn = fmaxf(mc[g], s);
+            lc[g] = lc[g] * rescale(mc[g], mcn) + __builtin_amdgcn_exp2f(s - mcn);
+            mc[g] = mcn;
+          }
+        }
+      }
+    }
+  }
+  // Lane groups of the wave (same columns, different keys): butterfly merge.
+#pragma unroll
+  for (int o = TPR; o < kWave; o <<= 1) {
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+      const float m2 = shfl_xor(m[g], o), l2 = shfl_xor(l[g], o);
+      const float mc2 = shfl_xor(mc[g], o), lc2 = shfl_xor(lc[g], o);
+      const float M = fmaxf(m[g], m2);
+      const float a = rescale(m[g], M), b = rescale(m2, M);
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        const float acc2 = shfl_xor(acc[g][e], o);
+        acc[g][e] = acc[g][e] * a + acc2 * b;
+      }
+      l[g] = l[g] * a + l2 * b;
+      m[g] = M;
+      const float Mc = fmaxf(mc[g], mc2);
+      lc[g] = lc[g] * rescale(mc[g], Mc) + lc2 * rescale(mc2, Mc);
+      mc[g] = Mc;
+    }
+  }
+  // The 4 waves through LDS, in wave order.
+  if (grp == 0) {
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) lds.acc[wv][g][e0 + e] = acc[g][e];
+      if (lane == 0) {
+        lds.st[wv][g][0] = m[g];
+        lds.st[wv][g][1] = l[g];
+        lds.st[wv][g][2] = mc[g];
+        lds.st[wv][g][3] = lc[g];
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < G * HD; i += kD18Threads) {
+    const int g = i / HD, e = i % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kD18Waves; ++w) M = fmaxf(M, lds.st[w][g][0]);
+    float a = 0.f;
+#pragma unroll
+    for (int w = 0; w < kD18Waves; ++w) a += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
+    acc_out[i] = a;
+  }
+  if (threadIdx.x < G) {
+    const int g = threadIdx.x;
+    float M = -INFINITY, Mc = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kD18Waves; ++w) {
+      M = fmaxf(M, lds.st[w][g][0]);
+      Mc = fmaxf(Mc, lds.st[w][g][2]);
+    }
+    float L = 0.f, Lc = 0.f;
+#pragma unroll
+    for (int w = 0; w < kD18Waves; ++w) {
+      L += lds.st[w][g][1] * rescale(lds.st[w][g][0], M);
+      Lc += lds.st[w][g][3] * rescale(lds.st[w][g][2], Mc);
+    }
+    ml_out[g] = make_float4(M, L, Mc, Lc);
+  }
+}
+
+// Partials of split s of unit u of (row t, kv head h), blockIdx = (t * hkv + h, u * S + s); u < D
+// a document (keys split into S ranges of ceil(N_d / S)), u = D the own rows (S ranges of
+// ceil((P + T) / S), cut at row t's causal end P + t + 1).  Layout: part_ml [T][hkv][D + 1][S][G],
+// part_acc [T][hkv][D + 1][S][G][hd].
+template <typename TD, int HD, int GP>
+__global__ __launch_bounds__(kD18Threads) void d18_partials_kernel(
+    int hq, int hkv, int n_docs, int S, const float* __restrict__ qd, const float* __restrict__ qo,
+    const TD* __restrict__ kd, const TD* __restrict__ vd, long long s_dh, long long s_dn,
+    const int* __restrict__ doc_ptr, const float* __restrict__ ko, const float* __restrict__ vo,
+    long long s_oh, long long s_on, int P, int T, float scale_log2, int skip,
+    float4* __restrict__ part_ml, float* __restrict__ part_acc) {
+  __shared__ D18Lds lds;
+  const int th = blockIdx.x;
+  const int t = th / hkv, h = th % hkv;
+  const int u = blockIdx.y / S, sp = blockIdx.y % S;
+  const int G = hq / hkv;
+  const long long slot = (((long long)th * (n_docs + 1) + u) * S + sp) * G;
+  if (u < n_docs) {
+    const int n0 = doc_ptr[u], N = doc_ptr[u + 1] - n0;
+    const int chunk = (N + S - 1) / S;
+    const int lo = sp * chunk, n = min(N - lo, chunk);
+    const float* q = qd + (((long long)u * T + t) * hq + (long long)h * G) * HD;
+    const long long off = (long long)h * s_dh + (long long)(n0 + lo) * s_dn;
+    d18_unit<TD, HD, GP>(q, G, kd + off, vd + off, s_dn, n, lo, N > skip ? skip : 0, scale_log2, part_ml + slot,
+                     part_acc + slot * HD, lds);
+  } else {
+    const int chunk = (P + T + S - 1) / S;
+    const int lo = sp * chunk, n = min(P + t + 1 - lo, chunk);
+    const float* q = qo + ((long long)t * hq + (long long)h * G) * HD;
+    const long long off = (long long)h * s_oh + (long long)lo * s_on;
+    d18_unit<float, HD, GP>(q, G, ko + off, vo + off, s_on, n, lo, -1, scale_log2, part_ml + slot,
+                        part_acc + slot * HD, lds);
+  }
+}
+
+// One workgroup per (row t, kv head h, query head g), blockIdx.x = (t * hkv + h) * G + g.  The
+// S splits of every unit are merged first (in split order): their rescale factors and the unit
+// states go to LDS.  Wave 0 forms the routing weights (one lane per document); then thread e
+// sums o[e] = sum_d w_d o_d[e], o_d the join of document d and the own rows.
+// w, r, rmax: [hkv][G][T][D] (the reference's [Hkv, G, T, D]); out: [T][hq][hd].
+__global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(
+    int T, int hq, int hkv, int hd, int n_docs, int S, const float4* __restrict__ part_ml,
+    const float* __restrict__ part_acc, float beta, int top_k, int force, const float* __restrict__ wfix,
+    float* __restrict__ out, float* __restrict__ w_out, float* __restrict__ r_out, float* __restrict__ rmax_out) {
+  __shared__ float wl[kD18MaxDocs];
+  __shared__ float4 ust[kD18MaxDocs + 1];                       // per unit: (M, L, Mc, Lc) over splits
+  __shared__ float fac[(kD18MaxDocs + 1) * kD18MaxSplits];      // 2^(m_split - M_unit)
+  __shared__ float4 sst[(kD18MaxDocs + 1) * kD18MaxSplits];     // the split states
+  const int G = hq / hkv, U = n_docs + 1;
+  const int g = blockIdx.x % G, th = blockIdx.x / G;
+  const int t = th / hkv, h = th % hkv;
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  // slot of (unit u, split s): ((th * U + u) * S + s) * G + g
+  auto slot = [&](int u, int sp) { return (((long long)th * U + u) * S + sp) * G + g; };
+  // Split states to LDS (one load per thread), then per unit the max / sums in split order.
+  for (int i = threadIdx.x; i < U * S; i += kD18Threads) sst[i] = part_ml[slot(i / S, i % S)];
+  __syncthreads();
+  for (int u = threadIdx.x; u < U; u += kD18Threads) {
+    float M = -INFINITY, Mc = -INFINITY;
+    for (int sp = 0; sp < S; ++sp) {
+      M = fmaxf(M, sst[u * S + sp].x);
+      Mc = fmaxf(Mc, sst[u * S + sp].z);
+    }
+    float L = 0.f, Lc = 0.f;
+    for (int sp = 0; sp < S; ++sp) {
+      const float4 st = sst[u * S + sp];
+      const float f = rescale(st.x, M);
+      fac[u * S + sp] = f;
+      L += st.y * f;
+      Lc += st.w * rescale(st.z, Mc);
+    }
+    ust[u] = make_float4(M, L, Mc, Lc);
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const int d = lane;
+    const bool has = d < n_docs;
+    const float4 st = has ? ust[d] : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
+    const float r = st.w > 0.f ? st.z * kLn2 + logf(st.w) : -INFINITY;
+    float w;
+    if (force >= 0) {
+      w = d == force ? 1.f : 0.f;
+    } else if (wfix) {
+      w = has ? wfix[d] : 0.f;
+    } else {
+      const float logit = beta * r;
+      bool keep = has;
+      if (top_k > 0 && top_k < n_docs) {
+        // Rank by (logit, lower index first) over 64-bit order keys, as the routing top-k does.
+        const unsigned long long key =
+            has ? ((unsigned long long)order_key(logit) << 32) | (unsigned)~d : 0ull;
+        const unsigned hi = (unsigned)(key >> 32), lo = (unsigned)key;
+        int rank = 0;
+        for (int j = 0; j < n_docs; ++j) {
+          const unsigned long long kj = ((unsigned long long)(unsigned)__shfl((int)hi, j) << 32) |
+                                        (unsigned)__shfl((int)lo, j);
+          rank += kj > key ? 1 : 0;
+        }
+        keep = has && rank < top_k;
+      }
+      const float mx = wave_max(keep ? logit : -INFINITY);
+      const float e = keep ? expf(logit - mx) : 0.f;
+      w = e / wave_sum(e);
+    }
+    if (has) {
+      const long long o = (((long long)h * G + g) * T + t) * n_docs + d;
+      w_out[o] = w;
+      r_out[o] = r;
+      rmax_out[o] = st.w > 0.f ? st.z * kLn2 : -INFINITY;
+      wl[d] = w;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < hd; e += kD18Threads) {
+    // All S partial accumulators of a unit are loaded before they are summed (in split order).
+    auto unit_acc = [&](int u) {
+      float v[kD18MaxSplits];
+#pragma unroll
+      for (int sp = 0; sp < kD18MaxSplits; ++sp) v[sp] = sp < S ? part_acc[slot(u, sp) * hd + e] : 0.f;
+      float a = 0.f;
+#pragma unroll
+      for (int sp = 0; sp < kD18MaxSplits; ++sp)
+        if (sp < S) a = fmaf(v[sp], fac[u * S + sp], a);
+      return a;
+    };
+    const float4 so = ust[n_docs];
+    const float ao = unit_acc(n_docs);
+    float o = 0.f;
+    for (int d = 0; d < n_docs; ++d) {
+      const float4 sd = ust[d];
+      const float M = fmaxf(sd.x, so.x);
+      const float a = rescale(sd.x, M), b = rescale(so.x, M);
+      o = fmaf(wl[d], (unit_acc(d) * a + ao * b) / (sd.y * a + so.y * b), o);
+    }
+    out[((long long)t * hq + (long long)h * G + g) * hd + e] = o;
+  }
+}
+
+size_t d18_align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+}  // namespace
+}  // namespace xenc
+
+using namespace xenc;
+
+extern "C" size_t xenc_d18_workspace_bytes(int T, int hq, int n_docs, int hd, int nsplit) {
+  if (T < 0 || hq <= 0 || n_docs <= 0 || hd <= 0 || nsplit <= 0) return 0;
+  const size_t units = (size_t)T * hq * (n_docs + 1) * nsplit;
+  return d18_align256(units * sizeof(float4)) + d18_align256(units * hd * sizeof(float));
+}
+
+extern "C" int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_docs, const float* qd,
+                             const float* qo, const void* k_docs, const void* v_docs, long long s_dh,
+                             long long s_dn, const int* doc_ptr, const float* k_own, const float* v_own,
+                             long long s_oh, long long s_on, int P, float scale, int skip, float beta,
+                             int top_k, int force, const float* wfix, int nsplit, float* out, float* w,
+                             float* r, float* rmax, void* workspace, size_t workspace_bytes, void* stream) {
+  if (dtype < 0 || dtype > 2) return XENC_EINVAL;
+  if (T < 0 || P < 0 || skip < 0 || top_k < 0 || hkv <= 0 || hq <= 0 || hq % hkv != 0) return XENC_EINVAL;
+  if (hq / hkv > kD18MaxG || n_docs < 1 || n_docs > kD18MaxDocs || force >= n_docs || force < -1)
+    return XENC_EINVAL;
+  if (nsplit < 1 || nsplit > kD18MaxSplits) return XENC_EINVAL;
+  // hd in {32, 64, 128, 256}: a key row is hd / EPL lanes, a power of two <= 64, for the 16-bit
+  // document keys (EPL 8) and the fp32 own rows (EPL 4) alike.
+  if (hd != 32 && hd != 64 && hd != 128 && hd != 256) return XENC_EINVAL;
+  const int epl = dtype == 2 ? 4 : 8;
+  if (s_dh % epl || s_dn % epl || s_oh % 4 || s_on % 4) return XENC_EALIGN;
+  if (T == 0) return XENC_OK;
+  if (!qd || !qo || !k_docs || !v_docs || !doc_ptr || !k_own || !v_own || !out || !w || !r || !rmax)
+    return XENC_ENULL;
+  if (!aligned16(qd) || !aligned16(qo) || !aligned16(k_docs) || !aligned16(v_docs) || !aligned16(k_own) ||
+      !aligned16(v_own))
+    return XENC_EALIGN;
+  if (!workspace) return XENC_ENULL;
+  if (workspace_bytes < xenc_d18_workspace_bytes(T, hq, n_docs, hd, nsplit)) return XENC_EWORKSPACE;
+  if ((long long)T * hq > 0x7fffffffLL) return XENC_EINVAL;
+  const size_t units = (size_t)T * hq * (n_docs + 1) * nsplit;
+  float4* part_ml = static_cast<float4*>(workspace);
+  float* part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + d18_align256(units * sizeof(float4)));
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)(T * hkv), (unsigned)((n_docs + 1) * nsplit));
+  const float sl2 = scale * kLog2e;
+  // Query heads per kv head padded to 1, 2, 4 or 8 (padded heads have q = 0 and are not written).
+  const int G = hq / hkv, GP = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
+#define XENC_D18_LAUNCH(TD, HDV, GPV)                                                              \
+  hipLaunchKernelGGL((d18_partials_kernel<TD, HDV, GPV>), grid, dim3(kD18Threads), 0, st, hq, hkv,   \
+                     n_docs, nsplit, qd, qo, static_cast<const TD*>(k_docs),                         \
+                     static_cast<const TD*>(v_docs), s_dh, s_dn, doc_ptr, k_own, v_own, s_oh, s_on, P, \
+                     T, sl2, skip, part_ml, part_acc)
+#define XENC_D18_GP(TD, HDV)                            \
+  switch (GP) {                                         \
+    case 1: XENC_D18_LAUNCH(TD, HDV, 1); break;         \
+    case 2: XENC_D18_LAUNCH(TD, HDV, 2); break;         \
+    case 4: XENC_D18_LAUNCH(TD, HDV, 4); break;         \
+    default: XENC_D18_LAUNCH(TD, HDV, 8); break;        \
+  }
+#define XENC_D18_HD(TD)                                  \
+  switch (hd) {                                          \
+    case 32: XENC_D18_GP(TD, 32) break;                  \
+    case 64: XENC_D18_GP(TD, 64) break;                  \
+    case 128: XENC_D18_GP(TD, 128) break;                \
+    default: XENC_D18_GP(TD, 256) break;                 \
+  }
+  switch (dtype) {
+    case 0: XENC_D18_HD(_Float16) break;
+    case 1: XENC_D18_HD(__bf16) break;
+    default: XENC_D18_HD(float) break;
+  }
+#undef XENC_D18_HD
+#undef XENC_D18_GP
+#undef XENC_D18_LAUNCH
+  hipLaunchKernelGGL(d18_merge_kernel, dim3((unsigned)(T * hq)), dim3(kD18Threads), 0, st, T, hq, hkv, hd,
+                     n_docs, nsplit, part_ml, part_acc, beta, top_k, force, wfix, out, w, r, rmax);
+  return check_launch();
+}

@@ -96,15 +96,6 @@ __device__ __forceinline__ void select_topk_softmax_reg(const float* dots, int C
   }
 }
 
-// Order key of a logit: unsigned integers compare as the floats do, -0 is folded onto +0 (the
-// reference's == ties them) and every NaN onto one key above +inf (topk ranks NaN first).
-__device__ __forceinline__ unsigned order_key(float x) {
-  if (x == 0.f) x = 0.f;
-  if (x != x) x = __uint_as_float(0x7fc00000u);
-  const unsigned b = __float_as_uint(x);
-  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
-}
-
 // Rank variant for C <= 64 (one chunk per lane): the top-k is a rank count instead of k dependent
 // wave arg-max rounds.  Lane l publishes the 64-bit key (order_key(logit_l) << 32) | ~l, logit =
 // dot * route_temp as the reference ranks it: a larger key is a larger logit, or the same logit

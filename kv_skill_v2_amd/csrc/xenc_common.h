@@ -72,6 +72,15 @@ __device__ __forceinline__ bool ranks_before(float va, int ia, float vb, int ib)
   return va > vb || (va == vb && ia < ib);
 }
 
+// Order key of a logit: unsigned integers compare as the floats do, -0 is folded onto +0 (the
+// reference's == ties them) and every NaN onto one key above +inf (topk ranks NaN first).
+__device__ __forceinline__ unsigned order_key(float x) {
+  if (x == 0.f) x = 0.f;
+  if (x != x) x = __uint_as_float(0x7fc00000u);
+  const unsigned b = __float_as_uint(x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Tile b is

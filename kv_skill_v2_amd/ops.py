@@ -867,8 +867,105 @@ def branch_read(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, read_temp: 
     return read_rows(q, w, idx, wsel, lib_, read_temp, read_softmax), w
 
 
+# ----------------------------------------------------------------------------- D18 multi-document read
+_D18_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+@dataclass
+class D18Operators:
+    """One layer's document operators packed for xenc_d18_read: K, V [Hkv, Ntot, hd] (documents
+    back to back, one dtype), doc_ptr int32 [D + 1] on the device, lengths N_d."""
+    K: torch.Tensor
+    V: torch.Tensor
+    doc_ptr: torch.Tensor
+    lengths: list
+
+    @property
+    def n_docs(self) -> int:
+        return len(self.lengths)
+
+
+def d18_pack(ops) -> D18Operators:
+    """Pack [(K_d, V_d) [Hkv, N_d, hd], ...] (the operator list of lib_read) once per load."""
+    if isinstance(ops, D18Operators):
+        return ops
+    if not ops:
+        raise ValueError("d18: need at least one document operator")
+    K0 = ops[0][0]
+    for K, V in ops:
+        if K.shape != V.shape or K.dim() != 3 or K.shape[0] != K0.shape[0] or K.shape[2] != K0.shape[2]:
+            raise ValueError("d18: every operator is (K, V) [Hkv, N_d, hd] with one Hkv and hd")
+        if K.dtype != K0.dtype or V.dtype != K0.dtype or K0.dtype not in _D18_DTYPES:
+            raise ValueError("d18: operators are fp16, bf16 or fp32, all one dtype")
+        _require_device(K, "K_d")
+        _require_device(V, "V_d")
+    lengths = [int(K.shape[1]) for K, _ in ops]
+    ptr_ = [0]
+    for n in lengths:
+        ptr_.append(ptr_[-1] + n)
+    return D18Operators(torch.cat([K for K, _ in ops], 1).contiguous(), torch.cat([V for _, V in ops], 1).contiguous(),
+                        torch.tensor(ptr_, dtype=torch.int32, device=K0.device), lengths)
+
+
+def d18_nsplit(T: int, hkv: int, lengths, own: int) -> int:
+    """Key splits per unit: about one partials workgroup per CU (256) with at least 128 keys per
+    split (a decode step of 6 documents x 2048 rows, 2 kv heads: 16 splits, the fastest of 4-32
+    measured)."""
+    units = T * hkv * (len(lengths) + 1)
+    want = -(-256 // max(units, 1))
+    return max(1, min(32, want, max(max(lengths), own) // 128))
+
+
+def d18_read(qd: torch.Tensor, qo: torch.Tensor, ops, Kown: torch.Tensor, Vown: torch.Tensor, scale: float,
+             skip: int = 0, beta: float = 1.0, top_k: int = 0, force: int | None = None,
+             wfix: torch.Tensor | None = None, nsplit: int | None = None) -> dict:
+    """The attention core of lib_read (xenc/d18_library.py:63-90) on HIP (csrc/d18.hip →
+    xenc_d18_read): qd [D, Hq, T, hd] the query rotated for each document (at N_d + P + t), qo
+    [Hq, T, hd] rotated at P + t, ops the operators (a list of (K_d, V_d) [Hkv, N_d, hd] or
+    d18_pack's result), Kown / Vown [Hkv, P + T, hd] the own rows (row t sees P + t + 1 of them).
+    -> {"o" [T, Hq*hd] (before the gate and o_proj), "w", "r", "rmax" [Hkv, G, T, D], "n" [D]}.
+    Forward only: the reference evaluates D18 under no_grad."""
+    P_ops = d18_pack(ops)
+    D, Hq, T, hd = qd.shape
+    Hkv = P_ops.K.shape[0]
+    if D != P_ops.n_docs or qo.shape != (Hq, T, hd) or P_ops.K.shape[2] != hd or Hq % Hkv:
+        raise ValueError("d18: qd [D, Hq, T, hd], qo [Hq, T, hd] and the operators must agree")
+    if Kown.shape != Vown.shape or Kown.dim() != 3 or Kown.shape[0] != Hkv or Kown.shape[2] != hd \
+            or Kown.shape[1] < T:
+        raise ValueError("d18: Kown / Vown are [Hkv, P + T, hd]")
+    if torch.is_grad_enabled() and any(t.requires_grad for t in (qd, qo, Kown, Vown)):
+        raise RuntimeError("d18_read has no backward: call it under torch.no_grad()")
+    for name, t in (("qd", qd), ("qo", qo), ("Kown", Kown), ("Vown", Vown)):
+        _require_device(t, name)
+    dev = qd.device
+    P = Kown.shape[1] - T
+    G = Hq // Hkv
+    qd_ = qd.detach().float().transpose(1, 2).contiguous()          # [D, T, Hq, hd]
+    qo_ = qo.detach().float().transpose(0, 1).contiguous()          # [T, Hq, hd]
+    ko, vo = Kown.detach().float().contiguous(), Vown.detach().float().contiguous()
+    out = torch.empty(T, Hq, hd, dtype=torch.float32, device=dev)
+    w = torch.empty(Hkv, G, T, D, dtype=torch.float32, device=dev)
+    r = torch.empty_like(w)
+    rmax = torch.empty_like(w)
+    wf = None
+    if force is None and wfix is not None:
+        wf = wfix.detach().to(device=dev, dtype=torch.float32).reshape(-1).contiguous()
+        if wf.numel() != D:
+            raise ValueError("d18: wfix has one weight per document")
+    S = d18_nsplit(T, Hkv, P_ops.lengths, P + T) if nsplit is None else int(nsplit)
+    nbytes = lib().xenc_d18_workspace_bytes(T, Hq, D, hd, S)
+    ws = torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+    check(lib().xenc_d18_read(_D18_DTYPES[P_ops.K.dtype], T, Hq, Hkv, hd, D, ptr(qd_), ptr(qo_),
+                              ptr(P_ops.K), ptr(P_ops.V), P_ops.K.stride(0), P_ops.K.stride(1), ptr(P_ops.doc_ptr),
+                              ptr(ko), ptr(vo), ko.stride(0), ko.stride(1), P, float(scale), int(skip), float(beta),
+                              int(top_k), -1 if force is None else int(force), ptr(wf), S, ptr(out), ptr(w), ptr(r),
+                              ptr(rmax), ptr(ws), ws.numel(), stream_handle(dev)), "xenc_d18_read")
+    n = torch.tensor([float(m - skip) if m > skip else float(m) for m in P_ops.lengths], device=dev)
+    return {"o": out.reshape(T, Hq * hd), "w": w, "r": r, "rmax": rmax, "n": n}
+
+
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
            "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "RouteFn", "ReadFn",
            "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS",
            "build_pages", "write_back", "select_scores", "topk_rows", "gather_library", "selector_weights",
-           "selector_apply", "gate_scale"]
+           "selector_apply", "gate_scale", "D18Operators", "d18_pack", "d18_read", "d18_nsplit"]

@@ -22,6 +22,10 @@ Pins (each function is checked by tests/test_oracle.py against something other t
   select_scores / topk_read    pure-Python loops over heads and slots on tiny inputs; the read
                                over every slot of a one-chunk library == read (the reference's
                                own equivalence, tests/test_topk_read.py:150-170)
+  d18_core / d18_lib_read      pure-Python loops per (head, row) on tiny inputs; the routing modes
+                               the reference's tests use (tests/test_d18_library.py:73-93); one
+                               document == the D13 joint read with absolute RoPE (xenc/d18_library
+                               .py:14-15; a planted RoPE-offset mistake moves y by 0.06)
   epilogue                     parity unpinned for rms_norm's eps and ModelInterface internals
                                (deltaskill is absent); fixed here as documented parameters.
 """

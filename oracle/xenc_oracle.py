@@ -303,4 +303,92 @@ def topk_read(q: torch.Tensor, K: torch.Tensor, idx: torch.Tensor, read_temp: fl
     return torch.einsum("btk,bkd->btd", a, Vs)
 
 
+# ----------------------------------------------------------------------------- D18 multi-document read ((f)4)
+def d18_core(qd: torch.Tensor, qo: torch.Tensor, docs: list, Kown: torch.Tensor, Vown: torch.Tensor, P: int,
+             scale: float, skip: int = 0, beta: float = 1.0, top_k: int = 0, force: int | None = None,
+             wfix: torch.Tensor | None = None) -> dict:
+    """The attention core of lib_read, xenc/d18_library.py:63-90, given the rotated queries:
+    qd [D, Hkv, G, T, hd] (rotated at N_d + P + t for document d), qo [Hkv, G, T, hd] (rotated at
+    P + t), docs = [(K_d, V_d) [Hkv, N_d, hd]], Kown / Vown [Hkv, P + T, hd] (row t sees own
+    columns <= P + t).  Per document: o_d = softmax([s_d ; s_own]) . [V_d ; V_own],
+    r_d = logsumexp(s_d[skip:]) (all of s_d when N_d <= skip), rmax_d = max(s_d[skip:]);
+    w = softmax_d(beta * r) (top_k kept, ties to the lower index; or force / wfix);
+    o = sum_d w_d o_d.  -> {"o" [T, Hq*hd], "w", "r", "rmax" [Hkv, G, T, D], "n" [D]}."""
+    Hkv, G, T, hd = qo.shape
+    s_own = torch.einsum("kgtd,kcd->kgtc", qo, Kown) * scale
+    col = torch.arange(P + T).view(1, -1)
+    s_own = s_own.masked_fill((col > P + torch.arange(T).view(-1, 1)).view(1, 1, T, -1), float("-inf"))
+    outs, routes, rmax, nlen = [], [], [], []
+    for d, (K, V) in enumerate(docs):
+        N = K.shape[1]
+        s = torch.einsum("kgtd,kcd->kgtc", qd[d], K.to(qo.dtype)) * scale
+        m = torch.maximum(s.amax(-1, keepdim=True), s_own.amax(-1, keepdim=True))
+        e_d, e_o = (s - m).exp(), (s_own - m).exp()
+        Z = e_d.sum(-1, keepdim=True) + e_o.sum(-1, keepdim=True)
+        outs.append((torch.einsum("kgtc,kcd->kgtd", e_d, V.to(qo.dtype)) + torch.einsum("kgtc,kcd->kgtd", e_o, Vown)) / Z)
+        sc = s[..., skip:] if N > skip else s
+        routes.append(torch.logsumexp(sc, -1))
+        rmax.append(sc.amax(-1))
+        nlen.append(float(sc.shape[-1]))
+    r = torch.stack(routes, -1)
+    D = r.shape[-1]
+    if force is not None:
+        w = torch.zeros_like(r)
+        w[..., int(force)] = 1.0
+    elif wfix is not None:
+        w = wfix.to(r).view(1, 1, 1, D).expand_as(r)
+    else:
+        logit = beta * r
+        if top_k and top_k < D:
+            logit = logit.masked_fill(~topk_mask(logit, top_k), float("-inf"))
+        w = torch.softmax(logit, -1)
+    O = torch.stack(outs, -2)
+    o = (w.unsqueeze(-1) * O).sum(-2).reshape(Hkv * G, T, hd).transpose(0, 1).reshape(T, Hkv * G * hd)
+    return {"o": o, "w": w, "r": r, "rmax": torch.stack(rmax, -1), "n": torch.tensor(nlen)}
+
+
+def d18_lib_read(itf, li: int, x: torch.Tensor, ops: list, past=None, skip: int = 0, beta: float = 1.0,
+                 top_k: int = 0, force: int | None = None, wfix: torch.Tensor | None = None,
+                 dtype=torch.float64) -> dict:
+    """lib_read, xenc/d18_library.py:34-96: the reader rows' query / gate / own key and value from
+    the interface's projections (:41-49), the RoPE rotations at relative positions P + t and
+    N_d + P + t (:50-55, :68-70), the core above, then o_proj(o * sigmoid(gate)) and B (:93-96).
+    Evaluated in `dtype` (fp64 by default)."""
+    from transformers.models.qwen3_5.modeling_qwen3_5 import apply_rotary_pos_emb
+    att = itf.att[str(li)]
+    hd = att.head_dim
+    with torch.no_grad():
+        xe = itf.map_x(li, x)
+        T = xe.shape[0]
+        qh, gate = torch.chunk(att.q_proj(xe).view(T, -1, hd * 2), 2, dim=-1)
+        gate = gate.reshape(T, -1)
+        q = att.q_norm(qh).transpose(0, 1)
+        k = att.k_norm(att.k_proj(xe).view(T, -1, hd)).transpose(0, 1)
+        v = att.v_proj(xe).view(T, -1, hd).transpose(0, 1)
+        Hq, Hkv = q.shape[0], k.shape[0]
+        G = Hq // Hkv
+        P = 0 if past is None else past[0].shape[1]
+        rel = torch.arange(P, P + T)
+
+        def rope(pos):
+            cos, sin = itf.rot(xe.unsqueeze(0), pos.view(1, 1, -1).expand(3, 1, -1))
+            return cos.float(), sin.float()
+
+        cos, sin = rope(rel)
+        qo, ko = apply_rotary_pos_emb(q.unsqueeze(0), k.unsqueeze(0), cos, sin)
+        qo, ko = qo[0], ko[0]
+        Kown = ko if past is None else torch.cat([past[0], ko], 1)
+        Vown = v if past is None else torch.cat([past[1], v], 1)
+        qd = []
+        for K, _ in ops:
+            cos, sin = rope(rel + K.shape[1])
+            qd.append(apply_rotary_pos_emb(q.unsqueeze(0), k.unsqueeze(0), cos, sin)[0][0])
+        core = d18_core(torch.stack(qd).view(len(ops), Hkv, G, T, hd).to(dtype), qo.view(Hkv, G, T, hd).to(dtype),
+                        [(K.to(dtype), V.to(dtype)) for K, V in ops], Kown.to(dtype), Vown.to(dtype), P,
+                        att.scaling, skip, beta, top_k, force, wfix)
+        o = att.o_proj((core["o"] * torch.sigmoid(gate.to(dtype))).float())
+        return {"y": itf.Bmap(li, o), "o": o, "w": core["w"], "past": (Kown, Vown), "r": core["r"],
+                "rmax": core["rmax"], "n": core["n"]}
+
+
 __all__ = [n for n in dir() if not n.startswith("_") and n not in ("math", "torch", "annotations")]

@@ -359,3 +359,110 @@ def test_topk_read_pure_python_and_one_chunk_equivalence():
     M1 = torch.ones(1, N, dtype=torch.bool)
     ref, _ = O.read(q, K1, M1, torch.ones(1, T, 1, dtype=torch.float64), 12.0)
     assert torch.allclose(O.topk_read(q, K1, torch.arange(N).view(1, -1), 12.0), ref, atol=1e-12)
+
+
+# ----------------------------------------------------------------------------- D18 ((f)4)
+def _d18_case(Ns=(5, 7, 4), T=3, P=2, Hkv=2, G=2, hd=4, seed=3):
+    g = torch.Generator().manual_seed(seed)
+
+    def r(*s):
+        return torch.randn(*s, generator=g, dtype=torch.float64)
+    D = len(Ns)
+    docs = [(r(Hkv, n, hd), r(Hkv, n, hd)) for n in Ns]
+    return r(D, Hkv, G, T, hd), r(Hkv, G, T, hd), docs, r(Hkv, P + T, hd), r(Hkv, P + T, hd), P
+
+
+def test_d18_core_pure_python_loop():
+    """d18_core against per-(head, row) loops: joint softmax over [doc keys (doc query) ; own keys
+    (own query, causal)], LSE and max over the keys past `skip`, softmax over documents."""
+    qd, qo, docs, Kown, Vown, P = _d18_case(Ns=(5, 7, 1))
+    scale, skip, beta = 0.7, 2, 1.3
+    out = O.d18_core(qd, qo, docs, Kown, Vown, P, scale, skip, beta)
+    Hkv, G, T, hd = qo.shape
+    dot = lambda a, b: sum(float(a[e]) * float(b[e]) for e in range(hd))
+    for h, gg, t in itertools.product(range(Hkv), range(G), range(T)):
+        od, rr, mx = [], [], []
+        for d, (K, V) in enumerate(docs):
+            sd = [scale * dot(qd[d, h, gg, t], K[h, j]) for j in range(K.shape[1])]
+            so = [scale * dot(qo[h, gg, t], Kown[h, j]) for j in range(P + t + 1)]
+            m = max(sd + so)
+            ed, eo = [math.exp(x - m) for x in sd], [math.exp(x - m) for x in so]
+            Z = sum(ed) + sum(eo)
+            od.append([(sum(ed[j] * float(V[h, j, e]) for j in range(len(sd)))
+                        + sum(eo[j] * float(Vown[h, j, e]) for j in range(len(so)))) / Z for e in range(hd)])
+            content = sd[skip:] if len(sd) > skip else sd
+            mc = max(content)
+            rr.append(mc + math.log(sum(math.exp(x - mc) for x in content)))
+            mx.append(mc)
+        lm = max(beta * x for x in rr)
+        ex = [math.exp(beta * x - lm) for x in rr]
+        w = [x / sum(ex) for x in ex]
+        assert torch.allclose(out["r"][h, gg, t], torch.tensor(rr, dtype=torch.float64), atol=1e-12)
+        assert torch.allclose(out["rmax"][h, gg, t], torch.tensor(mx, dtype=torch.float64), atol=1e-12)
+        assert torch.allclose(out["w"][h, gg, t], torch.tensor(w, dtype=torch.float64), atol=1e-12)
+        want = [sum(w[d] * od[d][e] for d in range(len(docs))) for e in range(hd)]
+        got = out["o"][t, (h * G + gg) * hd:(h * G + gg + 1) * hd]
+        assert torch.allclose(got, torch.tensor(want, dtype=torch.float64), atol=1e-12)
+    assert out["n"].tolist() == [3.0, 5.0, 1.0]          # N_d - skip, or N_d when N_d <= skip
+
+
+def test_d18_core_routing_modes():
+    """The routing modes the reference's tests exercise (tests/test_d18_library.py:73-93): w sums
+    to 1; force = d is the one-document read of d; top_k = 1 is one-hot at the largest logit;
+    wfix is used as given; a sharp beta picks the soft argmax; rmax <= r."""
+    qd, qo, docs, Kown, Vown, P = _d18_case(Ns=(6, 9, 4, 8))
+    soft = O.d18_core(qd, qo, docs, Kown, Vown, P, 0.5, skip=2)
+    assert torch.allclose(soft["w"].sum(-1), torch.ones(soft["w"].shape[:-1], dtype=torch.float64))
+    assert bool((soft["rmax"] <= soft["r"] + 1e-12).all())
+    f1 = O.d18_core(qd, qo, docs, Kown, Vown, P, 0.5, skip=2, force=1)
+    one = O.d18_core(qd[1:2], qo, docs[1:2], Kown, Vown, P, 0.5, skip=2)
+    assert torch.allclose(f1["o"], one["o"], atol=1e-12) and torch.equal(one["w"], torch.ones_like(one["w"]))
+    hard = O.d18_core(qd, qo, docs, Kown, Vown, P, 0.5, skip=2, top_k=1)
+    assert torch.equal(hard["w"].argmax(-1), soft["r"].argmax(-1))
+    assert torch.allclose(hard["w"].max(-1).values, torch.ones_like(hard["w"].max(-1).values))
+    wf = torch.tensor([0.1, 0.2, 0.3, 0.4], dtype=torch.float64)
+    fixed = O.d18_core(qd, qo, docs, Kown, Vown, P, 0.5, wfix=wf)
+    assert torch.equal(fixed["w"][0, 0, 0], wf)
+    sharp = O.d18_core(qd, qo, docs, Kown, Vown, P, 0.5, skip=2, beta=1e4)
+    assert torch.equal(sharp["w"].argmax(-1), soft["w"].argmax(-1))
+
+
+def test_d18_lib_read_one_document_is_the_joint_read():
+    """With one document lib_read equals the D13 joint read (xenc/d18_library.py:14-15, RoPE is
+    relative): q and the own keys rotated at the absolute positions N + P + t, one softmax over
+    [operator ; own rows] (xenc/d13_read.py:192-245).  Also the incremental form: rows 0..3 then
+    4..6 with the first call's past == all rows at once (tests/test_d18_library.py:60-70)."""
+    pytest.importorskip("transformers")
+    from transformers.models.qwen3_5.modeling_qwen3_5 import apply_rotary_pos_emb
+    import d18_tiny
+    itf = d18_tiny.TinyItf()
+    li = 5
+    (K, V), = d18_tiny.operators(itf, [11])
+    x = torch.randn(7, 64, generator=torch.Generator().manual_seed(3))
+    got = O.d18_lib_read(itf, li, x, [(K, V)])
+    att = itf.att[str(li)]
+    hd = att.head_dim
+    with torch.no_grad():
+        xe = itf.map_x(li, x)
+        T, N = xe.shape[0], K.shape[1]
+        qh, gate = torch.chunk(att.q_proj(xe).view(T, -1, hd * 2), 2, dim=-1)
+        q = att.q_norm(qh).transpose(0, 1)
+        k = att.k_norm(att.k_proj(xe).view(T, -1, hd)).transpose(0, 1)
+        v = att.v_proj(xe).view(T, -1, hd).transpose(0, 1)
+        pos = torch.arange(N, N + T).view(1, 1, T).expand(3, 1, T)
+        cos, sin = itf.rot(xe.unsqueeze(0), pos)
+        qr, kr = apply_rotary_pos_emb(q.unsqueeze(0), k.unsqueeze(0), cos.float(), sin.float())
+        Hkv = k.shape[0]
+        G = q.shape[0] // Hkv
+        Kall = torch.cat([K, kr[0]], 1).double()
+        Vall = torch.cat([V, v], 1).double()
+        s = torch.einsum("kgtd,kcd->kgtc", qr[0].double().view(Hkv, G, T, hd), Kall) * att.scaling
+        col = torch.arange(N + T).view(1, -1)
+        s = s.masked_fill((col > N + torch.arange(T).view(-1, 1)).view(1, 1, T, -1), float("-inf"))
+        o = torch.einsum("kgtc,kcd->kgtd", torch.softmax(s, -1), Vall).reshape(-1, T, hd).transpose(0, 1).reshape(T, -1)
+        y = itf.Bmap(li, att.o_proj((o * torch.sigmoid(gate.reshape(T, -1).double())).float()))
+    assert torch.allclose(got["y"], y, atol=1e-5), float((got["y"] - y).abs().max())
+    assert torch.equal(got["w"], torch.ones_like(got["w"]))
+    a = O.d18_lib_read(itf, li, x[:4], [(K, V)])
+    b = O.d18_lib_read(itf, li, x[4:], [(K, V)], past=a["past"])
+    assert torch.allclose(torch.cat([a["y"], b["y"]]), got["y"], atol=1e-5)
