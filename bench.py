@@ -148,9 +148,11 @@ def bench_prefill(args):
     torch.cuda.synchronize()
     frag_ms = (time.perf_counter() - t0) * 1e3
 
+    qh = torch.empty(q.shape[0], lib.d, dtype=torch.float16, device=dev)
+
     def fwd():
-        w, _, _ = ops.route_topk_rows(q, lib, plan, top_k=0)
-        r, p = ops.prefill_forward(q, w, lib, plan)
+        w, _, _ = ops.route_topk_rows(q, lib, plan, top_k=0, q_f16=qh)
+        r, p = ops.prefill_forward(q, w, lib, plan, qh=qh)
         return w, r, p
 
     def bwd(w, p):

@@ -65,12 +65,14 @@ int xenc_route_topk(const float* q, long long ldq, int M, int d,
  * row_ptr[g] .. row_ptr[g+1]-1; tile_ptr[g] = sum_{g'<g} ceil(T_g'/32) * ceil(C_g'/32) (G+1
  * entries, n_tiles = tile_ptr[G]).  Same outputs and top-k / softmax as xenc_route_topk; the dots
  * are computed as 32-row x 32-chunk fp32 tiles (each summary row read once per 32 query rows).
- * ldw <= 1364.  Replaces LibraryInjector.route (xenc/injector.py:220-229) for many tokens.
+ * ldw <= 1364.  q_f16 (optional, 16-byte aligned): also writes q as contiguous fp16 rows
+ * [M, d] (the operand of xenc_prefill_scores), from the same read of q.
+ * Replaces LibraryInjector.route (xenc/injector.py:220-229) for many tokens.
  */
 int xenc_route_topk_rows(const float* q, long long ldq, int M, int d, const float* S,
                          const int* chunk_ptr, const int* row_ptr, const int* tile_ptr, int G,
                          int n_tiles, int top_k, float route_temp, float* w_dense, long long ldw,
-                         int* idx, float* w_sel, int kk, void* stream);
+                         int* idx, float* w_sel, int kk, void* q_f16, void* stream);
 
 /*
  * Decode read over routed pages (split-K over slots, log-sum-exp merge):

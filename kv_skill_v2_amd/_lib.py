@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lock = threading.Lock()
 _lib = None
@@ -35,7 +35,7 @@ SIGNATURES = {
         c_void_p, c_longlong, c_int, c_int, c_void_p,  # q, ldq, M, d, S
         c_void_p, c_void_p, c_void_p, c_int, c_int,  # chunk_ptr, row_ptr, tile_ptr, G, n_tiles
         c_int, c_float, c_void_p, c_longlong,        # top_k, route_temp, w_dense, ldw
-        c_void_p, c_void_p, c_int, c_void_p]),       # idx, w_sel, kk, stream
+        c_void_p, c_void_p, c_int, c_void_p, c_void_p]),       # idx, w_sel, kk, stream
     "xenc_decode_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int]),
     "xenc_decode_workspace_init": (c_int, [c_void_p, c_size_t, c_int, c_void_p]),
     "xenc_library_read_decode": (c_int, [

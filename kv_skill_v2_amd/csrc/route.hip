@@ -304,12 +304,15 @@ __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
 
 // ------------------------------------------------------------------------------------------
 // Routing of many query rows (prefill / registration): rows are grouped by library and the
-// q . S dots of a 32-row x 32-chunk tile are one fp32 register-blocked GEMM tile (each summary
-// row is read once per 32 query rows instead of once per row).  Thread (tr, tc) of 256 owns rows
-// tr, tr + 16 and chunks tc, tc + 16; k steps of 128 through LDS (row stride 132 floats), the
-// next step's global loads in flight while the current step computes.  The raw dots land in
-// w_dense; route_rows_select_kernel then runs the same wave top-k + softmax as the per-row
-// kernel, one wave per row.  Fixed summation order per (row, chunk).
+// q . S dots of a 32-row x 32-chunk tile are one fp32 GEMM tile on MFMA (each summary row is read
+// once per 32 query rows instead of once per row).  k steps of 128 are staged through LDS (row
+// stride 132 floats) with coalesced loads, the next step's global loads in flight while the
+// current step computes; wave w multiplies columns [32w, 32w + 32) of every step with
+// v_mfma_f32_32x32x2f32, and the 4 partial tiles are summed through LDS in wave order.  The raw
+// dots land in w_dense; route_rows_select_kernel then runs the same top-k + softmax as the
+// per-row kernel, one wave per row.  Fixed summation order per (row, chunk).  When qh is given,
+// the first chunk tile of each row tile also writes the rows it stages as fp16 (qh [M, d]), the
+// operand of the MFMA read, so q is read from HBM once for both.
 constexpr int kRouteRows = 32, kRouteChunks = 32, kRouteK = 128, kRouteLd = kRouteK + 4;
 constexpr int kRouteLoads = kRouteRows * kRouteK / 4 / 256;   // float4 per thread per operand
 
@@ -325,7 +328,8 @@ __device__ __forceinline__ int find_tile_group(const int* __restrict__ tile_ptr,
 __global__ __launch_bounds__(256) void route_rows_logits_kernel(
     const float* __restrict__ q, long long ldq, int d, const float* __restrict__ S,
     const int* __restrict__ chunk_ptr, const int* __restrict__ row_ptr,
-    const int* __restrict__ tile_ptr, int G, float* __restrict__ w_dense, long long ldw) {
+    const int* __restrict__ tile_ptr, int G, float* __restrict__ w_dense, long long ldw,
+    _Float16* __restrict__ qh) {
   __shared__ float qs[kRouteRows * kRouteLd];
   __shared__ float ss[kRouteChunks * kRouteLd];
   const int b = blockIdx.x;
@@ -338,7 +342,6 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
   const int row0 = rbeg + (local / nct) * kRouteRows;
   const int cb0 = (local % nct) * kRouteChunks;
   const int tid = threadIdx.x;
-  const int tr = tid >> 4, tc = tid & 15;
   // Staging: 32 rows x 32 float4 per k step, kRouteLoads per thread and operand (rows / chunks
   // past the end re-read the last one; their dots are not stored).
   const float* qsrc[kRouteLoads];
@@ -361,7 +364,12 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
       sv[i] = in ? *reinterpret_cast<const float4*>(ssrc[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
-  float acc[2][2] = {};
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int lane = tid & (kWave - 1), wv = tid / kWave;
+  const int l32 = lane & 31, hl = lane >> 5;
+  const bool write_h = qh != nullptr && cb0 == 0;
+  f32x16 acc = {};
   load(0);
   for (int k0 = 0; k0 < d; k0 += kRouteK) {
     __syncthreads();   // the previous step's LDS reads are done
@@ -370,35 +378,44 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
       *reinterpret_cast<float4*>(&qs[lrow[i] * kRouteLd + lk[i]]) = qv[i];
       *reinterpret_cast<float4*>(&ss[lrow[i] * kRouteLd + lk[i]]) = sv[i];
     }
-    __syncthreads();
-    if (k0 + kRouteK < d) load(k0 + kRouteK);   // in flight during this step's FMAs
-#pragma unroll 8
-    for (int kk4 = 0; kk4 < kRouteK; kk4 += 4) {
-      float4 a[2], bb[2];
+    if (write_h) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i) a[i] = *reinterpret_cast<const float4*>(&qs[(tr + 16 * i) * kRouteLd + kk4]);
-#pragma unroll
-      for (int j = 0; j < 2; ++j) bb[j] = *reinterpret_cast<const float4*>(&ss[(tc + 16 * j) * kRouteLd + kk4]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[i][j] = fmaf(a[i].x, bb[j].x, acc[i][j]);
-          acc[i][j] = fmaf(a[i].y, bb[j].y, acc[i][j]);
-          acc[i][j] = fmaf(a[i].z, bb[j].z, acc[i][j]);
-          acc[i][j] = fmaf(a[i].w, bb[j].w, acc[i][j]);
+      for (int i = 0; i < kRouteLoads; ++i) {
+        const int row = row0 + lrow[i], k = k0 + lk[i];
+        if (row < rend && k < d) {
+          typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+          const half4 h = {(_Float16)qv[i].x, (_Float16)qv[i].y, (_Float16)qv[i].z, (_Float16)qv[i].w};
+          *reinterpret_cast<half4*>(qh + (long long)row * d + k) = h;
         }
+      }
+    }
+    __syncthreads();
+    if (k0 + kRouteK < d) load(k0 + kRouteK);   // in flight during this step's MFMAs
+    // Lane l feeds row / chunk l % 32 and columns kb + 4 (l / 32) .. + 3 to four MFMAs: MFMA i
+    // contracts column kb + 4h + i of both operands for lane half h.
+    constexpr int kPerWave = kRouteK / 4;
+#pragma unroll
+    for (int kq = 0; kq < kPerWave; kq += 8) {
+      const int kb = wv * kPerWave + kq + hl * 4;
+      const f32x4 a = *reinterpret_cast<const f32x4*>(&qs[l32 * kRouteLd + kb]);
+      const f32x4 b = *reinterpret_cast<const f32x4*>(&ss[l32 * kRouteLd + kb]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc, 0, 0, 0);
     }
   }
+  // acc[r] = partial dot of row 8(r/4) + 4hl + r%4, chunk l32.  Sum the 4 waves in order.
+  __syncthreads();
+  float* red = qs;   // 4 waves x 16 values x 64 lanes <= 32 x 132 floats
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = row0 + tr + 16 * i;
-    if (row >= rend) continue;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int c = cb0 + tc + 16 * j;
-      if (c < C) w_dense[(long long)row * ldw + c] = acc[i][j];
-    }
+  for (int r = 0; r < 16; ++r) red[(wv * 16 + r) * kWave + lane] = acc[r];
+  __syncthreads();
+  for (int i = tid; i < 16 * kWave; i += 256) {
+    const int r = i / kWave, ln = i % kWave;
+    const float v = ((red[(0 * 16 + r) * kWave + ln] + red[(1 * 16 + r) * kWave + ln]) +
+                     red[(2 * 16 + r) * kWave + ln]) + red[(3 * 16 + r) * kWave + ln];
+    const int row = row0 + (r >> 2) * 8 + (ln >> 5) * 4 + (r & 3);
+    const int c = cb0 + (ln & 31);
+    if (row < rend && c < C) w_dense[(long long)row * ldw + c] = v;
   }
 }
 
@@ -539,7 +556,7 @@ extern "C" int xenc_route_topk_rows(const float* q, long long ldq, int M, int d,
                                     const int* chunk_ptr, const int* row_ptr, const int* tile_ptr,
                                     int G, int n_tiles, int top_k, float route_temp,
                                     float* w_dense, long long ldw, int* idx, float* w_sel, int kk,
-                                    void* stream) {
+                                    void* q_f16, void* stream) {
   if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || ldw <= 0 || n_tiles < 0) return XENC_EINVAL;
   if (d % 8 != 0 || ldq < d || ldq % 4 != 0) return XENC_EINVAL;
   if (ldw > 1364) return XENC_EINVAL;  // up to 1364 chunks per library
@@ -547,10 +564,12 @@ extern "C" int xenc_route_topk_rows(const float* q, long long ldq, int M, int d,
   if (M == 0) return XENC_OK;
   if (!q || !S || !chunk_ptr || !row_ptr || !tile_ptr || !w_dense || !idx || !w_sel) return XENC_ENULL;
   if (!aligned16(q) || !aligned16(S)) return XENC_EALIGN;
+  if (q_f16 && n_tiles == 0) return XENC_EINVAL;
+  if (q_f16 && !aligned16(q_f16)) return XENC_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (n_tiles > 0)
     hipLaunchKernelGGL(route_rows_logits_kernel, dim3(n_tiles), dim3(256), 0, st, q, ldq, d, S,
-                       chunk_ptr, row_ptr, tile_ptr, G, w_dense, ldw);
+                       chunk_ptr, row_ptr, tile_ptr, G, w_dense, ldw, static_cast<_Float16*>(q_f16));
   hipLaunchKernelGGL(route_rows_select_kernel, dim3((M + kSelectWaves - 1) / kSelectWaves),
                      dim3(kSelectWaves * kWave), lds, st, M, chunk_ptr, row_ptr, nullptr, G, top_k,
                      route_temp, w_dense, (int)ldw, idx, w_sel, kk);

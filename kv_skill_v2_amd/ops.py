@@ -660,10 +660,11 @@ def unpack_p(p: torch.Tensor, M: int) -> torch.Tensor:
 
 
 def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
-                    read_temp: float = 12.0, softmax: bool = True):
+                    read_temp: float = 12.0, softmax: bool = True, qh: torch.Tensor | None = None):
     """(r [M, d] fp32, p fp16 octet-major [cmax*slots/8, M, 8]): the route-weighted masked-softmax
     (or linear) read of many query rows.  HIP kernels scores_kernel<0|2> + readout_kernel
-    (kv_skill_v2_amd/csrc/prefill.hip); unpack_p gives p row-major."""
+    (kv_skill_v2_amd/csrc/prefill.hip); unpack_p gives p row-major.  qh: q as fp16 rows already
+    (route_topk_rows(..., q_f16=) writes it); cast here when not given."""
     lib_.check_prefill()
     q = _query(q, lib_.d)
     M, d = q.shape
@@ -671,7 +672,10 @@ def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: 
         raise ValueError(f"q must have {plan.M} rows and w shape ({plan.M}, {lib_.cmax})")
     w = w.to(torch.float32).contiguous()
     L, st, N = lib(), stream_handle(q.device), lib_.slots_per_page
-    qh = cast_f16(q)
+    if qh is None:
+        qh = cast_f16(q)
+    elif qh.dtype != torch.float16 or qh.shape != (M, d) or not qh.is_contiguous():
+        raise ValueError(f"qh must be contiguous fp16 [{M}, {d}]")
     ka, vb = lib_.fragment_pages(0), lib_.fragment_pages(1, values=True)
     p = torch.empty(lib_.cmax * N // 8, M, 8, dtype=torch.float16, device=q.device)
     check(L.xenc_prefill_scores(0 if softmax else 2, ptr(qh), d, ptr(plan.row_ptr), ptr(plan.score_tiles),
@@ -730,10 +734,11 @@ def route_backward(w: torch.Tensor, dw: torch.Tensor, lib_: PagedLibrary, plan: 
 
 
 def route_topk_rows(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int = 0,
-                    route_temp: float = 10.0):
+                    route_temp: float = 10.0, q_f16: torch.Tensor | None = None):
     """route_topk for query rows grouped by library as in `plan` (rows of library g contiguous):
-    the q . S dots as 32 x 32 fp32 GEMM tiles, then the same wave top-k / softmax per row.
-    HIP kernels route_rows_logits_kernel + route_rows_select_kernel."""
+    the q . S dots as 32 x 32 fp32 MFMA tiles, then the same top-k / softmax per row.  HIP
+    kernels route_rows_logits_kernel + route_rows_select_kernel.  q_f16 (optional, fp16 [M, d]
+    contiguous) receives q as fp16 from the same read (prefill_forward's qh operand)."""
     q = _query(q, lib_.d)
     M = q.shape[0]
     if M != plan.M:
@@ -745,10 +750,13 @@ def route_topk_rows(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: i
     wsel = torch.empty(M, kk, dtype=torch.float32, device=dev)
     if M == 0:
         return w, idx, wsel
+    if q_f16 is not None and (q_f16.dtype != torch.float16 or q_f16.shape != (M, lib_.d)
+                              or not q_f16.is_contiguous()):
+        raise ValueError(f"q_f16 must be contiguous fp16 [{M}, {lib_.d}]")
     check(lib().xenc_route_topk_rows(ptr(q), q.stride(0), M, lib_.d, ptr(lib_.S), ptr(lib_.chunk_ptr),
                                      ptr(plan.row_ptr), ptr(plan.logit_tiles), lib_.n_libraries, plan.n_logit,
                                      int(top_k), float(route_temp), ptr(w), w.stride(0), ptr(idx), ptr(wsel),
-                                     kk, stream_handle(dev)), "xenc_route_topk_rows")
+                                     kk, ptr(q_f16), stream_handle(dev)), "xenc_route_topk_rows")
     return w, idx, wsel
 
 
@@ -761,11 +769,14 @@ class RouteFn(torch.autograd.Function):
     """w [M, cmax] = route(q); differentiable in q through the softmax over the kept logits."""
 
     @staticmethod
-    def forward(ctx, q, lib_, plan, top_k, route_temp):
+    def forward(ctx, q, lib_, plan, top_k, route_temp, qh=None):
         if plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
-            w, idx, wsel = route_topk_rows(q.detach(), lib_, plan, top_k=top_k, route_temp=route_temp)
+            w, idx, wsel = route_topk_rows(q.detach(), lib_, plan, top_k=top_k, route_temp=route_temp,
+                                           q_f16=qh)
         else:
             qg = _plan_groups(plan).to(q.device)
+            if qh is not None:
+                raise ValueError("qh is written by the row-grouped routing path only")
             w, idx, wsel = route_topk(q.detach(), lib_, qg, top_k=top_k, route_temp=route_temp)
         ctx.save_for_backward(w)
         ctx.lib, ctx.plan, ctx.route_temp = lib_, plan, route_temp
@@ -778,15 +789,15 @@ class RouteFn(torch.autograd.Function):
         dq = torch.zeros(w.shape[0], ctx.lib.d, dtype=torch.float32, device=w.device)
         if dw is not None:
             route_backward(w, dw, ctx.lib, ctx.plan, ctx.route_temp, dq)
-        return dq, None, None, None, None
+        return dq, None, None, None, None, None
 
 
 class ReadFn(torch.autograd.Function):
     """r [M, d] = route-weighted masked-softmax (or linear) read; differentiable in q and w."""
 
     @staticmethod
-    def forward(ctx, q, w, lib_, plan, read_temp, softmax=True):
-        r, p = prefill_forward(q.detach(), w.detach(), lib_, plan, read_temp, softmax)
+    def forward(ctx, q, w, lib_, plan, read_temp, softmax=True, qh=None):
+        r, p = prefill_forward(q.detach(), w.detach(), lib_, plan, read_temp, softmax, qh=qh)
         ctx.save_for_backward(w, p)
         ctx.lib, ctx.plan, ctx.read_temp, ctx.softmax = lib_, plan, read_temp, softmax
         return r
@@ -795,14 +806,19 @@ class ReadFn(torch.autograd.Function):
     def backward(ctx, dr):
         w, p = ctx.saved_tensors
         dq, gamma = prefill_backward(dr, w, p, ctx.lib, ctx.plan, ctx.read_temp, ctx.softmax)
-        return dq, gamma, None, None, None, None
+        return dq, gamma, None, None, None, None, None
 
 
 def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int = 0,
                  read_temp: float = 12.0, route_temp: float = 10.0, read_softmax: bool = True):
-    """(r [M, d], w [M, cmax]) with autograd through both routing and the read (MFMA path)."""
-    w, _, _ = RouteFn.apply(q, lib_, plan, int(top_k), float(route_temp))
-    r = ReadFn.apply(q, w, lib_, plan, float(read_temp), bool(read_softmax))
+    """(r [M, d], w [M, cmax]) with autograd through both routing and the read (MFMA path).  The
+    routing pass also writes the fp16 rows the read takes, so q is read from HBM once."""
+    lib_.check_prefill()
+    qh = None
+    if plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
+        qh = torch.empty(plan.M, lib_.d, dtype=torch.float16, device=_query(q, lib_.d).device)
+    w, _, _ = RouteFn.apply(q, lib_, plan, int(top_k), float(route_temp), qh)
+    r = ReadFn.apply(q, w, lib_, plan, float(read_temp), bool(read_softmax), qh)
     return r, w
 
 

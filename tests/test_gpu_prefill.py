@@ -161,6 +161,35 @@ def test_route_rows_matches_per_row_kernel(dev, counts, rows, top_k):
         off += T
 
 
+@pytest.mark.parametrize("counts,rows", [([32, 7, 130], [300, 64, 129]), ([3], [33]), ([40, 2], [1, 97])])
+def test_route_rows_fp16_rows_are_the_cast(dev, counts, rows):
+    """The routing pass's fp16 copy of q (q_f16) equals cast_f16 bit for bit on every row (ragged
+    row tiles, several chunk tiles per row tile), and prefill_forward gives the same bits with it
+    as with its own cast; library_read, which shares the copy between routing and read, equals
+    the two calls."""
+    say("route rows fp16 rows", dict(counts=counts, rows=rows))
+    d = 128
+    P = synth.pool(counts, 64, d, device="cpu", tail_lo=1)
+    lib = _lib(P, dev)
+    plan = ops.row_plan(lib, rows)
+    q = synth.queries(sum(rows), d, device=dev, seed=5)
+    qh = torch.full((q.shape[0], d), float("nan"), dtype=torch.float16, device=dev)
+    w, _, _ = ops.route_topk_rows(q, lib, plan, top_k=0, q_f16=qh)
+    assert torch.equal(qh, ops.cast_f16(q))
+    r1, p1 = ops.prefill_forward(q, w, lib, plan, qh=qh)
+    r2, p2 = ops.prefill_forward(q, w, lib, plan)
+    assert torch.equal(r1, r2)
+    u1, u2 = ops.unpack_p(p1, q.shape[0]), ops.unpack_p(p2, q.shape[0])
+    off = 0
+    for g, T in enumerate(rows):                 # p is written for each library's own chunks only
+        n = counts[g] * 64
+        assert torch.equal(u1[off:off + T, :n], u2[off:off + T, :n]), g
+        off += T
+    if sum(rows) >= ops.ROUTE_ROWS_MIN:
+        r3, w3 = ops.library_read(q, lib, plan)
+        assert torch.equal(r3, r2) and torch.equal(w3, w)
+
+
 def test_prefill_single_slot_chunks(dev):
     """Chunks of 1 and 3 valid slots next to a full one, softmax and linear, forward and dQ."""
     say("prefill 1-slot chunks")
