@@ -14,8 +14,9 @@
 // an online softmax in the log2 domain, and for a document also the max / sum of the keys past
 // `skip`.  A key row of hd elements is read by hd / EPL lanes (16-byte loads); lane groups merge
 // by shuffles and the 4 waves through LDS, in a fixed order.  d18_merge_kernel: one workgroup per
-// (row, query head) merges the splits, joins each document with the own rows (o_d), forms r, rmax
-// and the routing weights, and sums w_d o_d.  Deterministic: every sum runs in a fixed order.
+// (row, query head, 64 output dims) merges the splits, joins each document with the own rows
+// (o_d), forms r, rmax and the routing weights, and sums w_d o_d.  Deterministic: every sum runs
+// in a fixed order.
 #include <algorithm>
 
 #include "xenc_common.h"
@@ -23,8 +24,11 @@
 namespace xenc {
 namespace {
 
-constexpr int kD18Threads = 256;
+constexpr int kD18Threads = 256;                      // merge kernel
 constexpr int kD18Waves = kD18Threads / kWave;
+constexpr int kD18PartThreads = 256;                  // partials kernel (one wave per SIMD: 512 threads
+                                                      // cap a wave at 256 registers and spill)
+constexpr int kD18PartWaves = kD18PartThreads / kWave;
 constexpr int kD18MaxG = 8;
 constexpr int kD18MaxHd = 256;
 constexpr int kD18MaxDocs = 64;
@@ -37,28 +41,26 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 template <typename T> struct D18Elem { static constexpr int EPL = 8; };   // 16-bit keys
 template <> struct D18Elem<float> { static constexpr int EPL = 4; };
 
+// 16 bytes of T at p (16-byte aligned) as EPL fp32 values.
 template <typename T>
-__device__ __forceinline__ void load_f32(const T* p, float (&f)[D18Elem<T>::EPL]);
-template <> __device__ __forceinline__ void load_f32<_Float16>(const _Float16* p, float (&f)[8]) {
+__device__ __forceinline__ void load_f32(const T* p, float (&f)[D18Elem<T>::EPL]) {
   const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+  if constexpr (sizeof(T) == 4) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(v[i] & 0xffffu));
-    f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(v[i] >> 16));
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
+  } else if constexpr (__is_same(T, __bf16)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = __uint_as_float(v[i] << 16);
+      f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = (float)__builtin_bit_cast(_Float16, (unsigned short)(v[i] & 0xffffu));
+      f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (unsigned short)(v[i] >> 16));
+    }
   }
-}
-template <> __device__ __forceinline__ void load_f32<__bf16>(const __bf16* p, float (&f)[8]) {
-  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __uint_as_float(v[i] << 16);
-    f[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
-  }
-}
-template <> __device__ __forceinline__ void load_f32<float>(const float* p, float (&f)[4]) {
-  const f32x4_t v = *reinterpret_cast<const f32x4_t*>(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) f[i] = v[i];
 }
 
 // 2^(m - M) with m = -inf (an empty state) -> 0, also when M = -inf.
@@ -97,8 +99,8 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // LDS of one unit: per wave and query head the state (m, l, mc, lc) and the accumulator.
 struct D18Lds {
-  float st[kD18Waves][kD18MaxG][4];
-  float acc[kD18Waves][kD18MaxG][kD18MaxHd];
+  float st[kD18PartWaves][kD18MaxG][4];
+  float acc[kD18PartWaves][kD18MaxG][kD18MaxHd];
 };
 
 // One key split (n keys, the first at index j_base of its unit; n <= 0: empty) for the G query
@@ -117,7 +119,7 @@ __device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
   constexpr int EPL = D18Elem<TK>::EPL;
   constexpr int TPR = HD / EPL;              // lanes per key row: a power of two <= 64
   constexpr int KPW = kWave / TPR;           // keys per wave and load slot
-  constexpr int STEP = kD18Waves * KPW * kD18Kif;
+  constexpr int STEP = kD18PartWaves * KPW * kD18Kif;
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
   const int grp = lane / TPR, e0 = (lane % TPR) * EPL;
@@ -133,44 +135,82 @@ __device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
     m[g] = mc[g] = -INFINITY;
     l[g] = lc[g] = 0.f;
   }
-  for (int j0 = 0; j0 < n; j0 += STEP) {
-    float kf[kD18Kif][EPL], vf[kD18Kif][EPL];
+  // Keys j0 .. j0 + STEP - 1: issue the K / V loads of lane group grp (rows past n re-read the
+  // last row and are masked when consumed).
+  auto load_step = [&](float (&kf)[kD18Kif][EPL], float (&vf)[kD18Kif][EPL], int j0) {
 #pragma unroll
     for (int i = 0; i < kD18Kif; ++i) {
-      const int j = j0 + (i * kD18Waves + wv) * KPW + grp;
-      const long long row = (long long)(j < n ? j : n - 1) * s_n + e0;   // n >= 1 inside the loop
+      const int j = j0 + (i * kD18PartWaves + wv) * KPW + grp;
+      const long long row = (long long)(j < n ? j : n - 1) * s_n + e0;   // n >= 1 here
       load_f32<TK>(K + row, kf[i]);
       load_f32<TK>(V + row, vf[i]);
     }
+  };
+  // Content statistics of the split: none (own rows, or every key before skip_c), all (every key
+  // at or past skip_c: then they equal (m, l) and are copied at the end), or per key (the split
+  // that holds key skip_c).  Workgroup-uniform.
+  const int cmode = skip_c < 0 || j_base + n <= skip_c ? 0 : j_base >= skip_c ? 1 : 2;
+  // The lane group's kD18Kif keys of a step enter the online softmax as one block: one max
+  // update and one rescale of the accumulator per query head.
+  auto consume_step = [&](const float (&kf)[kD18Kif][EPL], const float (&vf)[kD18Kif][EPL], int j0) {
+    float sc[kD18Kif][GP];
+    bool ok[kD18Kif], cont[kD18Kif];
 #pragma unroll
     for (int i = 0; i < kD18Kif; ++i) {
-      const int j = j0 + (i * kD18Waves + wv) * KPW + grp;
-      float p[GP];
+      const int j = j0 + (i * kD18PartWaves + wv) * KPW + grp;
+      ok[i] = j < n;
+      cont[i] = ok[i] && j_base + j >= skip_c;
 #pragma unroll
       for (int g = 0; g < GP; ++g) {
-        p[g] = 0.f;
+        float p = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) p[g] = fmaf(qv[g][e], kf[i][e], p[g]);
+        for (int e = 0; e < EPL; ++e) p = fmaf(qv[g][e], kf[i][e], p);
+        sc[i][g] = group_sum<TPR>(p) * scale_log2;
       }
+    }
 #pragma unroll
-      for (int g = 0; g < GP; ++g) p[g] = group_sum<TPR>(p[g]);
-      if (j < n) {
+    for (int g = 0; g < GP; ++g) {
+      float mn = m[g];
 #pragma unroll
-        for (int g = 0; g < GP; ++g) {
-          const float s = p[g] * scale_log2;
-          const float mn = fmaxf(m[g], s);
-          const float a = rescale(m[g], mn), b = __builtin_amdgcn_exp2f(s - mn);
-          l[g] = l[g] * a + b;
+      for (int i = 0; i < kD18Kif; ++i) mn = ok[i] ? fmaxf(mn, sc[i][g]) : mn;
+      const float a = rescale(m[g], mn);
+      float b[kD18Kif];
 #pragma unroll
-          for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(acc[g][e], a, b * vf[i][e]);
-          m[g] = mn;
-          if (skip_c >= 0 && j_base + j >= skip_c) {
-            const float mcn = fmaxf(mc[g], s);
-            lc[g] = lc[g] * rescale(mc[g], mcn) + __builtin_amdgcn_exp2f(s - mcn);
-            mc[g] = mcn;
-          }
-        }
+      for (int i = 0; i < kD18Kif; ++i) b[i] = ok[i] ? __builtin_amdgcn_exp2f(sc[i][g] - mn) : 0.f;
+      float ls = l[g] * a;
+#pragma unroll
+      for (int i = 0; i < kD18Kif; ++i) ls += b[i];
+      l[g] = ls;
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) {
+        float x = acc[g][e] * a;
+#pragma unroll
+        for (int i = 0; i < kD18Kif; ++i) x = fmaf(b[i], vf[i][e], x);
+        acc[g][e] = x;
       }
+      m[g] = mn;
+      if (cmode == 2) {
+        float mcn = mc[g];
+#pragma unroll
+        for (int i = 0; i < kD18Kif; ++i) mcn = cont[i] ? fmaxf(mcn, sc[i][g]) : mcn;
+        float lcs = lc[g] * rescale(mc[g], mcn);
+#pragma unroll
+        for (int i = 0; i < kD18Kif; ++i) lcs += cont[i] ? __builtin_amdgcn_exp2f(sc[i][g] - mcn) : 0.f;
+        lc[g] = lcs;
+        mc[g] = mcn;
+      }
+    }
+  };
+  float kf[kD18Kif][EPL], vf[kD18Kif][EPL];
+  for (int j0 = 0; j0 < n; j0 += STEP) {
+    load_step(kf, vf, j0);
+    consume_step(kf, vf, j0);
+  }
+  if (cmode == 1) {
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+      mc[g] = m[g];
+      lc[g] = l[g];
     }
   }
   // Lane groups of the wave (same columns, different keys): butterfly merge.
@@ -194,7 +234,7 @@ __device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
       mc[g] = Mc;
     }
   }
-  // The 4 waves through LDS, in wave order.
+  // The 4 waves through LDS, summed in wave order.
   if (grp == 0) {
 #pragma unroll
     for (int g = 0; g < GP; ++g) {
@@ -209,27 +249,27 @@ __device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < G * HD; i += kD18Threads) {
+  for (int i = threadIdx.x; i < G * HD; i += kD18PartThreads) {
     const int g = i / HD, e = i % HD;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kD18Waves; ++w) M = fmaxf(M, lds.st[w][g][0]);
+    for (int w = 0; w < kD18PartWaves; ++w) M = fmaxf(M, lds.st[w][g][0]);
     float a = 0.f;
 #pragma unroll
-    for (int w = 0; w < kD18Waves; ++w) a += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
+    for (int w = 0; w < kD18PartWaves; ++w) a += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
     acc_out[i] = a;
   }
   if (threadIdx.x < G) {
     const int g = threadIdx.x;
     float M = -INFINITY, Mc = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kD18Waves; ++w) {
+    for (int w = 0; w < kD18PartWaves; ++w) {
       M = fmaxf(M, lds.st[w][g][0]);
       Mc = fmaxf(Mc, lds.st[w][g][2]);
     }
     float L = 0.f, Lc = 0.f;
 #pragma unroll
-    for (int w = 0; w < kD18Waves; ++w) {
+    for (int w = 0; w < kD18PartWaves; ++w) {
       L += lds.st[w][g][1] * rescale(lds.st[w][g][0], M);
       Lc += lds.st[w][g][3] * rescale(lds.st[w][g][2], Mc);
     }
@@ -242,7 +282,7 @@ __device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
 // ceil((P + T) / S), cut at row t's causal end P + t + 1).  Layout: part_ml [T][hkv][D + 1][S][G],
 // part_acc [T][hkv][D + 1][S][G][hd].
 template <typename TD, int HD, int GP>
-__global__ __launch_bounds__(kD18Threads) void d18_partials_kernel(
+__global__ __launch_bounds__(kD18PartThreads) void d18_partials_kernel(
     int hq, int hkv, int n_docs, int S, const float* __restrict__ qd, const float* __restrict__ qo,
     const TD* __restrict__ kd, const TD* __restrict__ vd, long long s_dh, long long s_dn,
     const int* __restrict__ doc_ptr, const float* __restrict__ ko, const float* __restrict__ vo,
@@ -272,11 +312,16 @@ __global__ __launch_bounds__(kD18Threads) void d18_partials_kernel(
   }
 }
 
-// One workgroup per (row t, kv head h, query head g), blockIdx.x = (t * hkv + h) * G + g.  The
-// S splits of every unit are merged first (in split order): their rescale factors and the unit
-// states go to LDS.  Wave 0 forms the routing weights (one lane per document); then thread e
-// sums o[e] = sum_d w_d o_d[e], o_d the join of document d and the own rows.
+// One workgroup per (row t, kv head h, query head g) and block of 64 output dims:
+// blockIdx.x = (t * hkv + h) * G + g, blockIdx.y = dim block.  The S splits of every unit are
+// merged first (in split order): their rescale factors and the unit states go to LDS.  Wave 0
+// forms the routing weights (one lane per document; block 0 writes w, r, rmax).  Then wave v
+// merges the split accumulators of units v, v + 4, ... for the block's dims (lane = dim, all S
+// loads of two units in flight) into LDS, and wave 0 sums o[e] = sum_d w_d o_d[e], o_d the join
+// of document d and the own rows.
 // w, r, rmax: [hkv][G][T][D] (the reference's [Hkv, G, T, D]); out: [T][hq][hd].
+constexpr int kD18MergeDims = kWave;
+
 __global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(
     int T, int hq, int hkv, int hd, int n_docs, int S, const float4* __restrict__ part_ml,
     const float* __restrict__ part_acc, float beta, int top_k, int force, const float* __restrict__ wfix,
@@ -285,6 +330,7 @@ __global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(
   __shared__ float4 ust[kD18MaxDocs + 1];                       // per unit: (M, L, Mc, Lc) over splits
   __shared__ float fac[(kD18MaxDocs + 1) * kD18MaxSplits];      // 2^(m_split - M_unit)
   __shared__ float4 sst[(kD18MaxDocs + 1) * kD18MaxSplits];     // the split states
+  __shared__ float ua[kD18MaxDocs + 1][kD18MergeDims];          // per unit: the merged accumulator
   const int G = hq / hkv, U = n_docs + 1;
   const int g = blockIdx.x % G, th = blockIdx.x / G;
   const int t = th / hkv, h = th % hkv;
@@ -342,34 +388,50 @@ __global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(
       w = e / wave_sum(e);
     }
     if (has) {
-      const long long o = (((long long)h * G + g) * T + t) * n_docs + d;
-      w_out[o] = w;
-      r_out[o] = r;
-      rmax_out[o] = st.w > 0.f ? st.z * kLn2 : -INFINITY;
+      if (blockIdx.y == 0) {
+        const long long o = (((long long)h * G + g) * T + t) * n_docs + d;
+        w_out[o] = w;
+        r_out[o] = r;
+        rmax_out[o] = st.w > 0.f ? st.z * kLn2 : -INFINITY;
+      }
       wl[d] = w;
     }
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < hd; e += kD18Threads) {
-    // All S partial accumulators of a unit are loaded before they are summed (in split order).
-    auto unit_acc = [&](int u) {
-      float v[kD18MaxSplits];
+  // Wave wv: the split sums of units wv, wv + 4, ... for dim e (in split order), all S loads of
+  // two units in flight.
+  const int e = blockIdx.y * kD18MergeDims + lane;
+  const int ec = min(e, hd - 1);   // lanes past hd load a valid dim and store nothing
+  for (int u0 = wv; u0 < U; u0 += 2 * kD18Waves) {
+    const int u1 = u0 + kD18Waves;
+    const bool two = u1 < U;   // wave-uniform
+    float v0[kD18MaxSplits], v1[kD18MaxSplits];
 #pragma unroll
-      for (int sp = 0; sp < kD18MaxSplits; ++sp) v[sp] = sp < S ? part_acc[slot(u, sp) * hd + e] : 0.f;
-      float a = 0.f;
+    for (int sp = 0; sp < kD18MaxSplits; ++sp) {
+      v0[sp] = sp < S ? part_acc[slot(u0, sp) * hd + ec] : 0.f;
+      v1[sp] = two && sp < S ? part_acc[slot(u1, sp) * hd + ec] : 0.f;
+    }
+    float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+    for (int sp = 0; sp < kD18MaxSplits; ++sp)
+      if (sp < S) a0 = fmaf(v0[sp], fac[u0 * S + sp], a0);
+    ua[u0][lane] = a0;
+    if (two) {
 #pragma unroll
       for (int sp = 0; sp < kD18MaxSplits; ++sp)
-        if (sp < S) a = fmaf(v[sp], fac[u * S + sp], a);
-      return a;
-    };
+        if (sp < S) a1 = fmaf(v1[sp], fac[u1 * S + sp], a1);
+      ua[u1][lane] = a1;
+    }
+  }
+  __syncthreads();   // ua and wl complete
+  if (wv == 0 && e < hd) {
     const float4 so = ust[n_docs];
-    const float ao = unit_acc(n_docs);
+    const float ao = ua[n_docs][lane];
     float o = 0.f;
     for (int d = 0; d < n_docs; ++d) {
       const float4 sd = ust[d];
       const float M = fmaxf(sd.x, so.x);
       const float a = rescale(sd.x, M), b = rescale(so.x, M);
-      o = fmaf(wl[d], (unit_acc(d) * a + ao * b) / (sd.y * a + so.y * b), o);
+      o = fmaf(wl[d], (ua[d][lane] * a + ao * b) / (sd.y * a + so.y * b), o);
     }
     out[((long long)t * hq + (long long)h * G + g) * hd + e] = o;
   }
@@ -422,7 +484,7 @@ extern "C" int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_do
   // Query heads per kv head padded to 1, 2, 4 or 8 (padded heads have q = 0 and are not written).
   const int G = hq / hkv, GP = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
 #define XENC_D18_LAUNCH(TD, HDV, GPV)                                                              \
-  hipLaunchKernelGGL((d18_partials_kernel<TD, HDV, GPV>), grid, dim3(kD18Threads), 0, st, hq, hkv,   \
+  hipLaunchKernelGGL((d18_partials_kernel<TD, HDV, GPV>), grid, dim3(kD18PartThreads), 0, st, hq, hkv, \
                      n_docs, nsplit, qd, qo, static_cast<const TD*>(k_docs),                         \
                      static_cast<const TD*>(v_docs), s_dh, s_dn, doc_ptr, k_own, v_own, s_oh, s_on, P, \
                      T, sl2, skip, part_ml, part_acc)
@@ -448,7 +510,8 @@ extern "C" int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_do
 #undef XENC_D18_HD
 #undef XENC_D18_GP
 #undef XENC_D18_LAUNCH
-  hipLaunchKernelGGL(d18_merge_kernel, dim3((unsigned)(T * hq)), dim3(kD18Threads), 0, st, T, hq, hkv, hd,
+  hipLaunchKernelGGL(d18_merge_kernel, dim3((unsigned)(T * hq), (unsigned)((hd + kD18MergeDims - 1) / kD18MergeDims)),
+                     dim3(kD18Threads), 0, st, T, hq, hkv, hd,
                      n_docs, nsplit, part_ml, part_acc, beta, top_k, force, wfix, out, w, r, rmax);
   return check_launch();
 }
