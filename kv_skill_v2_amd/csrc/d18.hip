@@ -68,35 +68,6 @@ __device__ __forceinline__ float rescale(float m, float M) {
   return m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
 }
 
-// Sum over each aligned group of TPR lanes (a power of two <= 64), every lane of the group ending
-// with the same bits.  Inside a 16-lane row the partner values come by DPP (quad xor 1, xor 2,
-// half-row mirror, row mirror), across rows by the gfx950 permlane swaps, so the VALU does the
-// whole reduction (no LDS-pipe permutes).  Each step adds the two halves in the same order in
-// both lanes of a pair.
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
-}
-
-template <int TPR>
-__device__ __forceinline__ float group_sum(float v) {
-  if constexpr (TPR >= 2) v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
-  if constexpr (TPR >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
-  if constexpr (TPR >= 8) v += dpp_f<0x141>(v);   // row_half_mirror: the other quad of the 8
-  if constexpr (TPR >= 16) v += dpp_f<0x140>(v);  // row_mirror: the other 8 of the row
-  if constexpr (TPR >= 32) {                    // rows 2i, 2i+1: (even row) + (odd row) in both
-    const unsigned u = __float_as_uint(v);
-    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-  if constexpr (TPR >= 64) {                    // lanes 0-31 + lanes 32-63 in both halves
-    const unsigned u = __float_as_uint(v);
-    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  }
-  return v;
-}
-
 // LDS of one unit: per wave and query head the state (m, l, mc, lc) and the accumulator.
 struct D18Lds {
   float st[kD18PartWaves][kD18MaxG][4];

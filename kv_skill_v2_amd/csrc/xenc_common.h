@@ -44,10 +44,59 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// DPP move of x with the given control (row_mask / bank_mask all, bound_ctrl on): a VALU
+// operand, no LDS-pipe permute.
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
+}
+
+// The value of lane ^ MASK (MASK 32 or 16) by the gfx950 permlane swaps.  hi = (lane & MASK) != 0.
+// permlane32_swap exchanges lanes 32-63 of its first operand with lanes 0-31 of its second
+// (permlane16_swap: the odd 16-lane rows with the even rows), so with x in both the first result
+// holds the partner's value in the upper lanes and the second in the lower lanes.
+template <int MASK>
+__device__ __forceinline__ float swap_partner(float x, bool hi) {
+  static_assert(MASK == 32 || MASK == 16, "permlane swaps pair lanes at distance 32 or 16");
+  const unsigned u = __float_as_uint(x);
+  if constexpr (MASK == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(hi ? r[0] : r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    return __uint_as_float(hi ? r[0] : r[1]);
+  }
+}
+
+// Sum over each aligned group of TPR lanes (a power of two <= 64), every lane of the group ending
+// with the same bits.  Inside a 16-lane row the partner values come by DPP (quad xor 1, xor 2,
+// half-row mirror, row mirror), across rows by the permlane swaps, so the VALU does the whole
+// reduction.  Each step adds the two halves in the same order in both lanes of a pair.
+template <int TPR>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (TPR >= 2) v += dpp_f<0xB1>(v);    // quad_perm [1,0,3,2]
+  if constexpr (TPR >= 4) v += dpp_f<0x4E>(v);    // quad_perm [2,3,0,1]
+  if constexpr (TPR >= 8) v += dpp_f<0x141>(v);   // row_half_mirror: the other quad of the 8
+  if constexpr (TPR >= 16) v += dpp_f<0x140>(v);  // row_mirror: the other 8 of the row
+  if constexpr (TPR >= 32) {                    // rows 2i, 2i+1: (even row) + (odd row) in both
+    const unsigned u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if constexpr (TPR >= 64) {                    // lanes 0-31 + lanes 32-63 in both halves
+    const unsigned u = __float_as_uint(v);
+    const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  return v;
+}
+
 // Reduce SPT per-lane partial values over the 64 lanes.  On return v[0] holds, in every lane,
 // the full sum for slot j = lane / (64 / SPT).  Step with lane bit MASK: lanes with the bit set
 // keep the upper half of the remaining values, send the lower half to their partner and add
-// what they receive.  Written as compile-time recursion so every array index is a constant.
+// what they receive.  The steps at lane distance 32 and 16 go through the permlane swaps; once
+// one value is left at distance 8, the 16-lane row is summed by DPP.  Written as compile-time
+// recursion so every array index is a constant.
 template <int SPT, int CNT = SPT, int MASK = 32>
 __device__ __forceinline__ void wave_reduce_scatter(float (&v)[SPT], int lane) {
   static_assert(SPT >= 1 && SPT <= 64 && (SPT & (SPT - 1)) == 0, "SPT must be a power of 2");
@@ -58,9 +107,18 @@ __device__ __forceinline__ void wave_reduce_scatter(float (&v)[SPT], int lane) {
     for (int i = 0; i < H; ++i) {
       const float send = hi ? v[i] : v[i + H];
       const float keep = hi ? v[i + H] : v[i];
-      v[i] = keep + shfl_xor(send, MASK);
+      if constexpr (MASK >= 16) {
+        v[i] = keep + swap_partner<MASK>(send, hi);
+      } else {
+        v[i] = keep + shfl_xor(send, MASK);
+      }
     }
     wave_reduce_scatter<SPT, H, MASK / 2>(v, lane);
+  } else if constexpr (MASK >= 16) {
+    v[0] += swap_partner<MASK>(v[0], (lane & MASK) != 0);
+    wave_reduce_scatter<SPT, 1, MASK / 2>(v, lane);
+  } else if constexpr (MASK == 8) {
+    v[0] = group_sum<16>(v[0]);
   } else if constexpr (MASK >= 1) {
     v[0] += shfl_xor(v[0], MASK);
     wave_reduce_scatter<SPT, 1, MASK / 2>(v, lane);
