@@ -33,7 +33,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="batched_paged_decode",
                     choices=["batched_paged_decode", "single_decode", "prefill", "multi_depth",
-                             "pool_build", "d18"])
+                             "pool_build", "d18", "op_b"])
     ap.add_argument("--nsplit", type=int, default=None)
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
@@ -531,6 +531,97 @@ def bench_d18(args):
     print(json.dumps(res), flush=True)
 
 
+def bench_op_b(args):
+    """Op B, the vLLM plugin's decode read (DecodeReader, xenc/d23_read_kernels.py:134-160), at the
+    serving shape of the reference's batch benchmark (xenc's scripts/bench_d23_vllm.py: Qwen3.5-9B
+    reader, batches up to 32, documents of 16k tokens): 32 decode rows, each over its own
+    16,384-row document operator joined with 64 own rows; hq 16, hkv 4, head dim 256, bf16 pools of
+    16-row blocks, block tables a seeded shuffle of the pools.  One step = one DecodeReader call (a
+    single xenc_paged_decode_joint launch).  Algorithmic bytes: every routed K and V row once
+    (rows x hkv x d x 2 B x 2), plus q and the fp32 outputs."""
+    from kv_skill_v2_amd.decode_reader import DecodeReader
+
+    dev = torch.device("cuda:0")
+    B, hq, hkv, d, bs, op_len, own_len = 32, 16, 4, 256, 16, 16384, 64
+    dt = torch.bfloat16
+    g = torch.Generator(device=dev)
+    g.manual_seed(23)
+    nb_op, nb_own = B * op_len // bs, B * own_len // bs
+    op_k = torch.randn(nb_op, bs, hkv, d, generator=g, device=dev).to(dt)
+    op_v = torch.randn(nb_op, bs, hkv, d, generator=g, device=dev).to(dt)
+    own_k = torch.randn(nb_own, bs, hkv, d, generator=g, device=dev).to(dt)
+    own_v = torch.randn(nb_own, bs, hkv, d, generator=g, device=dev).to(dt)
+    gc = torch.Generator().manual_seed(4)
+    op_bt = torch.randperm(nb_op, generator=gc).to(torch.int32).view(B, op_len // bs).to(dev)
+    own_bt = torch.randperm(nb_own, generator=gc).to(torch.int32).view(B, own_len // bs).to(dev)
+    op_l = torch.full((B,), op_len, dtype=torch.int32, device=dev)
+    own_l = torch.full((B,), own_len, dtype=torch.int32, device=dev)
+    q = torch.randn(B, hq, d, generator=g, device=dev).to(dt)
+    scale = d ** -0.5
+    chunk = 1024
+    dec = DecodeReader(B, hq, hkv, d, max_keys=op_len + own_len, device=dev, chunk=chunk)
+
+    def call():
+        return dec(q, op_k, op_v, op_bt, op_l, own_k, own_v, own_bt, own_l, scale)
+
+    alg_bytes = B * (op_len + own_len) * hkv * d * 2 * 2 + B * hq * d * (2 + 4)
+    for _ in range(args.warmup):
+        call()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
+    t0 = time.perf_counter()
+    for a, b in ev:
+        a.record(stream)
+        call()
+        b.record(stream)
+    torch.cuda.synchronize()
+    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    k_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    achieved = alg_bytes / (k_ms * 1e-3) / 1e9
+    cpu = None
+    if args.cpu_sample > 0:
+        import oracle as O
+        torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
+        rows = min(B, max(1, args.cpu_sample // 4))
+        need_op = op_bt[:rows].cpu().long()
+        need_own = own_bt[:rows].cpu().long()
+        # Only the blocks of the sampled rows go to the host, renumbered in table order.
+        a_op = (op_k[need_op.flatten()].cpu(), op_v[need_op.flatten()].cpu())
+        a_own = (own_k[need_own.flatten()].cpu(), own_v[need_own.flatten()].cpu())
+        bt_op = torch.arange(need_op.numel(), dtype=torch.int32).view(rows, -1)
+        bt_own = torch.arange(need_own.numel(), dtype=torch.int32).view(rows, -1)
+        qc, lo_c, lw_c = q[:rows].cpu(), op_l[:rows].cpu(), own_l[:rows].cpu()
+
+        def cpu_call():
+            O.decode_read_ref(qc, a_op[0], a_op[1], bt_op, lo_c, a_own[0], a_own[1], bt_own, lw_c, scale)
+
+        cpu_call()
+        ts = []
+        for _ in range(max(1, args.cpu_reps)):
+            t1 = time.perf_counter()
+            cpu_call()
+            ts.append(time.perf_counter() - t1)
+        cpu_s = statistics.median(ts)
+        cpu = {"value": rows / cpu_s, "unit": "decode rows/s", "cores": torch.get_num_threads(), "kind": "port",
+               "sample": (f"{rows} of the {B} rows: the reference's pure-torch decode read "
+                          f"(xenc/d23_read_kernels.py:31-47) in fp32 on the CPU oracle, median of "
+                          f"{max(1, args.cpu_reps)} reps after 1 warm-up; {cpu_model()}")}
+    res = {
+        "metric": "Op B decode read (DecodeReader): decode rows/s and HBM GB/s (% peak)",
+        "value": B / (k_ms * 1e-3), "unit": "decode rows/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "fp32 (bf16 pools)", "data": "synthetic",
+        "config": {"workload": "op_b", "rows": B, "operator_rows": op_len, "own_rows": own_len, "hq": hq,
+                   "hkv": hkv, "head_dim": d, "block_size": bs, "key_splits": dec.S, "chunk": chunk},
+        "roofline": {"bound": "hbm", "kernel": "joint_read_kernel", "achieved": achieved,
+                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                     "algorithmic_bytes": alg_bytes, "avg_launch_ms": k_ms},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -542,6 +633,8 @@ def main():
         sys.exit(2)
     if args.workload == "prefill":
         return bench_prefill(args)
+    if args.workload == "op_b":
+        return bench_op_b(args)
     if args.workload == "multi_depth":
         return bench_multi_depth(args)
     if args.workload == "pool_build":

@@ -196,7 +196,8 @@ int xenc_build_pages(const void* rows, const long long* row_off, int C, int d, c
  * Row l of a pool is block bt[n, l / block_size], slot l % block_size.  Pools are
  * [num_blocks, block_size, hkv, d] with element strides (sb, ss, sh) and d contiguous; K and V
  * pools of one kind share shape and strides.  dtype: 0 = fp16, 1 = bf16 (q, pools); out fp32
- * [N, hq, d] with strides (s_on, s_oh).  d % 8 == 0, d <= 512, G * d <= 4096.  Rows with no keys
+ * [N, hq, d] with strides (s_on, s_oh).  d % 8 == 0, d <= 512, G * d <= 4096; a pool block
+ * (sb, block_size * ss) and hkv * sh stay below 2^31 elements (else XENC_EINVAL).  Rows with no keys
  * give 0.  The joined range is split into nsplit ranges of `chunk` keys (the last split also
  * takes any keys past nsplit * chunk).  The caller guarantees op_len[n] <= op_bt row width *
  * block size and that block ids lie in the pool (they are device data; nothing is read back).

@@ -12,7 +12,8 @@
 // online max / sum / accumulator per query head in the log2 domain.  A key row of D elements is
 // read by a group of D/8 lanes (16-byte loads; groups padded to a power of two), so a wave reads
 // 64/TPR keys per step; 4 keys per lane group are in flight (block-table lookups first, then the
-// K / V loads).  Lane groups merge by shuffles, the 4 waves through LDS, and wave 0 writes the
+// K / V loads) and enter the online softmax as one block; score sums run on DPP and the
+// permlane swaps.  Lane groups merge by shuffles, the 4 waves through LDS, and wave 0 writes the
 // split's partial.  The last split of (n, h) to arrive (release / acquire on a per-(n, h)
 // counter) merges the partials in split order, so results are deterministic, and re-arms the
 // counter: the workspace is zeroed once and stays valid across calls and graph replays.
@@ -55,10 +56,50 @@ struct JointArgs {
   const void* own_k; const void* own_v; long long own_sb, own_ss, own_sh; int own_bs;
   const int* own_bt; long long own_bts; const int* own_len;
   int hkv, d, tpr, nsplit, chunk;
+  int op_shift, own_shift;   // log2 of the block sizes when they are powers of two, else -1
   float scale_log2;
   float* out; long long s_on, s_oh;
   int* counters; float2* part_ml; float* part_acc;   // [N*Hkv], [N*Hkv][S][G], [N*Hkv][S][G][D]
 };
+
+// Sum over each aligned group of tpr lanes (tpr a power of two <= 64, uniform over the launch)
+// for all N values at once: each step of group_sum that the group width needs is one uniform
+// branch over the whole array.
+template <int N>
+__device__ __forceinline__ void group_sums_rt(float (&v)[N], int tpr) {
+  if (tpr >= 2) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_f<0xB1>(v[i]);
+  }
+  if (tpr >= 4) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_f<0x4E>(v[i]);
+  }
+  if (tpr >= 8) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_f<0x141>(v[i]);
+  }
+  if (tpr >= 16) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] += dpp_f<0x140>(v[i]);
+  }
+  if (tpr >= 32) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const unsigned u = __float_as_uint(v[i]);
+      const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+      v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  }
+  if (tpr >= 64) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      const unsigned u = __float_as_uint(v[i]);
+      const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+      v[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+  }
+}
 
 // Online-softmax merge of state (mo, lo, ao) into (m, l, a); all in the log2 domain.
 __device__ __forceinline__ void lse_merge(float& m, float& l, float (&a)[8], float mo, float lo,
@@ -72,25 +113,30 @@ __device__ __forceinline__ void lse_merge(float& m, float& l, float (&a)[8], flo
   m = mn;
 }
 
-template <typename T, int G>
+// TPR: the lanes per key row when fixed at compile time (16 for head dim 128, 32 for 256), so the
+// score sums are straight-line code; 0 takes it from the arguments.
+template <typename T, int G, int TPR>
 __global__ __launch_bounds__(kJointThreads) void joint_read_kernel(JointArgs A) {
   __shared__ float lds_acc[2][G][512];
   __shared__ float lds_ml[2][G][2];
   __shared__ bool is_last_s;
 
+  // Launch order (row, split, kv head): the kv heads of one key range run side by side, so a pool
+  // row's heads (adjacent in memory) are read together.
   const int S = A.nsplit;
-  const int s = blockIdx.x % S;
-  const int nh = blockIdx.x / S;
-  const int h = nh % A.hkv;
-  const int n = nh / A.hkv;
+  const int h = blockIdx.x % A.hkv;
+  const int s = (blockIdx.x / A.hkv) % S;
+  const int n = blockIdx.x / (A.hkv * S);
+  const int nh = n * A.hkv + h;
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
-  const int tpr = A.tpr;                 // lanes per key row (power of two, >= D/8)
+  const int tpr = TPR > 0 ? TPR : A.tpr;   // lanes per key row (power of two, >= D/8)
   const int lr = lane & (tpr - 1);
   const int grp = lane / tpr;
   const int groups = kWave / tpr;        // keys per wave step
   const int dim0 = lr * 8;
   const bool active = dim0 < A.d;
+  const int dimc = min(dim0, A.d - 8);   // padding lanes (q = 0) read a valid column
 
   // q of the G heads, pre-scaled into the log2 domain.
   float qf[G][8];
@@ -125,50 +171,108 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_kernel(JointArgs A) 
   const int* owbt = A.own_bt + n * A.own_bts;
 
   const int step = kJointWaves * groups;              // keys per workgroup step
-  for (int base = k0 + wv * groups + grp; base < k1; base += step * kKeysInFlight) {
+  const int stride = step * kKeysInFlight;
+  // Block and row of the kKeysInFlight keys base, base + step, ... (block 0 for keys past k1, which
+  // load nothing).  The next iteration's lookups are issued while this one's keys are in flight,
+  // so the table loads are off the critical path.
+  // Keys past k1 are clamped to k1 - 1 (a valid key of a non-empty split): every table and row
+  // load is in bounds and unconditional, and those keys are masked out of the softmax.
+  const bool pow2 = A.op_shift >= 0 && A.own_shift >= 0;   // uniform: block sizes 2^k take shifts
+  auto lookup = [&](int base, int (&blk)[kKeysInFlight], int (&row)[kKeysInFlight]) {
+#pragma unroll
+    for (int u = 0; u < kKeysInFlight; ++u) {
+      const int key = min(base + u * step, k1 - 1);
+      const bool ow = key >= lo;
+      const int kk = ow ? key - lo : key;
+      int bi;
+      if (pow2) {
+        const int sh = ow ? A.own_shift : A.op_shift;
+        bi = kk >> sh;
+        row[u] = kk & ((1 << sh) - 1);
+      } else {
+        const int bs = ow ? A.own_bs : A.op_bs;
+        bi = kk / bs;
+        row[u] = kk - bi * bs;
+      }
+      const int* tb = ow ? owbt : opbt;
+      blk[u] = tb[bi];
+    }
+  };
+  // Strides are below 2^31 (checked on the host): the block base is one 64-bit multiply-add and
+  // the offset inside the block 32-bit.
+  const unsigned op_sb = (unsigned)A.op_sb, op_ss = (unsigned)A.op_ss, own_sb = (unsigned)A.own_sb,
+                 own_ss = (unsigned)A.own_ss;
+  const unsigned op_h = (unsigned)(h * A.op_sh), own_h = (unsigned)(h * A.own_sh);
+  int blk[kKeysInFlight], brow[kKeysInFlight];
+  const int first = k0 + wv * groups + grp;
+  if (k0 < k1) lookup(first, blk, brow);   // workgroup-uniform: an empty split loads nothing
+  for (int base = first; base < k1; base += stride) {
     long long offk[kKeysInFlight];
     bool own[kKeysInFlight], live[kKeysInFlight];
 #pragma unroll
     for (int u = 0; u < kKeysInFlight; ++u) {
       const int key = base + u * step;
       live[u] = key < k1;
-      own[u] = key >= lo;
-      const int kk = live[u] ? (own[u] ? key - lo : key) : 0;
-      const int bs = own[u] ? A.own_bs : A.op_bs;
-      const int blk = live[u] ? (own[u] ? owbt[kk / bs] : opbt[kk / bs]) : 0;
-      offk[u] = own[u] ? blk * A.own_sb + (kk % bs) * A.own_ss + h * A.own_sh
-                       : blk * A.op_sb + (kk % bs) * A.op_ss + h * A.op_sh;
+      own[u] = min(key, k1 - 1) >= lo;
+      offk[u] = own[u] ? (unsigned long long)(unsigned)blk[u] * own_sb + (brow[u] * own_ss + own_h)
+                       : (unsigned long long)(unsigned)blk[u] * op_sb + (brow[u] * op_ss + op_h);
     }
     u32x4_t kv[kKeysInFlight], vv[kKeysInFlight];
 #pragma unroll
     for (int u = 0; u < kKeysInFlight; ++u) {
-      const bool ld = live[u] && active;
-      const T* kp = (own[u] ? owk : opk) + offk[u] + dim0;
-      const T* vp = (own[u] ? owv : opv) + offk[u] + dim0;
-      kv[u] = ld ? *reinterpret_cast<const u32x4_t*>(kp) : (u32x4_t){};
-      vv[u] = ld ? *reinterpret_cast<const u32x4_t*>(vp) : (u32x4_t){};
+      const T* kp = (own[u] ? owk : opk) + offk[u] + dimc;
+      const T* vp = (own[u] ? owv : opv) + offk[u] + dimc;
+      kv[u] = *reinterpret_cast<const u32x4_t*>(kp);
+      vv[u] = *reinterpret_cast<const u32x4_t*>(vp);
+    }
+    lookup(base + stride, blk, brow);
+    // Scores of the lane group's kKeysInFlight keys, then one online-softmax update per head for
+    // the block (one max update and one accumulator rescale), then the values.
+    float sc[kKeysInFlight][G];
+    float flat[kKeysInFlight * G];
+#pragma unroll
+    for (int u = 0; u < kKeysInFlight; ++u) {
+      float kf[8];
+      to_f32<T>(kv[u], kf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float x = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x = fmaf(qf[g][e], kf[e], x);
+        flat[u * G + g] = x;
+      }
+    }
+    group_sums_rt(flat, tpr);
+#pragma unroll
+    for (int u = 0; u < kKeysInFlight; ++u)
+#pragma unroll
+      for (int g = 0; g < G; ++g) sc[u][g] = flat[u * G + g];
+    float c[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float mn = m[g];
+#pragma unroll
+      for (int u = 0; u < kKeysInFlight; ++u) mn = live[u] ? fmaxf(mn, sc[u][g]) : mn;
+      c[g] = mn == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[g] - mn);   // 0 before the first key
+      float ls = l[g] * c[g];
+#pragma unroll
+      for (int u = 0; u < kKeysInFlight; ++u) {
+        sc[u][g] = live[u] ? __builtin_amdgcn_exp2f(sc[u][g] - mn) : 0.f;
+        ls += sc[u][g];
+      }
+      l[g] = ls;
+      m[g] = mn;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[g][e] *= c[g];
     }
 #pragma unroll
     for (int u = 0; u < kKeysInFlight; ++u) {
-      float kf[8], vf[8];
-      to_f32<T>(kv[u], kf);
+      float vf[8];
       to_f32<T>(vv[u], vf);
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float sc = 0.f;
+      for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) sc = fmaf(qf[g][e], kf[e], sc);
-        for (int o = 1; o < tpr; o <<= 1) sc += shfl_xor(sc, o);
-        if (live[u]) {
-          const float mn = fmaxf(m[g], sc);
-          const float c = __builtin_amdgcn_exp2f(m[g] - mn);   // exp2(-inf) = 0 on the first key
-          const float p = __builtin_amdgcn_exp2f(sc - mn);
-          l[g] = l[g] * c + p;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(p, vf[e], acc[g][e] * c);
-          m[g] = mn;
-        }
-      }
+        for (int e = 0; e < 8; ++e) acc[g][e] = fmaf(sc[u][g], vf[e], acc[g][e]);
     }
   }
 
@@ -280,17 +384,27 @@ JointLayout joint_layout(int max_n, int N, int hkv, int nsplit, int g, int d) {
   return L;
 }
 
+template <typename T, int G>
+void launch_joint_g(dim3 grid, hipStream_t st, const JointArgs& a) {
+  if (a.tpr == 32)
+    hipLaunchKernelGGL((joint_read_kernel<T, G, 32>), grid, dim3(kJointThreads), 0, st, a);
+  else if (a.tpr == 16)
+    hipLaunchKernelGGL((joint_read_kernel<T, G, 16>), grid, dim3(kJointThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL((joint_read_kernel<T, G, 0>), grid, dim3(kJointThreads), 0, st, a);
+}
+
 template <typename T>
 int launch_joint(int G, dim3 grid, hipStream_t st, const JointArgs& a) {
   switch (G) {
-    case 1: hipLaunchKernelGGL((joint_read_kernel<T, 1>), grid, dim3(kJointThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((joint_read_kernel<T, 2>), grid, dim3(kJointThreads), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((joint_read_kernel<T, 3>), grid, dim3(kJointThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((joint_read_kernel<T, 4>), grid, dim3(kJointThreads), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((joint_read_kernel<T, 5>), grid, dim3(kJointThreads), 0, st, a); break;
-    case 6: hipLaunchKernelGGL((joint_read_kernel<T, 6>), grid, dim3(kJointThreads), 0, st, a); break;
-    case 7: hipLaunchKernelGGL((joint_read_kernel<T, 7>), grid, dim3(kJointThreads), 0, st, a); break;
-    case 8: hipLaunchKernelGGL((joint_read_kernel<T, 8>), grid, dim3(kJointThreads), 0, st, a); break;
+    case 1: launch_joint_g<T, 1>(grid, st, a); break;
+    case 2: launch_joint_g<T, 2>(grid, st, a); break;
+    case 3: launch_joint_g<T, 3>(grid, st, a); break;
+    case 4: launch_joint_g<T, 4>(grid, st, a); break;
+    case 5: launch_joint_g<T, 5>(grid, st, a); break;
+    case 6: launch_joint_g<T, 6>(grid, st, a); break;
+    case 7: launch_joint_g<T, 7>(grid, st, a); break;
+    case 8: launch_joint_g<T, 8>(grid, st, a); break;
     default: return XENC_EINVAL;
   }
   return check_launch();
@@ -337,6 +451,10 @@ extern "C" int xenc_paged_decode_joint(
   if (s_qh < d || s_qn < (long long)hq * s_qh || s_oh < d || s_on < (long long)hq * s_oh) return XENC_EINVAL;
   for (long long st : {s_qn, s_qh, op_sb, op_ss, op_sh, own_sb, own_ss, own_sh})
     if (st % 8 != 0 || st < 0) return XENC_EALIGN;
+  // One pool block (and a kv head's offset inside it) stays below 2^31 elements.
+  for (long long st : {op_sb, own_sb, (long long)op_bs * op_ss, (long long)own_bs * own_ss,
+                       (long long)hkv * op_sh, (long long)hkv * own_sh})
+    if (st >= (1LL << 31)) return XENC_EINVAL;
   if (N == 0) return XENC_OK;
   if (!q || !op_k || !op_v || !op_bt || !op_len || !own_k || !own_v || !own_bt || !own_len ||
       !out || !workspace)
@@ -347,10 +465,16 @@ extern "C" int xenc_paged_decode_joint(
   if (workspace_bytes < lay.total) return XENC_EWORKSPACE;
   int tpr = 1;
   while (tpr * 8 < d) tpr <<= 1;
+  auto shift_of = [](int bs) {
+    if (bs & (bs - 1)) return -1;
+    int sh = 0;
+    while ((1 << sh) < bs) ++sh;
+    return sh;
+  };
   char* ws = static_cast<char*>(workspace);
   JointArgs a{q, s_qn, s_qh, op_k, op_v, op_sb, op_ss, op_sh, op_bs, op_bt, op_bt_stride, op_len,
               own_k, own_v, own_sb, own_ss, own_sh, own_bs, own_bt, own_bt_stride, own_len,
-              hkv, d, tpr, nsplit, chunk, scale * kLog2e, out, s_on, s_oh,
+              hkv, d, tpr, nsplit, chunk, shift_of(op_bs), shift_of(own_bs), scale * kLog2e, out, s_on, s_oh,
               reinterpret_cast<int*>(ws + lay.counters), reinterpret_cast<float2*>(ws + lay.ml),
               reinterpret_cast<float*>(ws + lay.acc)};
   const long long blocks = (long long)N * hkv * nsplit;
