@@ -66,10 +66,11 @@ def test_host_side_validation_rejects_bad_sizes():
     def joint(**kw):
         a = {**args, **kw}
         return L.xenc_paged_decode_joint(a["dtype"], a["N"], a["hq"], a["hkv"], a["d"], None, 16 * 64, 64,
-                                         None, None, 64 * 4 * 16, 64 * 4, 64, 16, None, 8, None,
+                                         None, None, a.get("op_sb", 64 * 4 * 16), 64 * 4, 64, 16, None, 8, None,
                                          None, None, 64 * 4 * 16, 64 * 4, 64, 16, None, 8, None,
                                          0.125, 2, 512, None, 16 * 64, 64, None, 0, a.get("max_n", 4), None)
     assert joint(hq=36, hkv=4) == -1
+    assert joint(op_sb=1 << 31) == -1        # a pool block of 2^31 elements or more
     assert joint(d=60) == -1
     assert joint(dtype=2) == -1
     assert joint() == -2
