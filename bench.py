@@ -558,8 +558,8 @@ def bench_op_b(args):
     own_l = torch.full((B,), own_len, dtype=torch.int32, device=dev)
     q = torch.randn(B, hq, d, generator=g, device=dev).to(dt)
     scale = d ** -0.5
-    chunk = 1024
-    dec = DecodeReader(B, hq, hkv, d, max_keys=op_len + own_len, device=dev, chunk=chunk)
+    dec = DecodeReader(B, hq, hkv, d, max_keys=op_len + own_len, device=dev)
+    chunk = dec.chunk
 
     def call():
         return dec(q, op_k, op_v, op_bt, op_l, own_k, own_v, own_bt, own_l, scale)

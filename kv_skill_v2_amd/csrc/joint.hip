@@ -27,6 +27,7 @@ namespace {
 constexpr int kJointThreads = 256;
 constexpr int kJointWaves = kJointThreads / kWave;
 constexpr int kKeysInFlight = 4;
+constexpr int kMergeStates = 1024;   // split states (S x G) the last split stages in LDS
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -111,6 +112,87 @@ __device__ __forceinline__ void lse_merge(float& m, float& l, float (&a)[8], flo
 #pragma unroll
   for (int e = 0; e < 8; ++e) a[e] = a[e] * c0 + ao[e] * c1;
   m = mn;
+}
+
+// After the split's partial is written: publish it (release, then a per-(row, kv head) arrival
+// count); the last split of (n, h) to arrive acquires and merges the S partials in split order,
+// writes the output rows and re-arms the counter.
+template <int G>
+__device__ __forceinline__ void publish_and_merge(const JointArgs& A, int nh, int S, int n, int h,
+                                                  bool& is_last_s) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int prev = __hip_atomic_fetch_add(&A.counters[nh], 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == S - 1;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    is_last_s = last;
+  }
+  __syncthreads();
+  if (!is_last_s) return;
+  const long long p0 = (long long)nh * S;
+  if (S * G <= kMergeStates) {
+    // Split states to LDS; per head the max M, then per (split, head) the factor 2^(m - M) (0 for
+    // an empty split) and the denominator in split order; then every output sums its S partial
+    // accumulators in split order, 8 loads in flight.
+    __shared__ float2 sml[kMergeStates];
+    __shared__ float coef[kMergeStates];
+    __shared__ float den[8];
+    for (int i = threadIdx.x; i < S * G; i += kJointThreads) sml[i] = A.part_ml[p0 * G + i];
+    __syncthreads();
+    if (threadIdx.x < G) {
+      const int g = threadIdx.x;
+      float M = -INFINITY;
+      for (int j = 0; j < S; ++j)
+        if (sml[j * G + g].y > 0.f) M = fmaxf(M, sml[j * G + g].x);
+      float dsum = 0.f;
+      for (int j = 0; j < S; ++j) {
+        const float2 ml = sml[j * G + g];
+        const float c = ml.y > 0.f ? __builtin_amdgcn_exp2f(ml.x - M) : 0.f;
+        coef[j * G + g] = c;
+        dsum += c * ml.y;
+      }
+      den[g] = dsum;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < G * A.d; i += kJointThreads) {
+      const int g = i / A.d, dd = i % A.d;
+      const float* src = A.part_acc + (p0 * G + g) * A.d + dd;   // split j at src[j * G * d]
+      const long long js = (long long)G * A.d;
+      float num = 0.f;
+      int j = 0;
+      for (; j + 8 <= S; j += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[(j + u) * js];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) num += coef[(j + u) * G + g] * v[u];
+      }
+      for (; j < S; ++j) num += coef[j * G + g] * src[j * js];
+      A.out[n * A.s_on + (long long)(h * G + g) * A.s_oh + dd] = den[g] > 0.f ? num / den[g] : 0.f;
+    }
+  } else {
+    for (int i = threadIdx.x; i < G * A.d; i += kJointThreads) {
+      const int g = i / A.d, dd = i % A.d;
+      float M = -INFINITY;
+      for (int j = 0; j < S; ++j) {
+        const float2 ml = A.part_ml[(p0 + j) * G + g];
+        if (ml.y > 0.f) M = fmaxf(M, ml.x);
+      }
+      float num = 0.f, dsum = 0.f;
+      for (int j = 0; j < S; ++j) {
+        const float2 ml = A.part_ml[(p0 + j) * G + g];
+        if (ml.y > 0.f) {
+          const float c = __builtin_amdgcn_exp2f(ml.x - M);
+          dsum += c * ml.y;
+          num += c * A.part_acc[((p0 + j) * G + g) * A.d + dd];
+        }
+      }
+      A.out[n * A.s_on + (long long)(h * G + g) * A.s_oh + dd] = dsum > 0.f ? num / dsum : 0.f;
+    }
+  }
+  if (threadIdx.x == 0) atomicExch(&A.counters[nh], 0);
 }
 
 // TPR: the lanes per key row when fixed at compile time (16 for head dim 128, 32 for 256), so the
@@ -327,38 +409,7 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_kernel(JointArgs A) 
       }
     }
   }
-  // Publish; the last split of (n, h) to arrive merges.
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const int prev = __hip_atomic_fetch_add(&A.counters[nh], 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    const bool last = prev == S - 1;
-    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    is_last_s = last;
-  }
-  __syncthreads();
-  if (!is_last_s) return;
-  const long long p0 = (long long)nh * S;
-  for (int i = threadIdx.x; i < G * A.d; i += kJointThreads) {
-    const int g = i / A.d, dd = i % A.d;
-    float M = -INFINITY;
-    for (int j = 0; j < S; ++j) {
-      const float2 ml = A.part_ml[(p0 + j) * G + g];
-      if (ml.y > 0.f) M = fmaxf(M, ml.x);
-    }
-    float num = 0.f, den = 0.f;
-    for (int j = 0; j < S; ++j) {
-      const float2 ml = A.part_ml[(p0 + j) * G + g];
-      if (ml.y > 0.f) {
-        const float c = __builtin_amdgcn_exp2f(ml.x - M);
-        den += c * ml.y;
-        num += c * A.part_acc[((p0 + j) * G + g) * A.d + dd];
-      }
-    }
-    A.out[n * A.s_on + (long long)(h * G + g) * A.s_oh + dd] = den > 0.f ? num / den : 0.f;
-  }
-  if (threadIdx.x == 0) atomicExch(&A.counters[nh], 0);
+  publish_and_merge<G>(A, nh, S, n, h, is_last_s);
 }
 
 __global__ void joint_zero_kernel(int* p, int n) {
@@ -384,9 +435,286 @@ JointLayout joint_layout(int max_n, int N, int hkv, int nsplit, int g, int d) {
   return L;
 }
 
+// MFMA form for head dims 128 and 256 (fp16 / bf16 pools, G <= 8).  Same split, launch order,
+// partial layout and merge as joint_read_kernel; inside a split, wave w takes the 16-key tiles
+// w, w + 4, ... of its range.
+//   Scores: one v_mfma_f32_16x16x32 per 32 dims, A = the tile's 16 key rows (lane l: key l % 16,
+//   dims 8 (l / 16) .. +8 of each 32-dim block), B = q^T (lane l: query head l % 16 of the kv
+//   head, zero past G), so lane l receives the scores of keys 4 (l / 16) + i, head l % 16.
+//   Softmax: per head in the log2 domain over the tile (max and sum across the four lanes of a
+//   head by the permlane swaps), one accumulator rescale per tile.
+//   Values: lane l owns dims l * D/64 .. +D/64 of every head; the tile's weights and V row
+//   addresses pass through this wave's LDS slot, and each key is D/64 FMAs per head.
+// Keys past the split end are clamped to its last key (all loads in bounds) and get weight 0.
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ __forceinline__ f32x4_t mfma16x16x32(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
+  if constexpr (__is_same(T, __bf16))
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  else
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+template <typename T>
+__device__ __forceinline__ float half_to_f32(unsigned bits16) {
+  if constexpr (__is_same(T, __bf16))
+    return __uint_as_float(bits16 << 16);
+  else
+    return (float)__builtin_bit_cast(_Float16, (unsigned short)bits16);
+}
+
+constexpr int kTileKeys = 16;
+
+template <typename T, int G, int D>
+__global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArgs A) {
+  constexpr int KB = D / 32;    // 32-dim blocks of a key row
+  constexpr int DPL = D / 64;   // value dims per lane
+  static_assert(D == 128 || D == 256, "the MFMA form covers head dims 128 and 256");
+  __shared__ float lds_acc[2][G][D];
+  __shared__ float lds_ml[2][G][2];
+  __shared__ __align__(16) float lds_p[kJointWaves][kTileKeys][8];   // tile weights [key][head]
+  __shared__ const T* lds_v[kJointWaves][kTileKeys];                 // tile V rows
+  __shared__ float lds_c[kJointWaves][8];                            // tile rescale per head
+  __shared__ bool is_last_s;
+
+  const int S = A.nsplit;
+  const int h = blockIdx.x % A.hkv;
+  const int s = (blockIdx.x / A.hkv) % S;
+  const int n = blockIdx.x / (A.hkv * S);
+  const int nh = n * A.hkv + h;
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int l16 = lane & 15, lq = lane >> 4;
+
+  // q^T fragments of the G heads (raw 16-bit values; heads past G are zero).
+  u32x4_t qf[KB];
+  {
+    const T* qrow = static_cast<const T*>(A.q) + n * A.s_qn + (long long)(h * G + min(l16, G - 1)) * A.s_qh;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const u32x4_t v = *reinterpret_cast<const u32x4_t*>(qrow + kb * 32 + 8 * lq);
+      qf[kb] = l16 < G ? v : (u32x4_t){};
+    }
+  }
+  const int lo = A.op_len[n];
+  const int L = lo + A.own_len[n];
+  const int k0 = s * A.chunk;
+  const int k1 = s == S - 1 ? L : min(L, k0 + A.chunk);
+
+  const T* opk = static_cast<const T*>(A.op_k);
+  const T* opv = static_cast<const T*>(A.op_v);
+  const T* owk = static_cast<const T*>(A.own_k);
+  const T* owv = static_cast<const T*>(A.own_v);
+  const int* opbt = A.op_bt + n * A.op_bts;
+  const int* owbt = A.own_bt + n * A.own_bts;
+  const bool pow2 = A.op_shift >= 0 && A.own_shift >= 0;
+  const unsigned op_sb = (unsigned)A.op_sb, op_ss = (unsigned)A.op_ss, own_sb = (unsigned)A.own_sb,
+                 own_ss = (unsigned)A.own_ss;
+  const unsigned op_h = (unsigned)(h * A.op_sh), own_h = (unsigned)(h * A.own_sh);
+
+  float m = -INFINITY, l = 0.f;   // softmax state of head l16 (the same in its four lanes)
+  float acc[G][DPL];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) acc[g][j] = 0.f;
+
+  // Row offset of key tb + l16 (clamped to k1 - 1), pool chosen by the key.
+  auto locate = [&](int tb, unsigned long long& off, bool& ow) {
+    const int key = min(tb + l16, k1 - 1);
+    ow = key >= lo;
+    const int kk = ow ? key - lo : key;
+    int bi, row;
+    if (pow2) {
+      const int sh = ow ? A.own_shift : A.op_shift;
+      bi = kk >> sh;
+      row = kk & ((1 << sh) - 1);
+    } else {
+      const int bs = ow ? A.own_bs : A.op_bs;
+      bi = kk / bs;
+      row = kk - bi * bs;
+    }
+    const int blk = (ow ? owbt : opbt)[bi];
+    off = ow ? (unsigned long long)(unsigned)blk * own_sb + (row * own_ss + own_h)
+             : (unsigned long long)(unsigned)blk * op_sb + (row * op_ss + op_h);
+  };
+
+  constexpr int kWaveStride = kTileKeys * kJointWaves;
+  // Issue the K fragments and V slices of the tile whose row offset this lane holds (key
+  // tb + l16): the V row addresses go through this wave's LDS slot to every lane.
+  auto issue = [&](unsigned long long off, bool ow, u32x4_t (&kf)[KB], unsigned (&vraw)[kTileKeys][DPL / 2]) {
+    const T* kp = (ow ? owk : opk) + off;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) kf[kb] = *reinterpret_cast<const u32x4_t*>(kp + kb * 32 + 8 * lq);
+    if (lq == 0) lds_v[wv][l16] = (ow ? owv : opv) + off;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int k = 0; k < kTileKeys; ++k) {
+      const T* vr = lds_v[wv][k] + lane * DPL;
+      if constexpr (DPL == 4) {
+        const uint2 v2 = *reinterpret_cast<const uint2*>(vr);
+        vraw[k][0] = v2.x;
+        vraw[k][1] = v2.y;
+      } else {
+        vraw[k][0] = *reinterpret_cast<const unsigned*>(vr);
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();   // the slot is rewritten by the next issue
+  };
+  // Scores, softmax and values of tile tb from its loaded fragments.
+  auto consume = [&](int tb, const u32x4_t (&kf)[KB], const unsigned (&vraw)[kTileKeys][DPL / 2]) {
+    f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) sacc = mfma16x16x32<T>(kf[kb], qf[kb], sacc);
+    float sv[4];
+    bool ok[4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      ok[i] = tb + 4 * lq + i < k1;
+      sv[i] = sacc[i] * A.scale_log2;
+      mt = ok[i] ? fmaxf(mt, sv[i]) : mt;
+    }
+    mt = fmaxf(mt, swap_partner<16>(mt, (lane & 16) != 0));
+    mt = fmaxf(mt, swap_partner<32>(mt, (lane & 32) != 0));
+    const float mn = fmaxf(m, mt);   // key tb < k1 is in every tile: mt is finite
+    const float c = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      sv[i] = ok[i] ? __builtin_amdgcn_exp2f(sv[i] - mn) : 0.f;
+      ps += sv[i];
+    }
+    ps += swap_partner<16>(ps, (lane & 16) != 0);
+    ps += swap_partner<32>(ps, (lane & 32) != 0);
+    l = l * c + ps;
+    m = mn;
+    if (l16 < G) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) lds_p[wv][4 * lq + i][l16] = sv[i];
+      if (lq == 0) lds_c[wv][l16] = c;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float cg = lds_c[wv][g];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[g][j] *= cg;
+    }
+#pragma unroll
+    for (int k = 0; k < kTileKeys; ++k) {
+      float pk[8];
+      const float4 p0 = *reinterpret_cast<const float4*>(&lds_p[wv][k][0]);
+      pk[0] = p0.x; pk[1] = p0.y; pk[2] = p0.z; pk[3] = p0.w;
+      if constexpr (G > 4) {
+        const float4 p1 = *reinterpret_cast<const float4*>(&lds_p[wv][k][4]);
+        pk[4] = p1.x; pk[5] = p1.y; pk[6] = p1.z; pk[7] = p1.w;
+      }
+      float vf[DPL];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) vf[j] = half_to_f32<T>(j & 1 ? vraw[k][j / 2] >> 16 : vraw[k][j / 2] & 0xffffu);
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[g][j] = fmaf(pk[g], vf[j], acc[g][j]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();   // the weight slot is rewritten by the next tile
+  };
+
+  // Two tiles in flight per wave: tile t + stride is issued, and the table lookup of t + 2 stride
+  // started, before tile t is consumed (buffers A / B alternate; clamped keys keep every lookup
+  // in bounds and a wave with no tile issues nothing).
+  u32x4_t kfa[KB], kfb[KB];
+  unsigned vra[kTileKeys][DPL / 2], vrb[kTileKeys][DPL / 2];
+  unsigned long long offa = 0, offb = 0;
+  bool owa = false, owb = false;
+  const int t0 = k0 + kTileKeys * wv;
+  if (t0 < k1) {
+    locate(t0, offa, owa);
+    issue(offa, owa, kfa, vra);
+    if (t0 + kWaveStride < k1) locate(t0 + kWaveStride, offb, owb);
+  }
+  for (int tb = t0; tb < k1; tb += 2 * kWaveStride) {   // wave-uniform
+    const int t1 = tb + kWaveStride, t2 = tb + 2 * kWaveStride, t3 = tb + 3 * kWaveStride;
+    if (t1 < k1) {
+      issue(offb, owb, kfb, vrb);
+      if (t2 < k1) locate(t2, offa, owa);
+    }
+    consume(tb, kfa, vra);
+    if (t1 < k1) {
+      if (t2 < k1) {
+        issue(offa, owa, kfa, vra);
+        if (t3 < k1) locate(t3, offb, owb);
+      }
+      consume(t1, kfb, vrb);
+    }
+  }
+
+  // Per-head state as wave-uniform values (lane g holds head g).
+  float Mg[G], Lg[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    Mg[g] = readlane(m, g);
+    Lg[g] = readlane(l, g);
+  }
+  // Waves 2,3 -> 0,1, then 1 -> 0, through LDS.
+  for (int half = kJointWaves / 2; half >= 1; half >>= 1) {
+    if (wv >= half && wv < 2 * half) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) lds_acc[wv - half][g][lane * DPL + j] = acc[g][j];
+        if (lane == 0) {
+          lds_ml[wv - half][g][0] = Mg[g];
+          lds_ml[wv - half][g][1] = Lg[g];
+        }
+      }
+    }
+    __syncthreads();
+    if (wv < half) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float m2 = lds_ml[wv][g][0], l2 = lds_ml[wv][g][1];
+        const float M = fmaxf(Mg[g], m2);
+        const float a = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(Mg[g] - M);
+        const float b = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) acc[g][j] = acc[g][j] * a + lds_acc[wv][g][lane * DPL + j] * b;
+        Lg[g] = Lg[g] * a + l2 * b;
+        Mg[g] = M;
+      }
+    }
+    __syncthreads();
+  }
+  const long long part = (long long)nh * S + s;
+  if (wv == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (lane == 0) A.part_ml[part * G + g] = make_float2(Mg[g], Lg[g]);
+      float* dst = A.part_acc + (part * G + g) * A.d + lane * DPL;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) dst[j] = acc[g][j];
+    }
+  }
+  publish_and_merge<G>(A, nh, S, n, h, is_last_s);
+}
+
 template <typename T, int G>
 void launch_joint_g(dim3 grid, hipStream_t st, const JointArgs& a) {
-  if (a.tpr == 32)
+  if (a.d == 256)
+    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 256>), grid, dim3(kJointThreads), 0, st, a);
+  else if (a.d == 128)
+    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 128>), grid, dim3(kJointThreads), 0, st, a);
+  else if (a.tpr == 32)
     hipLaunchKernelGGL((joint_read_kernel<T, G, 32>), grid, dim3(kJointThreads), 0, st, a);
   else if (a.tpr == 16)
     hipLaunchKernelGGL((joint_read_kernel<T, G, 16>), grid, dim3(kJointThreads), 0, st, a);

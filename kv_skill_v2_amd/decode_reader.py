@@ -2,7 +2,7 @@
 
 Same constructor and call signature as xenc/d23_read_kernels.py:134-160:
 
-    dec = DecodeReader(max_n, hq, hkv, d, max_keys, device, chunk=1024, block_n=64)
+    dec = DecodeReader(max_n, hq, hkv, d, max_keys, device, chunk=None, block_n=64)
     out = dec(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale)   # fp32 [N, hq, d]
 
 For each query row n and query head, one softmax over the operator's rows (paged pool op_k/op_v,
@@ -13,7 +13,10 @@ Like the reference, the reader owns a static workspace sized at construction and
 of its own output buffer (callers clone it if they keep it across calls).  A call allocates
 nothing, reads no device value on the host and synchronises nothing, so it can be captured in a
 HIP graph and replayed with new lengths / block tables.  `block_n` is accepted for signature
-compatibility (it sized the reference's key tile); the HIP kernel picks its own tiling.
+compatibility (it sized the reference's key tile); the HIP kernel picks its own tiling.  `chunk`
+(keys per split) keeps the reference's meaning; left at None it is chosen from max_n, hkv and
+max_keys for about 1024 workgroups at full capacity (the reference's default is 1024).  The split
+only changes the order of the LSE merge, not what is computed.
 """
 
 from __future__ import annotations
@@ -28,13 +31,19 @@ _DTYPES = {torch.float16: 0, torch.bfloat16: 1}
 
 
 class DecodeReader:
-    def __init__(self, max_n: int, hq: int, hkv: int, d: int, max_keys: int, device, chunk: int = 1024,
+    def __init__(self, max_n: int, hq: int, hkv: int, d: int, max_keys: int, device, chunk: int | None = None,
                  block_n: int = 64):
         if hq % hkv:
             raise ValueError(f"hq={hq} must be a multiple of hkv={hkv}")
         self.G, self.hq, self.hkv, self.d = hq // hkv, int(hq), int(hkv), int(d)
         if not 1 <= self.G <= 8 or d % 8 or d > 512 or self.G * d > 4096:
             raise ValueError(f"unsupported head layout: G={self.G} (1..8), d={d} (multiple of 8, <= 512)")
+        if chunk is None:
+            # Keys per split: about 1024 workgroups at full capacity (32 rows x 16k keys, hkv 4:
+            # 2,112 keys, 0.43 ms against 0.49 ms at 1,024), at least 256 keys, a multiple of 64.
+            want = max(1, -(-1024 // max(1, int(max_n) * self.hkv)))
+            chunk = max(256, -(-int(max_keys) // want))
+            chunk = -(-chunk // 64) * 64
         self.max_n, self.chunk, self.block_n = int(max_n), int(chunk), int(block_n)
         self.S = max(1, math.ceil(max_keys / self.chunk))
         device = torch.device(device)

@@ -79,7 +79,8 @@ def test_decode_reader_matches_reference_and_replays(dev, N, nb_op, seed):
 
 @pytest.mark.parametrize("hq,hkv,d,dtype", [(16, 16, 128, torch.float16), (8, 4, 64, torch.bfloat16),
                                             (32, 4, 128, torch.bfloat16), (12, 4, 80, torch.float16),
-                                            (8, 1, 512, torch.float16)])
+                                            (8, 1, 512, torch.float16), (16, 8, 256, torch.float16),
+                                            (16, 2, 256, torch.bfloat16), (6, 2, 128, torch.bfloat16)])
 def test_decode_reader_layouts(dev, hq, hkv, d, dtype):
     say("op B layout", dict(hq=hq, hkv=hkv, d=d, dtype=str(dtype)))
     args = _case(5, hq, hkv, d, 8, 64, 24, 7, dtype, op_blocks=40, own_blocks=10,
