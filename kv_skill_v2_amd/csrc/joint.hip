@@ -478,7 +478,7 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
   __shared__ float lds_acc[2][G][D];
   __shared__ float lds_ml[2][G][2];
   __shared__ __align__(16) float lds_p[kJointWaves][kTileKeys][8];   // tile weights [key][head]
-  __shared__ const T* lds_v[kJointWaves][kTileKeys];                 // tile V rows
+  __shared__ long long lds_v[kJointWaves][kTileKeys];   // tile V rows, elements from the operator V pool
   __shared__ float lds_c[kJointWaves][8];                            // tile rescale per head
   __shared__ bool is_last_s;
 
@@ -516,6 +516,11 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
   const unsigned op_sb = (unsigned)A.op_sb, op_ss = (unsigned)A.op_ss, own_sb = (unsigned)A.own_sb,
                  own_ss = (unsigned)A.own_ss;
   const unsigned op_h = (unsigned)(h * A.op_sh), own_h = (unsigned)(h * A.own_sh);
+  // V rows are passed between lanes as element offsets from the operator V pool (the own pool at
+  // own_delta), so their loads index a kernel-argument pointer: global loads, not flat ones, whose
+  // completion would also hold up every LDS wait behind them.
+  const long long own_delta =
+      ((long long)(uintptr_t)owv - (long long)(uintptr_t)opv) / (long long)sizeof(T);   // pools 16-byte aligned
 
   float m = -INFINITY, l = 0.f;   // softmax state of head l16 (the same in its four lanes)
   float acc[G][DPL];
@@ -524,12 +529,14 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
 #pragma unroll
     for (int j = 0; j < DPL; ++j) acc[g][j] = 0.f;
 
-  // Row offset of key tb + l16 (clamped to k1 - 1), pool chosen by the key.
-  auto locate = [&](int tb, unsigned long long& off, bool& ow) {
+  // Block and row of key tb + l16 (clamped to k1 - 1), pool chosen by the key.  Only the table
+  // load is issued here; the row offset is formed when the tile is issued, so no wait for it
+  // holds up the loads already in flight.
+  auto locate = [&](int tb, int& blk, int& row, bool& ow) {
     const int key = min(tb + l16, k1 - 1);
     ow = key >= lo;
     const int kk = ow ? key - lo : key;
-    int bi, row;
+    int bi;
     if (pow2) {
       const int sh = ow ? A.own_shift : A.op_shift;
       bi = kk >> sh;
@@ -539,24 +546,24 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
       bi = kk / bs;
       row = kk - bi * bs;
     }
-    const int blk = (ow ? owbt : opbt)[bi];
-    off = ow ? (unsigned long long)(unsigned)blk * own_sb + (row * own_ss + own_h)
-             : (unsigned long long)(unsigned)blk * op_sb + (row * op_ss + op_h);
+    blk = (ow ? owbt : opbt)[bi];
   };
 
   constexpr int kWaveStride = kTileKeys * kJointWaves;
   // Issue the K fragments and V slices of the tile whose row offset this lane holds (key
   // tb + l16): the V row addresses go through this wave's LDS slot to every lane.
-  auto issue = [&](unsigned long long off, bool ow, u32x4_t (&kf)[KB], unsigned (&vraw)[kTileKeys][DPL / 2]) {
+  auto issue = [&](int blk, int row, bool ow, u32x4_t (&kf)[KB], unsigned (&vraw)[kTileKeys][DPL / 2]) {
+    const unsigned long long off = ow ? (unsigned long long)(unsigned)blk * own_sb + (row * own_ss + own_h)
+                                      : (unsigned long long)(unsigned)blk * op_sb + (row * op_ss + op_h);
     const T* kp = (ow ? owk : opk) + off;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) kf[kb] = *reinterpret_cast<const u32x4_t*>(kp + kb * 32 + 8 * lq);
-    if (lq == 0) lds_v[wv][l16] = (ow ? owv : opv) + off;
+    if (lq == 0) lds_v[wv][l16] = ow ? own_delta + (long long)off : (long long)off;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int k = 0; k < kTileKeys; ++k) {
-      const T* vr = lds_v[wv][k] + lane * DPL;
+      const T* vr = opv + lds_v[wv][k] + lane * DPL;
       if constexpr (DPL == 4) {
         const uint2 v2 = *reinterpret_cast<const uint2*>(vr);
         vraw[k][0] = v2.x;
@@ -630,32 +637,28 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
     __builtin_amdgcn_wave_barrier();   // the weight slot is rewritten by the next tile
   };
 
-  // Two tiles in flight per wave: tile t + stride is issued, and the table lookup of t + 2 stride
-  // started, before tile t is consumed (buffers A / B alternate; clamped keys keep every lookup
-  // in bounds and a wave with no tile issues nothing).
+  // Steady state per tile t: the table lookup of t + 2 strides, the K / V loads of t + 1, then t is
+  // consumed.  Every lookup and load is issued unconditionally (keys past the split clamp to its
+  // last key, so the extra loads re-read rows already in cache); only the consumes stop at the
+  // wave's last tile.  Loads complete in order, so each wait covers just the tile it needs.
   u32x4_t kfa[KB], kfb[KB];
   unsigned vra[kTileKeys][DPL / 2], vrb[kTileKeys][DPL / 2];
-  unsigned long long offa = 0, offb = 0;
-  bool owa = false, owb = false;
+  int blka, blkb, rowa, rowb;
+  bool owa, owb;
   const int t0 = k0 + kTileKeys * wv;
-  if (t0 < k1) {
-    locate(t0, offa, owa);
-    issue(offa, owa, kfa, vra);
-    if (t0 + kWaveStride < k1) locate(t0 + kWaveStride, offb, owb);
-  }
-  for (int tb = t0; tb < k1; tb += 2 * kWaveStride) {   // wave-uniform
-    const int t1 = tb + kWaveStride, t2 = tb + 2 * kWaveStride, t3 = tb + 3 * kWaveStride;
-    if (t1 < k1) {
-      issue(offb, owb, kfb, vrb);
-      if (t2 < k1) locate(t2, offa, owa);
-    }
-    consume(tb, kfa, vra);
-    if (t1 < k1) {
-      if (t2 < k1) {
-        issue(offa, owa, kfa, vra);
-        if (t3 < k1) locate(t3, offb, owb);
-      }
-      consume(t1, kfb, vrb);
+  if (t0 < k1) {   // wave-uniform
+    locate(t0, blka, rowa, owa);
+    locate(t0 + kWaveStride, blkb, rowb, owb);
+    issue(blka, rowa, owa, kfa, vra);
+    for (int tb = t0;; tb += 2 * kWaveStride) {
+      locate(tb + 2 * kWaveStride, blka, rowa, owa);
+      issue(blkb, rowb, owb, kfb, vrb);
+      consume(tb, kfa, vra);
+      if (tb + kWaveStride >= k1) break;
+      locate(tb + 3 * kWaveStride, blkb, rowb, owb);
+      issue(blka, rowa, owa, kfa, vra);
+      consume(tb + kWaveStride, kfb, vrb);
+      if (tb + 2 * kWaveStride >= k1) break;
     }
   }
 
