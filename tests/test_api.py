@@ -329,3 +329,16 @@ def test_param_groups():
     assert groups[-1]["name"] == "selector" and groups[-1]["lr"] == 5e-3
     ga = interface_param_groups(itf, 1e-3, lr_A=1e-2)
     assert [g["name"] for g in ga] == ["interface", "interface_A"] and ga[1]["lr"] == 1e-2
+
+
+def test_decode_reader_auto_chunk():
+    """DecodeReader's split size (host logic): about 1024 workgroups at capacity, >= 256 keys,
+    a multiple of 64, and splits that cover max_keys."""
+    import math
+    from kv_skill_v2_amd.decode_reader import DecodeReader
+    assert DecodeReader.auto_chunk(32, 4, 16448) == 2112
+    for max_n, hkv, mk in [(32, 4, 16448), (1, 4, 16448), (8, 4, 2048), (4, 16, 512), (256, 8, 100000), (1, 1, 1)]:
+        c = DecodeReader.auto_chunk(max_n, hkv, mk)
+        S = math.ceil(mk / c)
+        assert c >= 256 and c % 64 == 0 and S * c >= mk
+        assert max_n * hkv * S <= max(1024, max_n * hkv), (max_n, hkv, mk, c)
