@@ -478,7 +478,7 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
   __shared__ float lds_acc[2][G][D];
   __shared__ float lds_ml[2][G][2];
   __shared__ __align__(16) float lds_p[kJointWaves][kTileKeys][8];   // tile weights [key][head]
-  __shared__ long long lds_v[kJointWaves][kTileKeys];   // tile V rows, elements from the operator V pool
+  __shared__ long long lds_v[kJointWaves][kTileKeys];   // tile V rows: offset, own pool as ~offset
   __shared__ float lds_c[kJointWaves][8];                            // tile rescale per head
   __shared__ bool is_last_s;
 
@@ -516,11 +516,9 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
   const unsigned op_sb = (unsigned)A.op_sb, op_ss = (unsigned)A.op_ss, own_sb = (unsigned)A.own_sb,
                  own_ss = (unsigned)A.own_ss;
   const unsigned op_h = (unsigned)(h * A.op_sh), own_h = (unsigned)(h * A.own_sh);
-  // V rows are passed between lanes as element offsets from the operator V pool (the own pool at
-  // own_delta), so their loads index a kernel-argument pointer: global loads, not flat ones, whose
-  // completion would also hold up every LDS wait behind them.
-  const long long own_delta =
-      ((long long)(uintptr_t)owv - (long long)(uintptr_t)opv) / (long long)sizeof(T);   // pools 16-byte aligned
+  // V rows are passed between lanes as element offsets (the own pool's as ~offset) and loaded
+  // through the kernel-argument pool pointers: global loads, not flat ones, whose completion would
+  // also hold up every LDS wait behind them.
 
   float m = -INFINITY, l = 0.f;   // softmax state of head l16 (the same in its four lanes)
   float acc[G][DPL];
@@ -558,12 +556,13 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
     const T* kp = (ow ? owk : opk) + off;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb) kf[kb] = *reinterpret_cast<const u32x4_t*>(kp + kb * 32 + 8 * lq);
-    if (lq == 0) lds_v[wv][l16] = ow ? own_delta + (long long)off : (long long)off;
+    if (lq == 0) lds_v[wv][l16] = ow ? ~(long long)off : (long long)off;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
     for (int k = 0; k < kTileKeys; ++k) {
-      const T* vr = opv + lds_v[wv][k] + lane * DPL;
+      const long long vo = lds_v[wv][k];
+      const T* vr = (vo < 0 ? owv + ~vo : opv + vo) + lane * DPL;
       if constexpr (DPL == 4) {
         const uint2 v2 = *reinterpret_cast<const uint2*>(vr);
         vraw[k][0] = v2.x;
