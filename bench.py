@@ -35,6 +35,7 @@ def parse():
                     choices=["batched_paged_decode", "single_decode", "prefill", "multi_depth",
                              "pool_build", "d18", "op_b"])
     ap.add_argument("--nsplit", type=int, default=None)
+    ap.add_argument("--rows", type=int, default=32, help="op_b: decode rows (requests) per call")
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-graph", action="store_true", help="time the eager step only (no HIP graph replay)")
@@ -534,7 +535,8 @@ def bench_d18(args):
 def bench_op_b(args):
     """Op B, the vLLM plugin's decode read (DecodeReader, xenc/d23_read_kernels.py:134-160), at the
     serving shape of the reference's batch benchmark (xenc's scripts/bench_d23_vllm.py: Qwen3.5-9B
-    reader, batches up to 32, documents of 16k tokens): 32 decode rows, each over its own
+    reader, batches up to 32, documents of 16k tokens): 32 decode rows (--rows; 1 is the
+    reference's batch-1 latency case), each over its own
     16,384-row document operator joined with 64 own rows; hq 16, hkv 4, head dim 256, bf16 pools of
     16-row blocks, block tables a seeded shuffle of the pools.  One step = one DecodeReader call (a
     single xenc_paged_decode_joint launch).  Algorithmic bytes: every routed K and V row once
@@ -542,7 +544,7 @@ def bench_op_b(args):
     from kv_skill_v2_amd.decode_reader import DecodeReader
 
     dev = torch.device("cuda:0")
-    B, hq, hkv, d, bs, op_len, own_len = 32, 16, 4, 256, 16, 16384, 64
+    B, hq, hkv, d, bs, op_len, own_len = max(1, args.rows), 16, 4, 256, 16, 16384, 64
     dt = torch.bfloat16
     g = torch.Generator(device=dev)
     g.manual_seed(23)

@@ -56,10 +56,11 @@ class DecodeReader:
     @staticmethod
     def auto_chunk(max_n: int, hkv: int, max_keys: int) -> int:
         """Keys per split for about 1024 workgroups at full capacity (max_n rows x hkv heads x
-        splits), at least 256 keys, a multiple of 64 (the MFMA read's 16-key tiles over 4 waves).
-        32 rows x 16,448 keys at hkv 4 gives 2,112 keys (0.41 ms against 0.49 ms at 1,024)."""
+        splits), at least 512 keys, a multiple of 64 (the MFMA read's 16-key tiles over 4 waves).
+        At hkv 4 and 16,448 keys: 32 rows get 2,112 keys (0.41 ms against 0.49 ms at 1,024) and
+        one row 512 (37 us against 43 us at 256 and 48 us at 1,024)."""
         want = max(1, -(-1024 // max(1, int(max_n) * int(hkv))))
-        chunk = max(256, -(-int(max_keys) // want))
+        chunk = max(512, -(-int(max_keys) // want))
         return -(-chunk // 64) * 64
 
     @staticmethod
