@@ -230,7 +230,7 @@ __device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
     for (int w = 0; w < kD18PartWaves; ++w) a += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
     acc_out[i] = a;
   }
-  if (threadIdx.x < G) {
+  if ((int)threadIdx.x < G) {
     const int g = threadIdx.x;
     float M = -INFINITY, Mc = -INFINITY;
 #pragma unroll
