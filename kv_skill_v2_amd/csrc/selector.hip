@@ -170,7 +170,7 @@ __global__ __launch_bounds__(kRowThreads) void selector_apply_kernel(
 
 // One workgroup per query row m.
 __global__ __launch_bounds__(kRowThreads) void gate_scale_kernel(
-    int M, int d, const float* __restrict__ hn, long long ldh, const int* __restrict__ row_token,
+    [[maybe_unused]] int M, int d, const float* __restrict__ hn, long long ldh, const int* __restrict__ row_token,
     const int* __restrict__ row_pos, int n_pos, const float* __restrict__ gate_w,
     const float* __restrict__ gate_b, const float* __restrict__ log_gain, float gain_scale,
     float* __restrict__ scale, int vec4) {

@@ -19,7 +19,7 @@ namespace {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 __global__ __launch_bounds__(256) void decode_step_kernel(
-    int N, const int* __restrict__ row_slot, int* __restrict__ slots, int n_slots, int own_blocks,
+    [[maybe_unused]] int N, const int* __restrict__ row_slot, int* __restrict__ slots, int n_slots, int own_blocks,
     int block_size, int max_op_blocks, int dummy_block, int* __restrict__ op_bt, long long ld_op,
     int* __restrict__ op_len, int* __restrict__ own_bt, long long ld_own, int* __restrict__ own_len,
     long long* __restrict__ write_pos) {
