@@ -233,6 +233,7 @@ def bench_multi_depth(args):
     depth (union over the batch) x valid slots x d x 2, the S of the 8 Libraries, every B read,
     and the activations."""
     from kv_skill_v2_amd import ops, synth
+    from kv_skill_v2_amd.multi_depth import MultiDepthDecode
     from kv_skill_v2_amd.selector import LayerSelector, rms_norm
 
     c = synth.MULTI_DEPTH
@@ -247,25 +248,11 @@ def bench_multi_depth(args):
     gate_w = torch.zeros(dr, device=dev)
     gate_b = torch.full((L,), -2.0, device=dev)
     log_gain = torch.zeros(L, device=dev)
-    bidx = torch.arange(B, device=dev).repeat_interleave(c["k_sel"])
     hn = rms_norm(h)
-
-    bidx32 = bidx.to(torch.int32)
+    md = MultiDepthDecode(lib, Bw, gate_w, gate_b, log_gain, sel.log_alpha, k_sel=c["k_sel"], top_k=k)
 
     def step():
-        with torch.no_grad():
-            # selector top-2 + softmax (xenc_selector_weights): rows (b, j) in rank order
-            _, top, wtop = ops.selector_weights(z, c["k_sel"])
-            qg = top.reshape(-1)                                      # depth of each (token, j) row
-            qr = q_all[qg.long(), bidx]                               # [64, d]
-            _, idx, wsel = ops.route_topk(qr, lib, qg, top_k=k)
-            r = ops.library_read_decode(qr, lib, idx, wsel, qg)
-            # gate * gain per row (xenc_gate_scale), B of the row's depth (xenc_write_back)
-            scale = ops.gate_scale(hn, gate_w, gate_b, log_gain, 1.0, bidx32, qg)
-            dl = ops.write_back(r, Bw, qg, None, scale)               # [64, d_r]
-            # matched-norm rescale, selector weight and the sum over a token's two depths
-            out = ops.selector_apply(dl, h, wtop.reshape(-1), sel.log_alpha, k=c["k_sel"])
-            return out, idx, qg
+        return md(z, q_all, h, hn)
 
     _, idx0, qg0 = step()
     torch.cuda.synchronize()

@@ -27,42 +27,37 @@ __global__ __launch_bounds__(256) void selector_weights_kernel(
   const int b = blockIdx.x * 4 + threadIdx.x / kWave;
   if (b >= B) return;  // wave-uniform
   const float* zr = z + (long long)b * ldz;
+  // Candidate c carries the 64-bit key (order_key(z_c) << 32) | ~c: a larger key is a larger
+  // logit (NaN above +inf, as topk ranks it) or the same logit at a lower index.  Every real
+  // candidate's key is nonzero, taken and padding entries are 0, so each of the k <= n rounds
+  // picks an untaken candidate in [0, n), whatever the logits hold.
   float v[4];
-  bool taken[4];
+  unsigned long long key[4];
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int c = lane + u * kWave;
     v[u] = c < n ? zr[c] : -INFINITY;
-    taken[u] = c >= n;
+    key[u] = c < n ? ((unsigned long long)order_key(v[u]) << 32) | (unsigned)~c : 0ull;
   }
-  // k rounds of wave arg-max over the untaken entries: (value desc, index asc).
   float kept_v = -INFINITY;   // lane j < k ends with the j-th kept value and index
-  int kept_i = -1;
+  int kept_i = 0;
   for (int r = 0; r < k; ++r) {
-    float bv = -INFINITY;
-    int bi = 0x7fffffff;
+    unsigned long long best = key[0];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = lane + u * kWave;
-      if (!taken[u] && ranks_before(v[u], c, bv, bi)) {
-        bv = v[u];
-        bi = c;
-      }
-    }
+    for (int u = 1; u < 4; ++u) best = key[u] > best ? key[u] : best;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
-      const float ov = shfl_xor(bv, o);
-      const int oi = shfl_xor(bi, o);
-      if (ranks_before(ov, oi, bv, bi)) {
-        bv = ov;
-        bi = oi;
-      }
+      const unsigned lo = shfl_xor((int)(unsigned)best, o);
+      const unsigned hi = shfl_xor((int)(unsigned)(best >> 32), o);
+      const unsigned long long other = ((unsigned long long)hi << 32) | lo;
+      best = other > best ? other : best;
     }
+    const int bi = min(max((int)~(unsigned)best, 0), n - 1);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
-      if (lane + u * kWave == bi) taken[u] = true;
+      if (lane + u * kWave == bi) key[u] = 0ull;
     if (lane == r) {
-      kept_v = bv;
+      kept_v = zr[bi];
       kept_i = bi;
     }
   }

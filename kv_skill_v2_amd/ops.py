@@ -866,10 +866,13 @@ def read_rows(q: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, w_sel: torch.
     qp = _pad_rows(q, lib_)
     M = qp.shape[0]
     grad = torch.is_grad_enabled() and (q.requires_grad or w.requires_grad)
-    if grad or lib_.values is not None or M > DECODE_MAX_ROWS:
-        if not prefill_ok(lib_):
-            raise ValueError("this read needs the MFMA prefill path, which takes pages of <= 512 "
-                             f"slots (got {lib_.slots_per_page}); split the chunks")
+    mfma = grad or lib_.values is not None or M > DECODE_MAX_ROWS
+    if mfma and not prefill_ok(lib_):
+        if grad or lib_.values is not None:
+            raise ValueError("a differentiable or untied-value read takes pages of <= 512 slots "
+                             f"(got {lib_.slots_per_page})")
+        mfma = False        # a forward read of larger pages: the split-K decode path takes any size
+    if mfma:
         r = ReadFn.apply(qp, w, lib_, lib_.plan([M]), float(read_temp), bool(read_softmax))
     else:
         r = library_read_decode(qp, lib_, idx, w_sel, None, read_temp, read_softmax)

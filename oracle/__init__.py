@@ -26,8 +26,13 @@ Pins (each function is checked by tests/test_oracle.py against something other t
                                the reference's tests use (tests/test_d18_library.py:73-93); one
                                document == the D13 joint read with absolute RoPE (xenc/d18_library
                                .py:14-15; a planted RoPE-offset mistake moves y by 0.06)
-  epilogue                     parity unpinned for rms_norm's eps and ModelInterface internals
-                               (deltaskill is absent); fixed here as documented parameters.
+  rms_norm / query / epilogue  closed forms: a constant vector, the output RMS and scale
+                               invariance of rms_norm; identity A, the output norm, scale
+                               invariance and a pure-Python product for query; gate = 1/2 with
+                               B = I, sigmoid(log 3) = 3/4 with gain 2, B = 0 gives exactly 0, and
+                               a pure-Python loop for epilogue.  The eps value of rms_norm (1e-6)
+                               and the interface's initialisation remain documented parameters:
+                               deltaskill, which defines them, is absent.
 """
 
 from .xenc_oracle import *  # noqa: F401,F403

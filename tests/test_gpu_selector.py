@@ -34,6 +34,32 @@ def test_selector_weights(dev, B, n, k, ties):
     assert int((w.cpu() != 0).sum(1).min()) == k
 
 
+def test_selector_weights_non_finite_logits(dev):
+    """NaN, +inf and -inf logits: every kept index lies in [0, n) and the order is the oracle's
+    (NaN ranks above +inf as torch.sort / topk rank it, ties to the lower index); rows of all
+    NaN or all -inf included.  The weights of a row with a kept NaN are NaN, as the softmax of
+    the reference gives."""
+    say("selector weights, non-finite logits")
+    nan, inf = float("nan"), float("inf")
+    z = torch.randn(6, 8, generator=torch.Generator().manual_seed(4))
+    z[0, 3] = nan
+    z[1] = nan
+    z[2] = -inf
+    z[3, 5], z[3, 1] = inf, inf
+    z[4, :4] = nan
+    z[4, 6] = -inf
+    z[5, 7] = -inf
+    for k in (1, 2, 5, 8):
+        w, idx, w_sel = ops.selector_weights(z.to(dev), k)
+        idx = idx.cpu().long()
+        assert int(idx.min()) >= 0 and int(idx.max()) < 8
+        assert torch.equal(idx, O.topk_order(z, k)), k
+        finite_rows = [r for r in range(6) if torch.isfinite(z[r].gather(0, idx[r])).all()]
+        ref = O.selector_weights(z.double(), k)
+        for r in finite_rows:
+            assert float((w[r].cpu().double() - ref[r]).abs().max()) < 1e-6
+
+
 def test_selector_apply_one_and_summed(dev):
     say("selector apply")
     g = torch.Generator().manual_seed(3)

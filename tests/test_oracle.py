@@ -267,6 +267,93 @@ def test_selector_matched_norm_identity():
         assert torch.allclose(ratio, w[..., 3] * 0.02, atol=1e-5)
 
 
+# ---------------------------------------------------------------- R3 / R8: rms_norm, query, epilogue
+# deltaskill (which holds rms_norm and ModelInterface) is absent, so the eps and the interface's
+# initialisation stay documented parameters; what the mathematics fixes is pinned here.
+def test_rms_norm_closed_forms():
+    """Constant vector c*1 -> c / sqrt(c^2 + eps) in every entry (a sum in place of the mean would
+    give c / sqrt(d c^2)); the output RMS is sqrt(ms / (ms + eps)); positive scaling leaves the
+    output unchanged up to eps; a pure-Python loop on a ragged vector."""
+    for c, d in ((3.0, 7), (-0.5, 16), (1e-2, 5)):
+        y = O.rms_norm(torch.full((2, d), c, dtype=torch.float64))
+        want = c / math.sqrt(c * c + 1e-6)
+        assert torch.allclose(y, torch.full_like(y, want), rtol=0, atol=1e-15)
+    x = torch.randn(4, 33, generator=torch.Generator().manual_seed(5), dtype=torch.float64)
+    y = O.rms_norm(x)
+    ms = x.pow(2).mean(-1)
+    assert torch.allclose(y.pow(2).mean(-1).sqrt(), (ms / (ms + 1e-6)).sqrt(), rtol=0, atol=1e-14)
+    # scaling by a moves the output by the relative amount eps (1 - 1/a^2) / (2 ms) at most
+    assert torch.allclose(O.rms_norm(x * 250.0), y, rtol=2e-6, atol=0)
+    assert not torch.allclose(O.rms_norm(x * 250.0), y, rtol=1e-9, atol=0)
+    row = [0.25, -1.5, 2.0, 0.0, 3.75]
+    ms_py = sum(v * v for v in row) / len(row)
+    got = O.rms_norm(torch.tensor(row, dtype=torch.float64))
+    for j, v in enumerate(row):
+        assert abs(float(got[j]) - v / math.sqrt(ms_py + 1e-6)) < 1e-14
+
+
+def test_query_closed_forms():
+    """itf_query (xenc/injector.py:54-58): q = A hn / (|A hn| + 1e-6).  Identity A gives
+    hn / (|hn| + 1e-6); the norm is |A hn| / (|A hn| + 1e-6) < 1; positive scaling of hn keeps
+    the direction; a pure-Python matrix-vector product on a tiny case (a transposed A fails it)."""
+    g = torch.Generator().manual_seed(7)
+    hn = torch.randn(3, 4, 6, generator=g, dtype=torch.float64)
+    q = O.query(hn, torch.eye(6, dtype=torch.float64))
+    assert torch.allclose(q, hn / (hn.norm(dim=-1, keepdim=True) + 1e-6), rtol=0, atol=1e-15)
+    A = torch.randn(5, 6, generator=g, dtype=torch.float64)
+    q = O.query(hn, A)
+    n = (hn @ A.T).norm(dim=-1)
+    assert torch.allclose(q.norm(dim=-1), n / (n + 1e-6), rtol=0, atol=1e-14)
+    assert bool((q.norm(dim=-1) < 1).all())
+    q2 = O.query(hn * 40.0, A)
+    cos = (q * q2).sum(-1) / (q.norm(dim=-1) * q2.norm(dim=-1))
+    assert torch.allclose(cos, torch.ones_like(cos), rtol=0, atol=1e-14)
+    A2 = [[1.0, 2.0, 0.0], [0.0, -1.0, 3.0]]
+    h = [0.5, -2.0, 1.0]
+    Ah = [sum(A2[i][j] * h[j] for j in range(3)) for i in range(2)]
+    nrm = math.sqrt(sum(v * v for v in Ah))
+    got = O.query(torch.tensor([h], dtype=torch.float64), torch.tensor(A2, dtype=torch.float64))[0]
+    for i in range(2):
+        assert abs(float(got[i]) - Ah[i] / (nrm + 1e-6)) < 1e-15
+    bias = torch.tensor([1.0, -1.0], dtype=torch.float64)
+    got_b = O.query(torch.tensor([h], dtype=torch.float64), torch.tensor(A2, dtype=torch.float64), bias)[0]
+    Ahb = [Ah[0] + 1.0, Ah[1] - 1.0]
+    nb = math.sqrt(sum(v * v for v in Ahb))
+    assert abs(float(got_b[0]) - Ahb[0] / (nb + 1e-6)) < 1e-15
+
+
+def test_epilogue_closed_forms():
+    """delta = gain_scale * exp(log_gain[p]) * sigmoid(hn . gate_w + gate_b[p]) * B(r)
+    (xenc/injector.py:61-77, 266-267):
+      gate_w = 0, gate_b = 0, log_gain = 0, B = I       -> 0.5 r
+      gate_b = log 3 (sigmoid = 3/4), log_gain = log 2  -> 1.5 B r (a sign flip in the gate gives 0.5)
+      B = 0 (the interface's zero initialisation)       -> exactly 0 (the branch is a no-op at init)
+    and a pure-Python loop over a tiny case with a bias and gain_scale."""
+    g = torch.Generator().manual_seed(11)
+    hn = torch.randn(2, 3, 8, generator=g, dtype=torch.float64)
+    r = torch.randn(2, 3, 8, generator=g, dtype=torch.float64)
+    z8, one = torch.zeros(8, dtype=torch.float64), torch.eye(8, dtype=torch.float64)
+    zero = torch.tensor(0.0, dtype=torch.float64)
+    d = O.epilogue(hn, r, one, None, z8, zero, zero)
+    assert torch.allclose(d, 0.5 * r, rtol=0, atol=1e-15)
+    Bw = torch.randn(5, 8, generator=g, dtype=torch.float64)
+    d = O.epilogue(hn, r, Bw, None, z8, torch.tensor(math.log(3.0), dtype=torch.float64),
+                   torch.tensor(math.log(2.0), dtype=torch.float64))
+    assert torch.allclose(d, 1.5 * (r @ Bw.T), rtol=0, atol=1e-13)
+    d = O.epilogue(hn, r, torch.zeros(5, 8, dtype=torch.float64), None, torch.randn(8, generator=g,
+                   dtype=torch.float64), torch.tensor(-2.0, dtype=torch.float64), zero)
+    assert float(d.abs().max()) == 0.0
+    hn1, r1 = [0.5, -1.0, 2.0], [1.0, 0.25, -0.5]
+    gw, gb, lg, gs = [0.3, 0.1, -0.2], -0.4, 0.7, 2.5
+    Bm, bb = [[1.0, 0.0, 2.0], [-1.0, 3.0, 0.5]], [0.1, -0.2]
+    gate = 1.0 / (1.0 + math.exp(-(sum(a * b for a, b in zip(hn1, gw)) + gb)))
+    want = [gs * math.exp(lg) * gate * (sum(Bm[i][j] * r1[j] for j in range(3)) + bb[i]) for i in range(2)]
+    t = lambda v: torch.tensor(v, dtype=torch.float64)  # noqa: E731
+    got = O.epilogue(t([hn1]), t([r1]), t(Bm), t(bb), t(gw), t(gb), t(lg), gs)[0]
+    for i in range(2):
+        assert abs(float(got[i]) - want[i]) < 1e-14
+
+
 # ---------------------------------------------------------------- R11: op B oracle
 def _opb_case(N=3, hq=16, hkv=4, d=32, bs=4, nb_op=20, nb_own=10, seed=0):
     """Shapes and lengths of tests/test_d23_kernels.py:26-35."""
