@@ -35,7 +35,8 @@ enum {
   XENC_ENULL = -2,       /* a required pointer is NULL */
   XENC_EALIGN = -3,      /* a pointer or stride breaks the 16-byte alignment the kernels need */
   XENC_EWORKSPACE = -4,  /* the workspace passed in is smaller than the size query returned */
-  XENC_EHIP = -5         /* a kernel launch failed; see xenc_last_hip_error() */
+  XENC_EHIP = -5,        /* a kernel launch failed; see xenc_last_hip_error() */
+  XENC_ESCRATCH = -6     /* the call needs more than the allocation-free entry point's fixed scratch */
 };
 
 const char* xenc_strerror(int code);
@@ -103,6 +104,30 @@ int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
                              float read_temp, int softmax, int nsplit,
                              float* r, long long ldr,
                              void* workspace, size_t workspace_bytes, int max_rows, void* stream);
+
+/*
+ * Allocation-free variant of xenc_library_read_decode: the same read, the same arguments without
+ * the workspace.  Its partials, page order and arrival counters live in a file-scope device array
+ * of XENC_DECODE_SCRATCH_BYTES bytes (64 MiB) that each GPU the library runs on holds until the
+ * process ends; calls of up to XENC_DECODE_SCRATCH_ROWS query rows whose workspace
+ * (xenc_decode_workspace_bytes(XENC_DECODE_SCRATCH_ROWS, kk, nsplit, d) for those rows) fits in
+ * it are accepted, larger ones return XENC_ESCRATCH.  No hipMalloc, hipFree or allocating
+ * library call is made.  The first call on a device (with that device current) looks the array
+ * up and zeroes its counters with a kernel; make it before capturing a graph.  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (different streams, not ordered)
+ * race and give wrong results.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ */
+#define XENC_DECODE_SCRATCH_BYTES (64u << 20)
+#define XENC_DECODE_SCRATCH_ROWS 1024
+int xenc_library_read_decode_noalloc(const float* q, long long ldq, int M, int d,
+                                     const void* pages, int slots_per_page, long long page_stride,
+                                     const int* chunk_page, const int* chunk_nvalid,
+                                     const int* chunk_ptr, const int* q_group, int G,
+                                     const int* idx, const float* w_sel, int kk,
+                                     float read_temp, int softmax, int nsplit,
+                                     float* r, long long ldr, void* stream);
 
 /*
  * ---- Prefill / registration read (many query rows per library; MFMA, fp16 in, fp32 accumulate)

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _lock = threading.Lock()
 _lib = None
@@ -46,6 +46,13 @@ SIGNATURES = {
         c_float, c_int, c_int,                       # read_temp, softmax, nsplit
         c_void_p, c_longlong,                        # r, ldr
         c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_rows, stream
+    "xenc_library_read_decode_noalloc": (c_int, [
+        c_void_p, c_longlong, c_int, c_int,          # q, ldq, M, d
+        c_void_p, c_int, c_longlong,                 # pages, slots_per_page, page_stride
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,  # chunk_page, chunk_nvalid, chunk_ptr, q_group, G
+        c_void_p, c_void_p, c_int,                   # idx, w_sel, kk
+        c_float, c_int, c_int,                       # read_temp, softmax, nsplit
+        c_void_p, c_longlong, c_void_p]),            # r, ldr, stream
     "xenc_cast_rows_f16": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p]),
     "xenc_fragment_pages": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p]),
     "xenc_build_pages": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p,
@@ -158,7 +165,7 @@ def check(rc: int, what: str) -> None:
     msg = L.xenc_strerror(rc).decode()
     if rc == -5:
         msg += f" (hipError {L.xenc_last_hip_error()})"
-    if rc in (-1, -2, -3, -4):
+    if rc in (-1, -2, -3, -4, -6):
         raise ValueError(f"{what}: {msg}")
     raise XencError(f"{what}: {msg}")
 

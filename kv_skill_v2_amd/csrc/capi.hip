@@ -14,10 +14,11 @@ extern "C" const char* xenc_strerror(int code) {
     case XENC_EALIGN: return "pointer or stride is not 16-byte aligned";
     case XENC_EWORKSPACE: return "workspace is smaller than the size query returned";
     case XENC_EHIP: return "HIP kernel launch failed";
+    case XENC_ESCRATCH: return "the call needs more than the fixed scratch of the allocation-free entry point";
     default: return "unknown error code";
   }
 }
 
 extern "C" int xenc_last_hip_error(void) { return xenc::g_last_hip_error; }
 
-extern "C" int xenc_abi_version(void) { return 12; }
+extern "C" int xenc_abi_version(void) { return 13; }

@@ -28,6 +28,7 @@
 // no merge on the first kernel's critical path).  Smaller launches publish each partial and
 // increment the query's counter; the last workgroup of the query merges and re-arms the counter.
 #include <algorithm>
+#include <mutex>
 
 #include "xenc_common.h"
 
@@ -549,16 +550,16 @@ extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_byte
   return check_launch();
 }
 
-extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
-                                        const void* pages, int slots_per_page,
-                                        long long page_stride, const int* chunk_page,
-                                        const int* chunk_nvalid, const int* chunk_ptr,
-                                        const int* q_group, int G, const int* idx,
-                                        const float* w_sel, int kk, float read_temp, int softmax,
-                                        int nsplit, float* r, long long ldr, void* workspace,
-                                        size_t workspace_bytes, int max_rows, void* stream) {
+// Validation and launches of the decode read over a workspace of workspace_bytes at `workspace`
+// whose counter region is sized for max_rows (shared by the two entry points below).
+static int read_decode(const float* q, long long ldq, int M, int d, const void* pages,
+                       int slots_per_page, long long page_stride, const int* chunk_page,
+                       const int* chunk_nvalid, const int* chunk_ptr, const int* q_group, int G,
+                       const int* idx, const float* w_sel, int kk, float read_temp, int softmax,
+                       int nsplit, float* r, long long ldr, void* workspace, size_t workspace_bytes,
+                       int max_rows, int short_code, hipStream_t st) {
   if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || slots_per_page <= 0) return XENC_EINVAL;
-  if (M > max_rows) return XENC_EWORKSPACE;
+  if (M > max_rows) return short_code;
   if (d % 8 != 0 || d > 8 * 512) return XENC_EINVAL;
   if (nsplit < 1 || nsplit > 64) return XENC_EINVAL;
   if (ldq < d || ldr < d || ldq % 4 != 0 || ldr % 4 != 0) return XENC_EINVAL;
@@ -572,7 +573,7 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
     return XENC_EALIGN;
   const long long units = (long long)M * kk * nsplit;
   if (units > 0x7fffffffLL) return XENC_EINVAL;
-  if (workspace_bytes < workspace_need(max_rows, (long long)M * kk, units, d)) return XENC_EWORKSPACE;
+  if (workspace_bytes < workspace_need(max_rows, (long long)M * kk, units, d)) return short_code;
   // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
   const size_t lds =
       std::max((size_t)std::max(XENC_DECODE_NW / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
@@ -586,7 +587,6 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
   const int split_slots = (slots_per_page + nsplit - 1) / nsplit;
   const float scale2 = read_temp * kLog2e;
   const _Float16* pg = static_cast<const _Float16*>(pages);
-  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (grouped)
     hipLaunchKernelGGL(page_order_kernel, dim3((unsigned)((entries + kOrderPerWg - 1) / kOrderPerWg)),
                        dim3(512), 0, st, idx, q_group, chunk_ptr, chunk_page, G, kk, (int)entries,
@@ -610,4 +610,75 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
     hipLaunchKernelGGL(merge_kernel, dim3(M), dim3(512), (size_t)4 * kk * nsplit * sizeof(float), st,
                        ws, idx, w_sel, kk, nsplit, d, softmax, r, ldr);
   return check_launch();
+}
+
+extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
+                                        const void* pages, int slots_per_page,
+                                        long long page_stride, const int* chunk_page,
+                                        const int* chunk_nvalid, const int* chunk_ptr,
+                                        const int* q_group, int G, const int* idx,
+                                        const float* w_sel, int kk, float read_temp, int softmax,
+                                        int nsplit, float* r, long long ldr, void* workspace,
+                                        size_t workspace_bytes, int max_rows, void* stream) {
+  return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid,
+                     chunk_ptr, q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr,
+                     workspace, workspace_bytes, max_rows, XENC_EWORKSPACE,
+                     reinterpret_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------- the allocation-free variant
+// A file-scope device array replaces the caller's workspace: every GPU the library runs on holds
+// its own copy (XENC_DECODE_SCRATCH_BYTES) until the process ends.  In host code `scratch` is
+// only a stand-in for the symbol; its device address is looked up once per device with
+// hipGetSymbolAddress (with that device current) and only that address reaches kernels.
+// The counter region is sized for kScratchRows rows and zeroed by a kernel the first time a
+// device is used; every call leaves it zero again (the merging workgroup re-arms its row).
+static __device__ __align__(256) unsigned char scratch[XENC_DECODE_SCRATCH_BYTES];
+constexpr int kScratchRows = XENC_DECODE_SCRATCH_ROWS;
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_for_current_device(hipStream_t st, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return XENC_EINVAL;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_hip_error(e);
+      return XENC_EHIP;
+    }
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((kScratchRows + 255) / 256), dim3(256), 0, st,
+                       static_cast<int*>(p), kScratchRows);
+    const int rc = check_launch();
+    if (rc != XENC_OK) return rc;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return XENC_OK;
+}
+
+extern "C" int xenc_library_read_decode_noalloc(const float* q, long long ldq, int M, int d,
+                                                const void* pages, int slots_per_page,
+                                                long long page_stride, const int* chunk_page,
+                                                const int* chunk_nvalid, const int* chunk_ptr,
+                                                const int* q_group, int G, const int* idx,
+                                                const float* w_sel, int kk, float read_temp,
+                                                int softmax, int nsplit, float* r, long long ldr,
+                                                void* stream) {
+  if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || slots_per_page <= 0 || nsplit < 1) return XENC_EINVAL;
+  if (M > kScratchRows) return XENC_ESCRATCH;
+  if (M == 0) return XENC_OK;
+  const long long units = (long long)M * kk * nsplit;
+  if (workspace_need(kScratchRows, (long long)M * kk, units, d) > (size_t)XENC_DECODE_SCRATCH_BYTES)
+    return XENC_ESCRATCH;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int rc = scratch_for_current_device(st, &ws);
+  if (rc != XENC_OK) return rc;
+  return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid,
+                     chunk_ptr, q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr, ws,
+                     (size_t)XENC_DECODE_SCRATCH_BYTES, kScratchRows, XENC_ESCRATCH, st);
 }
