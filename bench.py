@@ -149,10 +149,8 @@ def bench_prefill(args):
     torch.cuda.synchronize()
     frag_ms = (time.perf_counter() - t0) * 1e3
 
-    qh = torch.empty(q.shape[0], lib.d, dtype=torch.float16, device=dev)
-
     def fwd():
-        w, _, _ = ops.route_topk_rows(q, lib, plan, top_k=0, q_f16=qh)
+        w, _, _, qh = ops.route_topk_rows(q, lib, plan, top_k=0, emit_f16=True)
         r, p = ops.prefill_forward(q, w, lib, plan, qh=qh)
         return w, r, p
 
@@ -547,7 +545,7 @@ def bench_op_b(args):
     own_l = torch.full((B,), own_len, dtype=torch.int32, device=dev)
     q = torch.randn(B, hq, d, generator=g, device=dev).to(dt)
     scale = d ** -0.5
-    dec = DecodeReader(B, hq, hkv, d, max_keys=op_len + own_len, device=dev)
+    dec = DecodeReader(B, hq, hkv, d, max_keys=op_len + own_len, device=dev, chunk=None)
     chunk = dec.chunk
 
     def call():

@@ -2,7 +2,7 @@
 
 Same constructor and call signature as xenc/d23_read_kernels.py:134-160:
 
-    dec = DecodeReader(max_n, hq, hkv, d, max_keys, device, chunk=None, block_n=64)
+    dec = DecodeReader(max_n, hq, hkv, d, max_keys, device, chunk=1024, block_n=64)
     out = dec(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale)   # fp32 [N, hq, d]
 
 For each query row n and query head, one softmax over the operator's rows (paged pool op_k/op_v,
@@ -14,9 +14,10 @@ of its own output buffer (callers clone it if they keep it across calls).  A cal
 nothing, reads no device value on the host and synchronises nothing, so it can be captured in a
 HIP graph and replayed with new lengths / block tables.  `block_n` is accepted for signature
 compatibility (it sized the reference's key tile); the HIP kernel picks its own tiling.  `chunk`
-(keys per split) keeps the reference's meaning; left at None it is chosen from max_n, hkv and
-max_keys for about 1024 workgroups at full capacity (the reference's default is 1024).  The split
-only changes the order of the LSE merge, not what is computed.
+(keys per split) keeps the reference's meaning and default (1024); chunk=None, an addition of this
+build, chooses it from max_n, hkv and max_keys for about 1024 workgroups at full capacity (faster
+at small batches: 37 against 48 us for one row over 16k keys).  The split only changes the order
+of the LSE merge, not what is computed.
 """
 
 from __future__ import annotations
@@ -25,13 +26,14 @@ import math
 
 import torch
 
+from . import torch_ops  # noqa: F401  (registers torch.ops.xenc.paged_decode_joint)
 from ._lib import check, lib, ptr, stream_handle
 
 _DTYPES = {torch.float16: 0, torch.bfloat16: 1}
 
 
 class DecodeReader:
-    def __init__(self, max_n: int, hq: int, hkv: int, d: int, max_keys: int, device, chunk: int | None = None,
+    def __init__(self, max_n: int, hq: int, hkv: int, d: int, max_keys: int, device, chunk: int | None = 1024,
                  block_n: int = 64):
         if hq % hkv:
             raise ValueError(f"hq={hq} must be a multiple of hkv={hkv}")
@@ -91,10 +93,10 @@ class DecodeReader:
             raise ValueError("pools must both be fp16 or both bf16")
         if op_k.shape[2:] != (self.hkv, self.d) or own_k.shape[2:] != (self.hkv, self.d):
             raise ValueError(f"pools must be [num_blocks, block_size, {self.hkv}, {self.d}]")
-        osb, oss, osh, obs = self._pool(op_k, op_v, "operator")
-        wsb, wss, wsh, wbs = self._pool(own_k, own_v, "own")
-        obt = self._table(op_bt, op_len, N, "op")
-        wbt = self._table(own_bt, own_len, N, "own")
+        self._pool(op_k, op_v, "operator")
+        self._pool(own_k, own_v, "own")
+        self._table(op_bt, op_len, N, "op")
+        self._table(own_bt, own_len, N, "own")
         if q.dtype != op_k.dtype:
             q = q.to(op_k.dtype)
         if q.stride(-1) != 1:
@@ -102,13 +104,8 @@ class DecodeReader:
         out = self.out[:N]
         if N == 0:
             return out
-        rc = lib().xenc_paged_decode_joint(
-            _DTYPES[op_k.dtype], N, self.hq, self.hkv, self.d, ptr(q), q.stride(0), q.stride(1),
-            ptr(op_k), ptr(op_v), osb, oss, osh, obs, ptr(op_bt), obt, ptr(op_len),
-            ptr(own_k), ptr(own_v), wsb, wss, wsh, wbs, ptr(own_bt), wbt, ptr(own_len),
-            float(scale), self.S, self.chunk, ptr(out), out.stride(0), out.stride(1),
-            ptr(self.workspace), self.workspace.numel(), self.max_n, stream_handle(self.device))
-        check(rc, "xenc_paged_decode_joint")
+        torch.ops.xenc.paged_decode_joint(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, float(scale),
+                                          self.S, self.chunk, self.workspace, self.max_n, out)
         return out
 
 

@@ -16,6 +16,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _lib
+from . import torch_ops  # noqa: F401  (registers the torch.ops.xenc operators)
 from ._lib import check, lib, ptr, stream_handle
 
 
@@ -322,23 +323,12 @@ def route_topk(q: torch.Tensor, lib_: PagedLibrary, q_group=None, top_k: int = 0
                route_temp: float = 10.0):
     """(w_dense [M, cmax], idx [M, kk] int32, w_sel [M, kk]) for query rows q [M, d].
 
-    HIP kernel `route_topk_kernel` (kv_skill_v2_amd/csrc/route.hip); replaces
+    Operator xenc::route_topk (HIP route kernels, kv_skill_v2_amd/csrc/route.hip); replaces
     LibraryInjector.route (xenc/injector.py:220-229)."""
     q = _query(q, lib_.d)
-    M = q.shape[0]
-    g = _groups(lib_, M, q_group)
-    kk = lib_.kept(int(top_k))
-    dev = q.device
-    w = torch.empty(M, lib_.cmax, dtype=torch.float32, device=dev)
-    idx = torch.empty(M, kk, dtype=torch.int32, device=dev)
-    wsel = torch.empty(M, kk, dtype=torch.float32, device=dev)
-    if M == 0:
-        return w, idx, wsel
-    rc = lib().xenc_route_topk(ptr(q), q.stride(0), M, lib_.d, ptr(lib_.S), ptr(lib_.chunk_ptr),
-                               ptr(g), lib_.n_libraries, int(top_k), float(route_temp), ptr(w),
-                               w.stride(0), ptr(idx), ptr(wsel), kk, stream_handle(dev))
-    check(rc, "xenc_route_topk")
-    return w, idx, wsel
+    g = _groups(lib_, q.shape[0], q_group)
+    return torch.ops.xenc.route_topk(q, lib_.S, lib_.chunk_ptr, g, int(top_k), float(route_temp), lib_.cmax,
+                                     lib_.kept(int(top_k)))
 
 
 def default_nsplit(units: int, slots_per_page: int) -> int:
@@ -395,27 +385,19 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
     idx = idx.to(torch.int32).contiguous()
     w_sel = w_sel.to(torch.float32).contiguous()
     kk = idx.shape[1]
-    r = torch.empty(M, lib_.d, dtype=torch.float32, device=q.device)
     if M == 0 or kk == 0:
-        return r.zero_()
+        return torch.zeros(M, lib_.d, dtype=torch.float32, device=q.device)
     ns = int(nsplit) if nsplit is not None else default_nsplit(M * kk, lib_.slots_per_page)
-    L = lib()
-    st = stream_handle(q.device)
-    ws, rows = _WORKSPACES.get(q.device, st, M, kk, ns, lib_.d)
-    rc = L.xenc_library_read_decode(
-        ptr(q), q.stride(0), M, lib_.d, ptr(lib_.pages), lib_.slots_per_page,
-        lib_.pages.stride(0), ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid), ptr(lib_.chunk_ptr),
-        ptr(g), lib_.n_libraries, ptr(idx), ptr(w_sel), kk, float(read_temp), int(bool(softmax)),
-        ns, ptr(r), r.stride(0), ptr(ws), ws.numel(), rows, st)
-    check(rc, "xenc_library_read_decode")
-    return r
+    ws, rows = _WORKSPACES.get(q.device, stream_handle(q.device), M, kk, ns, lib_.d)
+    return torch.ops.xenc.library_read(q, lib_.pages, lib_.chunk_page, lib_.chunk_nvalid, lib_.chunk_ptr, g,
+                                       idx, w_sel, float(read_temp), bool(softmax), ns, ws, rows)
 
 
 # ---------------------------------------------------------------------------------------------
 # Prefill / registration read (MFMA) and the autograd of routing + read
 ROWS_SCORES, ROWS_READOUT, ROWS_ROUTE_BWD = 128, 128, 16
 ROUTE_TILE = 32            # rows and chunks per tile of the many-row routing kernel
-ROUTE_ROWS_MIN = 64        # from this many rows RouteFn uses the many-row routing kernel
+ROUTE_ROWS_MIN = 64        # from this many rows differentiable routing uses the many-row routing kernel
 
 
 def write_back(r: torch.Tensor, W: torch.Tensor, row_group: torch.Tensor | None = None,
@@ -659,105 +641,77 @@ def unpack_p(p: torch.Tensor, M: int) -> torch.Tensor:
     return p.view(-1, M, 8).permute(1, 0, 2).reshape(M, -1)
 
 
+def _prefill_operands(lib_: PagedLibrary, plan: RowPlan) -> tuple:
+    """The pool's tensor operands of xenc::library_prefill_fwd / _bwd_dq after q (and qh), w."""
+    return (lib_.fragment_pages(0), lib_.fragment_pages(1, values=True), lib_.fragment_pages(0, values=True),
+            lib_.fragment_pages(1), lib_.chunk_ptr, lib_.chunk_page, lib_.chunk_nvalid, plan.row_ptr,
+            plan.score_tiles, plan.readout_tiles, plan.n_score, plan.n_readout, lib_.slots_per_page)
+
+
 def prefill_forward(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
                     read_temp: float = 12.0, softmax: bool = True, qh: torch.Tensor | None = None):
     """(r [M, d] fp32, p fp16 octet-major [cmax*slots/8, M, 8]): the route-weighted masked-softmax
-    (or linear) read of many query rows.  HIP kernels scores_kernel<0|2> + readout_kernel
-    (kv_skill_v2_amd/csrc/prefill.hip); unpack_p gives p row-major.  qh: q as fp16 rows already
-    (route_topk_rows(..., q_f16=) writes it); cast here when not given."""
+    (or linear) read of many query rows, operator xenc::library_prefill_fwd (HIP kernels
+    scores_kernel<0|2> + readout_kernel, kv_skill_v2_amd/csrc/prefill.hip); differentiable in q
+    and w.  unpack_p gives p row-major.  qh: q as fp16 rows already (route_topk_rows(...,
+    emit_f16=True) writes them); cast here when not given."""
     lib_.check_prefill()
     q = _query(q, lib_.d)
     M, d = q.shape
     if M != plan.M or w.shape != (M, lib_.cmax):
         raise ValueError(f"q must have {plan.M} rows and w shape ({plan.M}, {lib_.cmax})")
-    w = w.to(torch.float32).contiguous()
-    L, st, N = lib(), stream_handle(q.device), lib_.slots_per_page
-    if qh is None:
-        qh = cast_f16(q)
-    elif qh.dtype != torch.float16 or qh.shape != (M, d) or not qh.is_contiguous():
+    if w.dtype != torch.float32 or not w.is_contiguous():
+        w = w.to(torch.float32).contiguous()
+    if qh is not None and (qh.dtype != torch.float16 or qh.shape != (M, d) or not qh.is_contiguous()):
         raise ValueError(f"qh must be contiguous fp16 [{M}, {d}]")
-    ka, vb = lib_.fragment_pages(0), lib_.fragment_pages(1, values=True)
-    p = torch.empty(lib_.cmax * N // 8, M, 8, dtype=torch.float16, device=q.device)
-    check(L.xenc_prefill_scores(0 if softmax else 2, ptr(qh), d, ptr(plan.row_ptr), ptr(plan.score_tiles),
-                                lib_.n_libraries, plan.n_score, ptr(ka), N, ka.stride(0),
-                                ptr(lib_.chunk_ptr), ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid),
-                                float(read_temp), None, 0, ptr(p), M, None, None, 0, st), "xenc_prefill_scores")
-    r = torch.empty(M, d, dtype=torch.float32, device=q.device)
-    check(L.xenc_prefill_readout(ptr(p), M, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
-                                 plan.n_readout, ptr(vb), N, d, vb.stride(0), ptr(lib_.chunk_ptr),
-                                 ptr(lib_.chunk_page), ptr(w), w.stride(0), ptr(r), r.stride(0), st),
-          "xenc_prefill_readout")
-    return r, p
+    fk, fv, fvs, fkr, *rest = _prefill_operands(lib_, plan)
+    ragged = min(lib_.n_chunks) != lib_.cmax
+    return torch.ops.xenc.library_prefill_fwd(q, qh, w, fk, fv, fvs, fkr, *rest, float(read_temp), bool(softmax),
+                                              ragged)
 
 
 def prefill_backward(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, lib_: PagedLibrary,
                      plan: RowPlan, read_temp: float = 12.0, softmax: bool = True):
     """(dq through the read [M, d] fp32, gamma = dL/dw through the read [M, cmax] fp32) given the
-    upstream gradient g = dL/dr.  HIP kernels scores_kernel<1|3> (u = g . V) + readout_kernel
-    (dq = dS . K)."""
+    upstream gradient g = dL/dr: operator xenc::library_prefill_bwd_dq (scores_kernel<1|3>,
+    u = g . V, then readout_kernel, dq = dS . K)."""
     g = _query(g, lib_.d)
     M, d = g.shape
     w = w.to(torch.float32).contiguous()
-    L, st, N = lib(), stream_handle(g.device), lib_.slots_per_page
-    gh = cast_f16(g)
-    if p.shape != (lib_.cmax * N // 8, M, 8) or not p.is_contiguous():
+    if p.shape != (lib_.cmax * lib_.slots_per_page // 8, M, 8) or not p.is_contiguous():
         raise ValueError("p must be the octet-major probabilities prefill_forward returned")
-    va, kb = lib_.fragment_pages(0, values=True), lib_.fragment_pages(1)
-    ds = torch.empty_like(p)
-    gamma = torch.zeros(M, lib_.cmax, dtype=torch.float32, device=g.device)
-    check(L.xenc_prefill_scores(1 if softmax else 3, ptr(gh), d, ptr(plan.row_ptr), ptr(plan.score_tiles),
-                                lib_.n_libraries, plan.n_score, ptr(va), N, va.stride(0),
-                                ptr(lib_.chunk_ptr), ptr(lib_.chunk_page), ptr(lib_.chunk_nvalid),
-                                float(read_temp), ptr(w), w.stride(0), ptr(p), M, ptr(ds), ptr(gamma),
-                                gamma.stride(0), st), "xenc_prefill_scores")
-    dq = torch.empty(M, d, dtype=torch.float32, device=g.device)
-    check(L.xenc_prefill_readout(ptr(ds), M, ptr(plan.row_ptr), ptr(plan.readout_tiles), lib_.n_libraries,
-                                 plan.n_readout, ptr(kb), N, d, kb.stride(0), ptr(lib_.chunk_ptr),
-                                 ptr(lib_.chunk_page), None, 0, ptr(dq), dq.stride(0), st),
-          "xenc_prefill_readout")
-    return dq, gamma
+    _, _, fvs, fkr, *rest = _prefill_operands(lib_, plan)
+    return torch.ops.xenc.library_prefill_bwd_dq(g, w, p, fvs, fkr, *rest, float(read_temp), bool(softmax))
 
 
 def route_backward(w: torch.Tensor, dw: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
                    route_temp: float, dq: torch.Tensor, dw_ext: torch.Tensor | None = None) -> torch.Tensor:
-    """dq += route_temp * sum_c w (dw - sum w dw) S_c, in place (HIP route_backward_kernel)."""
+    """dq += route_temp * sum_c w (dw - sum w dw) S_c, in place (operator xenc::route_backward_)."""
     w = w.to(torch.float32).contiguous()
     dw = dw.to(torch.float32).contiguous()
     if dw_ext is not None:
         dw_ext = dw_ext.to(torch.float32).contiguous()
-    check(lib().xenc_route_backward(ptr(w), w.stride(0), ptr(dw), dw.stride(0), ptr(dw_ext),
-                                    dw_ext.stride(0) if dw_ext is not None else 0, ptr(plan.row_ptr),
-                                    ptr(plan.route_tiles), lib_.n_libraries, plan.n_route, lib_.cmax,
-                                    ptr(lib_.S), ptr(lib_.chunk_ptr), lib_.d, float(route_temp), ptr(dq),
-                                    dq.stride(0), stream_handle(dq.device)), "xenc_route_backward")
+    torch.ops.xenc.route_backward_(dq, w, dw, dw_ext, lib_.S, lib_.chunk_ptr, plan.row_ptr, plan.route_tiles,
+                                   plan.n_route, float(route_temp))
     return dq
 
 
 def route_topk_rows(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int = 0,
-                    route_temp: float = 10.0, q_f16: torch.Tensor | None = None):
+                    route_temp: float = 10.0, emit_f16: bool = False):
     """route_topk for query rows grouped by library as in `plan` (rows of library g contiguous):
-    the q . S dots as 32 x 32 fp32 MFMA tiles, then the same top-k / softmax per row.  HIP
-    kernels route_rows_logits_kernel + route_rows_select_kernel.  q_f16 (optional, fp16 [M, d]
-    contiguous) receives q as fp16 from the same read (prefill_forward's qh operand)."""
+    the q . S dots as 32 x 32 fp32 MFMA tiles, then the same top-k / softmax per row (operator
+    xenc::route_rows: route_rows_logits_kernel + route_rows_select_kernel; differentiable in q
+    through w).  Returns (w, idx, w_sel), plus q as fp16 rows from the same pass (the MFMA read's
+    operand) when emit_f16."""
     q = _query(q, lib_.d)
-    M = q.shape[0]
-    if M != plan.M:
+    if q.shape[0] != plan.M:
         raise ValueError(f"q must have {plan.M} rows")
-    kk = lib_.kept(int(top_k))
-    dev = q.device
-    w = torch.empty(M, lib_.cmax, dtype=torch.float32, device=dev)
-    idx = torch.empty(M, kk, dtype=torch.int32, device=dev)
-    wsel = torch.empty(M, kk, dtype=torch.float32, device=dev)
-    if M == 0:
-        return w, idx, wsel
-    if q_f16 is not None and (q_f16.dtype != torch.float16 or q_f16.shape != (M, lib_.d)
-                              or not q_f16.is_contiguous()):
-        raise ValueError(f"q_f16 must be contiguous fp16 [{M}, {lib_.d}]")
-    check(lib().xenc_route_topk_rows(ptr(q), q.stride(0), M, lib_.d, ptr(lib_.S), ptr(lib_.chunk_ptr),
-                                     ptr(plan.row_ptr), ptr(plan.logit_tiles), lib_.n_libraries, plan.n_logit,
-                                     int(top_k), float(route_temp), ptr(w), w.stride(0), ptr(idx), ptr(wsel),
-                                     kk, ptr(q_f16), stream_handle(dev)), "xenc_route_topk_rows")
-    return w, idx, wsel
+    if lib_.cmax > 1024:
+        raise ValueError("the many-row routing takes libraries of at most 1024 chunks")
+    out = torch.ops.xenc.route_rows(q, lib_.S, lib_.chunk_ptr, plan.row_ptr, plan.logit_tiles, plan.route_tiles,
+                                    plan.n_logit, plan.n_route, int(top_k), float(route_temp), lib_.cmax,
+                                    lib_.kept(int(top_k)), bool(emit_f16))
+    return out if emit_f16 else out[:3]
 
 
 def _plan_groups(plan: RowPlan) -> torch.Tensor:
@@ -765,19 +719,14 @@ def _plan_groups(plan: RowPlan) -> torch.Tensor:
     return g.to(torch.int32)
 
 
-class RouteFn(torch.autograd.Function):
-    """w [M, cmax] = route(q); differentiable in q through the softmax over the kept logits."""
+class _RouteFewRows(torch.autograd.Function):
+    """Differentiable routing of fewer rows than the many-row kernel's tiles pay for: forward by
+    xenc::route_topk, backward by xenc::route_backward_."""
 
     @staticmethod
-    def forward(ctx, q, lib_, plan, top_k, route_temp, qh=None):
-        if plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
-            w, idx, wsel = route_topk_rows(q.detach(), lib_, plan, top_k=top_k, route_temp=route_temp,
-                                           q_f16=qh)
-        else:
-            qg = _plan_groups(plan).to(q.device)
-            if qh is not None:
-                raise ValueError("qh is written by the row-grouped routing path only")
-            w, idx, wsel = route_topk(q.detach(), lib_, qg, top_k=top_k, route_temp=route_temp)
+    def forward(ctx, q, lib_, plan, top_k, route_temp):
+        qg = _plan_groups(plan).to(q.device)
+        w, idx, wsel = route_topk(q.detach(), lib_, qg, top_k=top_k, route_temp=route_temp)
         ctx.save_for_backward(w)
         ctx.lib, ctx.plan, ctx.route_temp = lib_, plan, route_temp
         ctx.mark_non_differentiable(idx, wsel)
@@ -789,24 +738,17 @@ class RouteFn(torch.autograd.Function):
         dq = torch.zeros(w.shape[0], ctx.lib.d, dtype=torch.float32, device=w.device)
         if dw is not None:
             route_backward(w, dw, ctx.lib, ctx.plan, ctx.route_temp, dq)
-        return dq, None, None, None, None, None
+        return dq, None, None, None, None
 
 
-class ReadFn(torch.autograd.Function):
-    """r [M, d] = route-weighted masked-softmax (or linear) read; differentiable in q and w."""
-
-    @staticmethod
-    def forward(ctx, q, w, lib_, plan, read_temp, softmax=True, qh=None):
-        r, p = prefill_forward(q.detach(), w.detach(), lib_, plan, read_temp, softmax, qh=qh)
-        ctx.save_for_backward(w, p)
-        ctx.lib, ctx.plan, ctx.read_temp, ctx.softmax = lib_, plan, read_temp, softmax
-        return r
-
-    @staticmethod
-    def backward(ctx, dr):
-        w, p = ctx.saved_tensors
-        dq, gamma = prefill_backward(dr, w, p, ctx.lib, ctx.plan, ctx.read_temp, ctx.softmax)
-        return dq, gamma, None, None, None, None, None
+def route_differentiable(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int, route_temp: float,
+                         emit_f16: bool = False):
+    """(w, idx, w_sel[, qh]) with autograd through w: the many-row routing operator for at least
+    ROUTE_ROWS_MIN rows, the few-row one below."""
+    if plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
+        return route_topk_rows(q, lib_, plan, top_k, route_temp, emit_f16=emit_f16)
+    out = _RouteFewRows.apply(_query(q, lib_.d), lib_, plan, int(top_k), float(route_temp))
+    return (*out, None) if emit_f16 else out
 
 
 def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int = 0,
@@ -814,11 +756,8 @@ def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int 
     """(r [M, d], w [M, cmax]) with autograd through both routing and the read (MFMA path).  The
     routing pass also writes the fp16 rows the read takes, so q is read from HBM once."""
     lib_.check_prefill()
-    qh = None
-    if plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
-        qh = torch.empty(plan.M, lib_.d, dtype=torch.float16, device=_query(q, lib_.d).device)
-    w, _, _ = RouteFn.apply(q, lib_, plan, int(top_k), float(route_temp), qh)
-    r = ReadFn.apply(q, w, lib_, plan, float(read_temp), bool(read_softmax), qh)
+    w, _, _, qh = route_differentiable(q, lib_, plan, int(top_k), float(route_temp), emit_f16=True)
+    r, _ = prefill_forward(q, w, lib_, plan, float(read_temp), bool(read_softmax), qh=qh)
     return r, w
 
 
@@ -851,7 +790,7 @@ def route_rows(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, route_temp: 
     _single(lib_)
     qp = _pad_rows(q, lib_)
     if torch.is_grad_enabled() and q.requires_grad:
-        return RouteFn.apply(qp, lib_, lib_.plan([qp.shape[0]]), int(top_k), float(route_temp))
+        return route_differentiable(qp, lib_, lib_.plan([qp.shape[0]]), int(top_k), float(route_temp))
     return route_topk(qp, lib_, None, top_k, route_temp)
 
 
@@ -873,7 +812,7 @@ def read_rows(q: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, w_sel: torch.
                              f"(got {lib_.slots_per_page})")
         mfma = False        # a forward read of larger pages: the split-K decode path takes any size
     if mfma:
-        r = ReadFn.apply(qp, w, lib_, lib_.plan([M]), float(read_temp), bool(read_softmax))
+        r, _ = prefill_forward(qp, w, lib_, lib_.plan([M]), float(read_temp), bool(read_softmax))
     else:
         r = library_read_decode(qp, lib_, idx, w_sel, None, read_temp, read_softmax)
     return r[:, :lib_.d_valid] if lib_.d != lib_.d_valid else r
@@ -984,7 +923,7 @@ def d18_read(qd: torch.Tensor, qo: torch.Tensor, ops, Kown: torch.Tensor, Vown: 
 
 
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
-           "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "RouteFn", "ReadFn",
+           "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "route_differentiable",
            "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS",
            "build_pages", "write_back", "select_scores", "topk_rows", "gather_library", "selector_weights",
            "selector_apply", "gate_scale", "D18Operators", "d18_pack", "d18_read", "d18_nsplit"]

@@ -22,7 +22,7 @@ ROOT = Path(__file__).resolve().parents[1]
 
 def _stub() -> dict:
     text = (ROOT / "INTEGRATION.md").read_text()
-    sec = text[text.index("## 2. Binding the C ABI"):]
+    sec = text[text.index("## 3. Binding the C ABI"):]
     code = re.search(r"```python\n(.*?)```", sec, re.S).group(1)
     code = code.replace("/path/to/kv_skill_v2_amd/_lib/libxenc_hip.so", str(_lib.LIB_PATH))
     ns: dict = {}

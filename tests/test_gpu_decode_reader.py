@@ -91,6 +91,45 @@ def test_decode_reader_layouts(dev, hq, hkv, d, dtype):
     assert _rel(out, ref) < 2e-3, _rel(out, ref)
 
 
+def _rel_rows(out, ref):
+    """Largest relative error over the (row, query head) vectors with a nonzero reference; rows
+    with no keys must read exactly 0."""
+    out, ref = out.double().cpu(), ref.double()
+    nrm = ref.norm(dim=-1)
+    live = nrm > 0
+    if bool((~live).any()):
+        assert float(out[~live].abs().max()) == 0.0
+    return float(((out - ref).norm(dim=-1)[live] / nrm[live]).max())
+
+
+@pytest.mark.parametrize("op_bs,own_bs", [(12, 16), (16, 12), (12, 12), (16, 8)])
+@pytest.mark.parametrize("hq,hkv,d,dtype", [(8, 2, 64, torch.bfloat16), (16, 4, 128, torch.float16),
+                                            (16, 4, 256, torch.bfloat16)])
+def test_decode_reader_block_sizes_per_row(dev, op_bs, own_bs, hq, hkv, d, dtype):
+    """Operator and own pools with different block sizes, including ones that are not powers of
+    two (the division path of the key lookup), on the VALU form (d = 64) and the MFMA form
+    (d = 128, 256); every (row, head) output within rel 2e-3 of the oracle on its own."""
+    say("op B block sizes", dict(op_bs=op_bs, own_bs=own_bs, hq=hq, hkv=hkv, d=d, dtype=str(dtype)))
+    g = torch.Generator().manual_seed(op_bs * 100 + own_bs + d)
+    N = 6
+    op_len, own_len = [300, 0, 12, 1, 257, 131], [5, 40, 0, 1, 80, 13]
+    nb_op, nb_own = 64, 40
+    op_k, op_v = (torch.randn(nb_op, op_bs, hkv, d, generator=g).to(dtype) for _ in range(2))
+    own_k, own_v = (torch.randn(nb_own, own_bs, hkv, d, generator=g).to(dtype) for _ in range(2))
+    q = torch.randn(N, hq, d, generator=g).to(dtype)
+    op_bt = torch.stack([torch.randperm(nb_op, generator=g)[:-(-max(op_len) // op_bs)] for _ in range(N)]).int()
+    own_bt = torch.stack([torch.randperm(nb_own, generator=g)[:-(-max(own_len) // own_bs)] for _ in range(N)]).int()
+    args = [q, op_k, op_v, op_bt, torch.tensor(op_len, dtype=torch.int32), own_k, own_v, own_bt,
+            torch.tensor(own_len, dtype=torch.int32)]
+    for chunk in (64, 1024):
+        dec = DecodeReader(8, hq, hkv, d, max_keys=max(a + b for a, b in zip(op_len, own_len)), device=dev,
+                           chunk=chunk)
+        out = dec(*[a.to(dev) for a in args], 1.0 / d ** 0.5)
+        ref = _ref(args, 1.0 / d ** 0.5)
+        err = _rel_rows(out, ref)
+        assert err < 2e-3, (chunk, err)
+
+
 def test_decode_reader_empty_rows_and_reuse(dev):
     """A row with no keys reads 0; one workspace serves calls of different N in any order; keys
     past nsplit * chunk are still read (the last split takes them)."""

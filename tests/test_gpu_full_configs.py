@@ -99,9 +99,8 @@ def test_prefill_full_shape_row_sample(dev):
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     g_up = torch.randn(G * T, d, generator=gen, device=dev)
-    qh = torch.empty(G * T, d, dtype=torch.float16, device=dev)
     with torch.no_grad():
-        w, _, _ = ops.route_topk_rows(q, lib, plan, top_k=0, q_f16=qh)
+        w, _, _, qh = ops.route_topk_rows(q, lib, plan, top_k=0, emit_f16=True)
         r, p = ops.prefill_forward(q, w, lib, plan, qh=qh)
         dq, gamma = ops.prefill_backward(g_up, w, p, lib, plan)
         ops.route_backward(w, gamma, lib, plan, 10.0, dq)

@@ -163,7 +163,7 @@ def test_route_rows_matches_per_row_kernel(dev, counts, rows, top_k):
 
 @pytest.mark.parametrize("counts,rows", [([32, 7, 130], [300, 64, 129]), ([3], [33]), ([40, 2], [1, 97])])
 def test_route_rows_fp16_rows_are_the_cast(dev, counts, rows):
-    """The routing pass's fp16 copy of q (q_f16) equals cast_f16 bit for bit on every row (ragged
+    """The routing pass's fp16 copy of q (emit_f16) equals cast_f16 bit for bit on every row (ragged
     row tiles, several chunk tiles per row tile), and prefill_forward gives the same bits with it
     as with its own cast; library_read, which shares the copy between routing and read, equals
     the two calls."""
@@ -173,8 +173,7 @@ def test_route_rows_fp16_rows_are_the_cast(dev, counts, rows):
     lib = _lib(P, dev)
     plan = ops.row_plan(lib, rows)
     q = synth.queries(sum(rows), d, device=dev, seed=5)
-    qh = torch.full((q.shape[0], d), float("nan"), dtype=torch.float16, device=dev)
-    w, _, _ = ops.route_topk_rows(q, lib, plan, top_k=0, q_f16=qh)
+    w, _, _, qh = ops.route_topk_rows(q, lib, plan, top_k=0, emit_f16=True)
     assert torch.equal(qh, ops.cast_f16(q))
     r1, p1 = ops.prefill_forward(q, w, lib, plan, qh=qh)
     r2, p2 = ops.prefill_forward(q, w, lib, plan)
