@@ -1,116 +1,141 @@
 """Reader-side injectors: forward hooks that add the Library read to a reader's residual stream.
 
-LibraryInjector keeps the API of xenc/injector.py:121-273: per-token routing over the chunk
-summary keys (optional top-k), the masked per-chunk read, the route-weighted merge, the
-gate * gain * B write-back, an optional LayerSelector, and the bookkeeping (mag_terms, last_route,
-route_terms, record_attn / last_attn, force_attn / force_norm_match, training_attn / attn_pos /
-attn_terms).  The routing and the read run in the HIP kernels of kv_skill_v2_amd.ops:
-    route_rows  -> route_topk_kernel (no grad) or RouteFn (route kernel + route backward)
-    read_rows   -> the split-K decode kernel (few rows, no grad) or ReadFn (MFMA prefill read and
-                   its dQ backward)
-The query map, RMS norm, gate, gain and B projection stay in torch around them, as in the
-reference.  The diagnostics that expose or replace the [C, N] slot attention (record_attn,
-training_attn, force_attn) compute that one [C, N] map with torch on the device from the
-Library's fp32 K.
+LibraryInjector keeps the API of xenc/injector.py:121-273 (constructor, load_library / unload,
+route, _branch, and the bookkeeping attributes mag_terms, last_route, route_terms, record_attn /
+last_attn, force_attn / force_norm_match, training_attn / attn_pos / attn_terms) and
+XEncInjector the single-skill API (xenc/injector.py:80-118).  The work of one hooked layer runs
+in three stages:
 
-XEncInjector is the single-skill path (xenc/injector.py:80-118): one skill is read as a one-chunk
-Library (routing over one chunk gives w = 1 exactly).
+    query      hn = rms_norm(h), q = the interface's query map of hn                  (torch)
+    read       routing over the chunk summaries, then the masked per-chunk read of the routed
+               pages merged by the route weights                                       (HIP)
+    update     delta = gain_scale * gain * gate * B(r), then the LayerSelector if set  (HIP on
+               the decode path, torch with autograd)
 
-The hook plumbing (`enabled`, `_handles`, `mag_terms`, `detach`, `gain_scale`, `calib`,
-`_pos_mask`) is the contract of the base injector the reference subclasses from an external
-package; it is restated in `SkillInjector`.  No position mask is applied (`_pos_mask` returns
-None) and gain_scale defaults to 1.0.
+The read goes through torch.ops.xenc: few rows without autograd take the split-K decode
+operators (xenc::route_topk, xenc::library_read), many rows or autograd the MFMA operators
+(xenc::route_rows, xenc::library_prefill_fwd, both differentiable).  With a LayerSelector the
+rows a layer does not select are not read: their routed-chunk lists are emptied on the device
+(index -1), so the read returns 0 for them without a host synchronisation, and their update is
+multiplied by the selector's exact 0 afterwards.
+
+The diagnostics that expose or replace the [C, N] slot attention (record_attn, training_attn,
+force_attn) compute that one map with torch on the device from the Library's K.
+
+The base class SkillInjector carries the hook contract of the external package the reference
+subclasses (enabled, _handles, mag_terms, detach, gain_scale, calib, _pos_mask): no position mask
+is applied (`_pos_mask` returns None) and gain_scale defaults to 1.0.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
 from . import ops
 from .depth import KVSkill, decoder_layers, for_reader
-from .interface import ModelInterface
+from .interface import ModelInterface, apply_map
 from .library import PAGE_ALIGN, Library
 from .selector import rms_norm
 
 
-def _on(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
-    """`t` on like's device; the same object when it is already there."""
+def _here(t: torch.Tensor, like: torch.Tensor) -> torch.Tensor:
     return t if t.device == like.device else t.to(like.device)
 
 
-def _linear(mod: nn.Module, x: torch.Tensor) -> torch.Tensor:
-    if isinstance(mod, nn.Sequential):
-        for m in mod:
-            x = _linear(m, x)
-        return x
-    b = None if mod.bias is None else _on(mod.bias, x)
-    return F.linear(x, _on(mod.weight, x), b)
+# ----------------------------------------------------------------------------- interface calls
+# An interface is any object with query(hn), gate(hn, li), gain(li) and write(r); ModelInterface's
+# methods bring their weights to the input's device themselves.
+def itf_query(itf, hn: torch.Tensor) -> torch.Tensor:
+    return itf.query(hn)
 
 
-# The fused write-back kernel serves the decode path (few rows, no autograd); many rows go to
-# the library GEMM, whose W reuse across rows the kernel does not have.
+def itf_gate(itf, hn: torch.Tensor, li: int) -> torch.Tensor:
+    return itf.gate(hn, li)
+
+
+def itf_gain(itf, li: int, like: torch.Tensor) -> torch.Tensor:
+    return _here(itf.gain(li), like)
+
+
+def itf_write(itf, r: torch.Tensor) -> torch.Tensor:
+    return itf.write(r)
+
+
+# The fused write-back serves the decode path (few rows, no autograd); many rows go to the
+# library GEMM, whose reuse of B across rows the kernel does not have.
 _FUSED_WRITE_ROWS = 64
+
+
+def _needs_grad(itf, *tensors) -> bool:
+    if not torch.is_grad_enabled():
+        return False
+    if any(isinstance(t, torch.Tensor) and t.requires_grad for t in tensors):
+        return True
+    return isinstance(itf, nn.Module) and any(p.requires_grad for p in itf.parameters())
 
 
 def write_delta(itf, hn: torch.Tensor, r: torch.Tensor, li: int, gain_scale: float,
                 gcal=1.0) -> torch.Tensor:
     """delta = gain_scale * gain * gcal * gate * B(r) (xenc/injector.py:266-267).  On the decode
-    path (a ModelInterface with an fp32 linear B, at most 64 rows, nothing requiring grad) the
-    product runs as one xenc_write_back launch: B streamed once with gate * gain folded into a
-    per-row scale."""
-    Bm = getattr(itf, "B", None) if isinstance(itf, ModelInterface) else None
+    path (a ModelInterface with a plain linear B in fp32, at most 64 rows, nothing requiring grad)
+    it is one HIP row scale (xenc_gate_scale) and one write-back launch that streams B once with
+    the scale folded in (xenc_write_back)."""
     rows = r.numel() // r.shape[-1]
-    grad = torch.is_grad_enabled() and (
-        r.requires_grad or hn.requires_grad
-        or (isinstance(itf, nn.Module) and any(p.requires_grad for p in itf.parameters()))
-        or (isinstance(gcal, torch.Tensor) and gcal.requires_grad))
-    fused = (isinstance(Bm, nn.Linear) and r.is_cuda and r.dtype == torch.float32
-             and Bm.weight.dtype == torch.float32 and rows <= _FUSED_WRITE_ROWS
-             and r.shape[-1] % 4 == 0 and not grad and isinstance(gcal, (int, float)))
+    B = itf.B if isinstance(itf, ModelInterface) else None
+    fused = (isinstance(B, nn.Linear) and r.is_cuda and r.dtype == torch.float32 and B.weight.dtype == torch.float32
+             and rows <= _FUSED_WRITE_ROWS and r.shape[-1] % 4 == 0 and isinstance(gcal, (int, float))
+             and not _needs_grad(itf, r, hn))
     if not fused:
         return gain_scale * itf_gain(itf, li, hn) * gcal * itf_gate(itf, hn, li) * itf_write(itf, r)
-    # gain_scale * gcal * exp(log_gain[p]) * sigmoid(hn . gate_w + gate_b[p]) per row on
-    # xenc_gate_scale, then B streamed once with that scale folded in (xenc_write_back).
     p = itf._pos[li]
-    scale = ops.gate_scale(hn.reshape(rows, hn.shape[-1]).float().contiguous(), _on(itf.gate_w, r),
-                           _on(itf.gate_b, r)[p:p + 1], _on(itf.log_gain, r)[p:p + 1],
+    scale = ops.gate_scale(hn.reshape(rows, hn.shape[-1]).float().contiguous(), _here(itf.gate_w, r),
+                           _here(itf.gate_b, r)[p:p + 1], _here(itf.log_gain, r)[p:p + 1],
                            float(gain_scale) * float(gcal))
-    W = _on(Bm.weight, r).contiguous()
-    b = None if Bm.bias is None else _on(Bm.bias, r).float().contiguous()
-    out = ops.write_back(r.reshape(rows, r.shape[-1]).contiguous(), W, None, b, scale)
-    return out.view(*r.shape[:-1], W.shape[0])
+    bias = None if B.bias is None else _here(B.bias, r).float().contiguous()
+    out = ops.write_back(r.reshape(rows, r.shape[-1]).contiguous(), _here(B.weight, r).contiguous(), None,
+                         bias, scale)
+    return out.view(*r.shape[:-1], B.weight.shape[0])
 
 
-def itf_query(itf, hn: torch.Tensor) -> torch.Tensor:
-    if not isinstance(itf, ModelInterface):
-        return itf.query(hn)
-    q = _linear(itf.A, hn)
-    return q / (q.norm(dim=-1, keepdim=True) + 1e-6)
+# ----------------------------------------------------------------------------- hooks
+class _AddUpdate:
+    """Forward hook of one injection layer: the layer's output hidden state plus the branch's
+    update, recording mean |delta| / |h| in the injector's mag_terms."""
+
+    def __init__(self, owner: "SkillInjector", li: int):
+        self.owner, self.li = owner, li
+
+    def __call__(self, module, args, output):
+        inj = self.owner
+        if not inj._active():
+            return output
+        packed = isinstance(output, tuple)
+        h = output[0] if packed else output
+        delta = inj._branch(h, self.li).to(h.dtype)
+        mask = inj._pos_mask(h)
+        if mask is not None:
+            delta = delta * mask
+        ratio = torch.linalg.vector_norm(delta.float(), dim=-1) / (torch.linalg.vector_norm(h.float(), dim=-1) + 1e-6)
+        inj.mag_terms.append(ratio.mean())
+        out = h + delta
+        return (out, *output[1:]) if packed else out
 
 
-def itf_gate(itf, hn: torch.Tensor, li: int) -> torch.Tensor:
-    if not isinstance(itf, ModelInterface):
-        return itf.gate(hn, li)
-    return torch.sigmoid(hn @ _on(itf.gate_w, hn) + _on(itf.gate_b, hn)[itf._pos[li]]).unsqueeze(-1)
+class _ResetSelector:
+    """Forward pre-hook on the first injection layer: a new forward starts, so the selector's
+    weights of the previous one are dropped (each decode step recomputes them)."""
 
+    def __init__(self, owner: "LibraryInjector"):
+        self.owner = owner
 
-def itf_gain(itf, li: int, like: torch.Tensor) -> torch.Tensor:
-    if not isinstance(itf, ModelInterface):
-        return _on(itf.gain(li), like)
-    return _on(itf.log_gain, like)[itf._pos[li]].exp()
-
-
-def itf_write(itf, r: torch.Tensor) -> torch.Tensor:
-    if not isinstance(itf, ModelInterface):
-        return itf.write(r)
-    return _linear(itf.B, r)
+    def __call__(self, module, args):
+        if self.owner.selector is not None:
+            self.owner.selector.reset()
 
 
 class SkillInjector:
-    """Hook plumbing: one forward hook per injection layer adds `_branch(h, li)` to the layer's
-    output hidden state and records mean ||delta|| / ||h|| in `mag_terms`."""
+    """Hook contract: one forward hook per injection layer of the interface."""
 
     def __init__(self, model: nn.Module, interface, read_fp32: bool = True, read_softmax: bool = True,
                  read_temp: float = 12.0, gain_scale: float = 1.0):
@@ -130,31 +155,13 @@ class SkillInjector:
     def _pos_mask(self, h: torch.Tensor):
         return None
 
-    def _hook(self, li: int):
-        def hook(mod, args, output):
-            if not self._active():
-                return output
-            is_tuple = isinstance(output, tuple)
-            h = output[0] if is_tuple else output
-            delta = self._branch(h, li).to(h.dtype)
-            mask = self._pos_mask(h)
-            if mask is not None:
-                delta = delta * mask
-            rel = delta.float().norm(dim=-1) / (h.float().norm(dim=-1) + 1e-6)
-            self.mag_terms.append(rel.mean())
-            h = h + delta
-            return (h,) + tuple(output[1:]) if is_tuple else h
-        return hook
-
     def _attach(self) -> None:
         blocks = decoder_layers(self.model)
-        for li in self.itf.inject_layers:
-            self._handles.append(blocks[li].register_forward_hook(self._hook(li)))
+        self._handles.extend(blocks[li].register_forward_hook(_AddUpdate(self, li)) for li in self.itf.inject_layers)
 
     def detach(self) -> None:
-        for h in self._handles:
-            h.remove()
-        self._handles.clear()
+        while self._handles:
+            self._handles.pop().remove()
 
     def load(self, skill) -> None:
         self.skill = skill
@@ -163,56 +170,53 @@ class SkillInjector:
         self.skill = None
         self.mag_terms.clear()
 
+    def _query(self, h: torch.Tensor):
+        hn = rms_norm(h)
+        return hn, itf_query(self.itf, hn)
+
 
 class XEncInjector(SkillInjector):
+    """One skill read as a one-chunk Library: routing over a single chunk gives w = 1 exactly, so
+    the read is softmax(read_temp q K^T) V over every skill row."""
+
     def load(self, skill: KVSkill) -> None:
         if skill.meta.get("keyed_by") == "rho":
             skill = for_reader(skill, self.model)
         if skill.d_s != self.itf.d_s:
-            raise ValueError(f"skill d_s={skill.d_s} (encoder) != interface d_s={self.itf.d_s}")
-        missing = set(self.itf.inject_layers) - set(skill.K)
-        if missing:
-            raise KeyError(f"skill has no operator for reader layers {sorted(missing)}")
-        self._skill_pool = {}
+            raise ValueError(f"the skill has d_s={skill.d_s} (its encoder), the interface d_s={self.itf.d_s}")
+        uncovered = sorted(set(self.itf.inject_layers) - set(skill.K))
+        if uncovered:
+            raise KeyError(f"the skill holds no operator for reader layers {uncovered}")
+        self._skill_pools = {}
         super().load(skill)
 
-    def _skill_kv(self, li: int, like: torch.Tensor):
-        """Skill K / V of layer li on like's device (moved once, cached in the loaded skill)."""
-        K, V = self.skill.K[li], self.skill.V[li]
-        if K.device != like.device:
-            K = self.skill.K[li] = K.to(like.device)
-        if V.device != like.device:
-            V = self.skill.V[li] = V.to(like.device)
-        return K, V
+    def _skill_pool(self, li: int, device) -> ops.PagedLibrary:
+        """The skill of layer li as a one-chunk read pool on `device` (built once per load)."""
+        key = (li, device)
+        pool = self._skill_pools.get(key)
+        if pool is None:
+            K, V = self.skill.K[li], self.skill.V[li]
+            K3 = K.float()[None]
+            mask = torch.ones(K3.shape[:2], dtype=torch.bool, device=K3.device)
+            pool = ops.PagedLibrary.from_padded(K3, mask, K3[0].mean(0, keepdim=True), device=device,
+                                                V=None if V is K else V.float()[None], pad_to=PAGE_ALIGN)
+            self._skill_pools[key] = pool
+        return pool
 
-    def _skill_paged(self, li: int, like: torch.Tensor):
-        """The skill of layer li as a one-chunk HIP read pool (all rows valid)."""
-        key = (li, like.device)
-        pl = self._skill_pool.get(key)
-        if pl is None:
-            K, V = self._skill_kv(li, like)
-            K3 = K.float().unsqueeze(0)
-            M = torch.ones(K3.shape[:2], dtype=torch.bool, device=K3.device)
-            S = K3[0].mean(0, keepdim=True)
-            pl = ops.PagedLibrary.from_padded(K3, M, S, device=like.device,
-                                              V=None if V is K else V.float().unsqueeze(0), pad_to=PAGE_ALIGN)
-            self._skill_pool[key] = pl
-        return pl
+    def _calibrated(self, r: torch.Tensor, li: int):
+        """(r, gcal) after the optional per-layer calibration {li: {"scale", "gain"}}."""
+        if self.calib is None or li not in self.calib:
+            return r, 1.0
+        cal = self.calib[li]
+        g = cal["gain"]
+        return r * _here(cal["scale"], r), (_here(g, r) if isinstance(g, torch.Tensor) else g)
 
     def _branch(self, h: torch.Tensor, li: int) -> torch.Tensor:
-        """delta = gain_scale * gain * gate * B(read), the read over all skill rows."""
-        hn = rms_norm(h.float())
-        q = itf_query(self.itf, hn)
-        B_, T_, d = q.shape
-        r, _ = ops.branch_read(q.reshape(B_ * T_, d), self._skill_paged(li, hn), 0, self.read_temp,
-                               1.0, self.read_softmax)
-        r = r.view(B_, T_, d)
-        gcal = 1.0
-        if self.calib is not None and li in self.calib:
-            r = r * _on(self.calib[li]["scale"], r)
-            gcal = self.calib[li]["gain"]
-            if isinstance(gcal, torch.Tensor):
-                gcal = _on(gcal, r)
+        hn, q = self._query(h)
+        lead, d = q.shape[:-1], q.shape[-1]
+        r, _ = ops.branch_read(q.reshape(-1, d), self._skill_pool(li, hn.device), 0, self.read_temp, 1.0,
+                               self.read_softmax)
+        r, gcal = self._calibrated(r.view(*lead, -1), li)
         return write_delta(self.itf, hn, r, li, self.gain_scale, gcal)
 
 
@@ -228,10 +232,11 @@ class LibraryInjector(XEncInjector):
         self.last_attn: dict = {}
         self.force_attn = None         # a [C, N] map (or {li: [C, N]}) replacing the attention
         self.force_norm_match = False  # rescale the forced read per token to the computed read's norm
-        self.training_attn = False     # keep aw[0, attn_pos] with grad per hooked layer
+        self.training_attn = False     # keep the [C, N] attention at attn_pos with grad per hooked layer
         self.attn_pos: int = -1
         self.attn_terms: list = []
         self.route_terms: list = []
+        self._dense_cache: dict = {}
         super().__init__(model, interface, read_fp32=read_fp32, read_softmax=read_softmax,
                          read_temp=read_temp)
 
@@ -242,149 +247,130 @@ class LibraryInjector(XEncInjector):
 
     def load_library(self, lib: Library) -> None:
         if lib.d_s != self.itf.d_s:
-            raise ValueError(f"library d_s={lib.d_s} (encoder) != interface d_s={self.itf.d_s}")
-        missing = set(self.itf.inject_layers) - set(lib.K)
-        if missing:
-            raise KeyError(f"library has no operator for reader layers {sorted(missing)}")
+            raise ValueError(f"the library has d_s={lib.d_s} (its encoder), the interface d_s={self.itf.d_s}")
+        uncovered = sorted(set(self.itf.inject_layers) - set(lib.K))
+        if uncovered:
+            raise KeyError(f"the library holds no operator for reader layers {uncovered}")
         dtype = torch.float32 if self.read_fp32 else next(self.model.parameters()).dtype
         self.skill = None
+        self._dense_cache = {}
         self.lib = lib.to(self.model.device, dtype)
 
     def unload(self) -> None:
         """Unload and clear the per-forward bookkeeping."""
-        self.skill = None
-        self.lib = None
-        self.mag_terms.clear()
-        self.route_terms.clear()
-        self.attn_terms.clear()
-        self.last_route = None
+        self.skill = self.lib = self.last_route = None
+        self._dense_cache = {}
+        for log in (self.mag_terms, self.route_terms, self.attn_terms):
+            log.clear()
 
     # ------------------------------------------------------------------ hooks
     def _active(self) -> bool:
         return self.enabled and (self.skill is not None or self.lib is not None)
 
     def _attach(self) -> None:
-        blocks = decoder_layers(self.model)
-
-        def pre(mod, args):          # start of every forward (each decode step included)
-            if self.selector is not None:
-                self.selector.reset()
-
-        self._handles.append(blocks[self.itf.inject_layers[0]].register_forward_pre_hook(pre))
+        first = decoder_layers(self.model)[self.itf.inject_layers[0]]
+        self._handles.append(first.register_forward_pre_hook(_ResetSelector(self)))
         super()._attach()
 
     # ------------------------------------------------------------------ library tensors
-    def _lib_layer(self, li: int, like: torch.Tensor):
-        """(K, mask, S) of layer li on like's device, moved once and cached in the Library."""
-        lib = self.lib
-        if lib.K[li].device != like.device:
-            lib.K[li] = lib.K[li].to(like.device)
-            lib.mask[li] = lib.mask[li].to(like.device)
-            lib.S[li] = lib.S[li].to(like.device)
-        return lib.K[li], lib.mask[li], lib.S[li]
-
-    def _lib_values(self, li: int, like: torch.Tensor) -> torch.Tensor:
-        lib = self.lib
-        if lib.V is None:
-            return self._lib_layer(li, like)[0]
-        if lib.V[li].device != like.device:
-            lib.V[li] = lib.V[li].to(like.device)
-        return lib.V[li]
-
-    def _pool(self, li: int, like: torch.Tensor):
+    def _pool(self, li: int, like: torch.Tensor) -> ops.PagedLibrary:
         return self.lib.paged(li, like.device)
+
+    def _dense(self, li: int, device) -> tuple:
+        """(K, mask, V) of layer li on `device` for the torch diagnostics (V is K when tied)."""
+        key = (li, device)
+        if key not in self._dense_cache:
+            K = self.lib.K[li].to(device)
+            M = self.lib.mask[li].to(device)
+            V = K if self.lib.V is None else self.lib.V[li].to(device)
+            self._dense_cache[key] = (K, M, V)
+        return self._dense_cache[key]
 
     # ------------------------------------------------------------------ route / read
     def route(self, q: torch.Tensor, li: int) -> torch.Tensor:
         """Routing weights [B, T, C] over the chunks: sum to 1, exactly top_k nonzeros if set."""
-        pl = self._pool(li, q)
-        B_, T_, d = q.shape
-        w, _, _ = ops.route_rows(q.reshape(B_ * T_, d), pl, self.top_k, self.route_temp)
-        return w.view(B_, T_, -1)
+        w, _, _ = ops.route_rows(q.reshape(-1, q.shape[-1]), self._pool(li, q), self.top_k, self.route_temp)
+        return w.view(*q.shape[:-1], -1)
 
-    def _attn_rows(self, q_rows: torch.Tensor, w_rows: torch.Tensor, li: int) -> torch.Tensor:
-        """aw [R, C, N] = (masked softmax or linear read weights) * w for a few rows (torch)."""
-        K, M, _ = self._lib_layer(li, q_rows)
-        a = torch.einsum("rd,cnd->rcn", q_rows.to(K.dtype), K)
+    def _read(self, q: torch.Tensor, pool: ops.PagedLibrary, keep: torch.Tensor | None = None):
+        """(r [B, T, d], w [B, T, C]).  keep (bool [B, T], device): rows left out read nothing and
+        get r = 0 (their routed-chunk lists are emptied on the device)."""
+        lead, d = q.shape[:-1], q.shape[-1]
+        rows = q.reshape(-1, d)
+        w, idx, w_sel = ops.route_rows(rows, pool, self.top_k, self.route_temp)
+        if keep is not None:
+            idx = torch.where(keep.reshape(-1, 1), idx, torch.full_like(idx, -1))
+        r = ops.read_rows(rows, w, idx, w_sel, pool, self.read_temp, self.read_softmax)
+        return r.view(*lead, -1), w.view(*lead, -1)
+
+    def _slot_attention(self, q_rows: torch.Tensor, w_rows: torch.Tensor, li: int) -> torch.Tensor:
+        """Route-weighted slot attention [R, C, N] of a few query rows (torch)."""
+        K, M, _ = self._dense(li, q_rows.device)
+        s = torch.einsum("rd,cnd->rcn", q_rows.to(K.dtype), K)
         if self.read_softmax:
-            a = torch.softmax((a * self.read_temp).masked_fill(~M, float("-inf")), -1)
+            a = torch.softmax((s * self.read_temp).masked_fill(~M, float("-inf")), dim=-1)
         else:
-            n = M.sum(-1).to(a.dtype).clamp_min(1)
-            a = a.masked_fill(~M, 0.0) / n.sqrt().view(1, -1, 1)
-        return a * w_rows.to(a.dtype).unsqueeze(-1)
+            n = M.sum(-1).to(s.dtype).clamp_min(1)
+            a = s.masked_fill(~M, 0.0) / n.sqrt()[None, :, None]
+        return a * w_rows.to(a.dtype)[..., None]
 
-    def _forced(self, li: int, like: torch.Tensor, r: torch.Tensor) -> tuple:
-        """(r, fa, scale): the read under force_attn.  fa [C, N] replaces the attention of every
-        token; with force_norm_match each token's forced map is scaled by scale [B, T, 1] =
-        ||computed read|| / (||forced read|| + 1e-6), both reads taken with K as values."""
+    def _forced_read(self, li: int, q: torch.Tensor, r: torch.Tensor):
+        """(r, fa, scale) under force_attn: the [C, N] map fa replaces every token's attention.
+        With force_norm_match each token's forced read is scaled by |computed read| /
+        (|forced read| + 1e-6), both taken with K as the values."""
         fa = self.force_attn.get(li) if isinstance(self.force_attn, dict) else self.force_attn
-        K, M, _ = self._lib_layer(li, like)
-        fa = _on(fa, K).to(K.dtype)
+        K, M, V = self._dense(li, q.device)
+        fa = _here(fa, K).to(K.dtype)
         if fa.shape != M.shape:
-            raise ValueError(f"force_attn {tuple(fa.shape)} != library [C,N] {tuple(M.shape)}")
-        Vt = self._lib_values(li, like)
-        out = (fa.reshape(-1) @ Vt.reshape(-1, Vt.shape[-1])).expand_as(r).to(r.dtype)
-        scale = None
-        if self.force_norm_match:
-            r0 = r
-            if self.lib.V is not None:   # the computed read's norm is taken with K as values
-                pl = self._pool(li, like)
-                tied = ops.PagedLibrary(pl.pages, pl.chunk_page, pl.chunk_nvalid, pl.chunk_ptr, pl.S,
-                                        n_chunks=pl.n_chunks, nvalid=pl.nvalid, d_valid=pl.d_valid)
-                r0 = self._read_all(self._last_q, li, tied)[0]
-            k1 = fa.reshape(-1) @ K.reshape(-1, K.shape[-1])
-            scale = r0.norm(dim=-1, keepdim=True) / (k1.norm() + 1e-6)
-            out = out * scale.to(out.dtype)
-        return out, fa, scale
+            raise ValueError(f"force_attn {tuple(fa.shape)} does not match the library's [C, N] {tuple(M.shape)}")
+        flat = fa.reshape(-1)
+        out = (flat @ V.reshape(-1, V.shape[-1])).to(r.dtype).expand_as(r)
+        if not self.force_norm_match:
+            return out, fa, None
+        r_keys = r
+        if self.lib.V is not None:        # the computed read's norm is taken with K as the values
+            pool = self._pool(li, q)
+            tied = ops.PagedLibrary(pool.pages, pool.chunk_page, pool.chunk_nvalid, pool.chunk_ptr, pool.S,
+                                    n_chunks=pool.n_chunks, nvalid=pool.nvalid, d_valid=pool.d_valid)
+            r_keys = self._read(q, tied)[0]
+        forced_keys = flat @ K.reshape(-1, K.shape[-1])
+        scale = torch.linalg.vector_norm(r_keys, dim=-1, keepdim=True) / (torch.linalg.vector_norm(forced_keys) + 1e-6)
+        return out * scale.to(out.dtype), fa, scale
 
-    def _read_all(self, q: torch.Tensor, li: int, pl, rows: torch.Tensor | None = None):
-        """(r [B, T, d], w [B, T, C]); with `rows` (bool [B, T]) only those rows are read, the
-        others get r = 0 (their update is multiplied by an exact 0 afterwards)."""
-        B_, T_, d = q.shape
-        q2 = q.reshape(B_ * T_, d)
-        w, idx, wsel = ops.route_rows(q2, pl, self.top_k, self.route_temp)
-        if rows is None:
-            r = ops.read_rows(q2, w, idx, wsel, pl, self.read_temp, self.read_softmax)
+    def _keep_diagnostics(self, li: int, q, w, fa, scale) -> None:
+        """record_attn: the [C, N] attention of the last position (detached, on the host);
+        training_attn: the one at attn_pos with grad (batch row 0 for both)."""
+        want_train = self.training_attn and torch.is_grad_enabled()
+        if not (self.record_attn or want_train):
+            return
+        at = [q.shape[1] - 1, self.attn_pos]
+        if fa is None:
+            maps = self._slot_attention(q[0, at], w[0, at], li)
         else:
-            sel = rows.reshape(-1).nonzero().squeeze(1)
-            r = torch.zeros(B_ * T_, d, dtype=torch.float32, device=q.device)
-            if sel.numel():
-                rs = ops.read_rows(q2.index_select(0, sel), w.index_select(0, sel), idx.index_select(0, sel),
-                                   wsel.index_select(0, sel), pl, self.read_temp, self.read_softmax)
-                r = r.index_copy(0, sel, rs)
-        return r.view(B_, T_, d), w.view(B_, T_, -1)
+            maps = fa[None].expand(2, *fa.shape)
+            if scale is not None:
+                maps = maps * scale[0, at].to(fa.dtype).view(2, 1, 1)
+        if self.record_attn:
+            self.last_attn[li] = maps[0].detach().float().cpu()
+        if want_train:
+            self.attn_terms.append(maps[1].float())
 
     def _branch(self, h: torch.Tensor, li: int) -> torch.Tensor:
         if self.lib is None:                               # single-skill path
             delta = super()._branch(h, li)
         else:
-            hn = rms_norm(h.float())
-            q = itf_query(self.itf, hn)                    # [B, T, d_s]
-            pl = self._pool(li, hn)
-            diag = self.force_attn is not None or self.record_attn or (
+            hn, q = self._query(h)                         # q [B, T, d_s]
+            pool = self._pool(li, hn)
+            diagnostics = self.force_attn is not None or self.record_attn or (
                 self.training_attn and torch.is_grad_enabled())
-            rows = None
-            if self.selector is not None and hasattr(self.selector, "selected_rows") and not diag:
-                rows = self.selector.selected_rows(h, li)
-            self._last_q = q
-            r, w = self._read_all(q, li, pl, rows)
+            keep = None
+            if self.selector is not None and hasattr(self.selector, "selected_rows") and not diagnostics:
+                keep = self.selector.selected_rows(h, li)
+            r, w = self._read(q, pool, keep)
             fa = scale = None
             if self.force_attn is not None:
-                r, fa, scale = self._forced(li, hn, r)
-            if self.record_attn or (self.training_attn and torch.is_grad_enabled()):
-                pos = [q.shape[1] - 1, self.attn_pos]
-                if fa is None:
-                    aw2 = self._attn_rows(q[0, pos], w[0, pos], li)
-                else:
-                    aw2 = fa.unsqueeze(0).expand(2, *fa.shape)
-                    if scale is not None:
-                        aw2 = aw2 * scale[0, pos].to(fa.dtype).view(2, 1, 1)
-                last, at = aw2[0], aw2[1]
-                if self.record_attn:
-                    self.last_attn[li] = last.detach().float().cpu()
-                if self.training_attn and torch.is_grad_enabled():
-                    self.attn_terms.append(at.float())
-            self._last_q = None
+                r, fa, scale = self._forced_read(li, q, r)
+            self._keep_diagnostics(li, q, w, fa, scale)
             delta = write_delta(self.itf, hn, r, li, self.gain_scale)
             self.last_route = w.detach()
             if torch.is_grad_enabled():
@@ -395,4 +381,4 @@ class LibraryInjector(XEncInjector):
 
 
 __all__ = ["SkillInjector", "XEncInjector", "LibraryInjector", "itf_query", "itf_gate", "itf_gain",
-           "itf_write", "write_delta", "rms_norm"]
+           "itf_write", "write_delta", "rms_norm", "apply_map"]

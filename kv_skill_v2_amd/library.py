@@ -1,16 +1,21 @@
 """Library: the chunk operators of one or more documents, keyed by reader layer.
 
-Per reader layer li (the API of xenc/library.py:21-136):
-    K[li]    [C, N_max, d_s]  chunk slot rows, zero-padded past each chunk's n_c valid rows
+Per reader layer li (the attributes of xenc/library.py:25-136):
+    K[li]    [C, N_max, d_s]  chunk slot rows, zero past each chunk's n_c valid rows
     mask[li] [C, N_max] bool  valid slots (a prefix of each row)
     S[li]    [C, d_s]         summary key L2(mean of the valid rows), used for routing
     V[li]    [C, N_max, d_s]  values, only when the chunks carry untied values (else V is None
                               and K serves as the values)
 
-On top of the reference layout, `paged(li, device)` gives the device pool the HIP read kernels
-take: fp16 pages [C, N_pad, d_pad] (one page per chunk, N and d rounded up to 64 with masked
-slots / zero features), the page table, valid counts and fp32 S.  It is built once per
-(layer, device) and dropped whenever the Library is moved, cast or re-centred.
+Every layer is assembled the same way from a list of per-chunk row blocks [n_c, d_s] (`_assemble`):
+the constructor passes the cache rows (centred first when a centre is given), `subset` passes
+the valid rows of the chosen chunks, so a subset is by construction the Library those chunks
+would build alone.
+
+`paged(li, device)` gives the device pool the HIP read kernels take: fp16 pages [C, N_pad, d_pad]
+(one page per chunk, N and d rounded up to 64 with masked slots / zero features), the page table,
+valid counts and fp32 S.  It is built once per (layer, device) and dropped whenever the Library is
+moved, cast or re-centred.
 """
 
 from __future__ import annotations
@@ -25,13 +30,36 @@ PAGE_ALIGN = 64   # page slots and features are padded to this for the MFMA pref
 
 
 def l2(x: torch.Tensor) -> torch.Tensor:
-    return x / (x.norm(dim=-1, keepdim=True) + _EPS)
+    return x / (torch.linalg.vector_norm(x, dim=-1, keepdim=True) + _EPS)
 
 
-def _field(chunk, name):
-    if hasattr(chunk, name):
-        return getattr(chunk, name)
-    return chunk.get(name) if isinstance(chunk, dict) else None
+def _get(chunk, name):
+    """Field `name` of a chunk given as an object (attribute) or a cache dict (key)."""
+    if isinstance(chunk, dict):
+        return chunk.get(name)
+    return getattr(chunk, name, None)
+
+
+def _meta_of(chunk) -> dict:
+    m = getattr(chunk, "meta", None)
+    if m is None and isinstance(chunk, dict):
+        m = {k: v for k, v in chunk.items() if k not in ("K", "V")}
+    return dict(m or {})
+
+
+def _assemble(blocks: list[torch.Tensor]) -> tuple[torch.Tensor, torch.Tensor]:
+    """(padded [C, N_max, d], valid-prefix mask [C, N_max]) from per-chunk blocks [n_c, d]."""
+    padded = pad_sequence(blocks, batch_first=True)
+    counts = torch.tensor([b.shape[0] for b in blocks], device=padded.device)
+    mask = torch.arange(padded.shape[1], device=padded.device)[None, :] < counts[:, None]
+    return padded, mask
+
+
+def masked_mean_l2(K: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """S = L2(sum of the valid rows / max(n_c, 1)) per chunk."""
+    m = mask.to(K.dtype)
+    total = torch.einsum("cnd,cn->cd", K, m)
+    return l2(total / m.sum(1, keepdim=True).clamp_min(1))
 
 
 class Library:
@@ -44,46 +72,37 @@ class Library:
             raise ValueError("Library needs at least one chunk")
         depths = sorted(float(r) for r in depths)
         if len(reader_layers) != len(depths):
-            raise ValueError(f"{len(reader_layers)} reader layers for {len(depths)} depths")
+            raise ValueError(f"got {len(reader_layers)} reader layers for {len(depths)} depths")
+        keys = [_get(c, "K") for c in chunks]
+        vals = [_get(c, "V") for c in chunks]
+        untied = any(v is not None and v is not k for k, v in zip(keys, vals))
         self.depths = depths
         self.reader_layers = list(reader_layers)
         self.rho_of = dict(zip(self.reader_layers, depths))
-        Ks = [_field(c, "K") for c in chunks]
-        Vs = [_field(c, "V") for c in chunks]
-        untied = any(v is not None and v is not k for v, k in zip(Vs, Ks))
-        if meta is None:
-            meta = []
-            for c in chunks:
-                m = getattr(c, "meta", None)
-                if m is None and isinstance(c, dict):
-                    m = {k: v for k, v in c.items() if k not in ("K", "V")}
-                meta.append(dict(m or {}))
-        self.chunk_meta = meta
+        self.chunk_meta = list(meta) if meta is not None else [_meta_of(c) for c in chunks]
+        self.center = center
         self.K, self.mask, self.S = {}, {}, {}
         self.V = {} if untied else None
+
+        def rows_at(src, rho):
+            return [x[rho_key(x, rho)].to(device=device, dtype=dtype) for x in src]
+
         for li, rho in self.rho_of.items():
-            rows = [k[rho_key(k, rho)].to(device=device, dtype=dtype) for k in Ks]
-            n = torch.tensor([r.shape[0] for r in rows], device=device)
-            Kt = pad_sequence(rows, batch_first=True)
-            M = torch.arange(Kt.shape[1], device=device).view(1, -1) < n.view(-1, 1)
+            kb = rows_at(keys, rho)
             if center is not None:   # a centre dict must cover every depth (KeyError otherwise)
                 mu = center[rho_key(center, rho)].to(device=device, dtype=dtype)
-                Kt = torch.where(M.unsqueeze(-1), l2(Kt - mu), torch.zeros_like(Kt))
-            self.K[li], self.mask[li] = Kt, M
-            if untied:
-                vrows = [(v if v is not None else k) for v, k in zip(Vs, Ks)]
-                self.V[li] = pad_sequence([v[rho_key(v, rho)].to(device=device, dtype=dtype) for v in vrows],
-                                          batch_first=True)
-        self.center = center
+                kb = [l2(b - mu) for b in kb]
+            vb = rows_at([v if v is not None else k for k, v in zip(keys, vals)], rho) if untied else None
+            self._set_layer(li, kb, vb)
         self._summaries()
 
+    def _set_layer(self, li: int, key_blocks: list, value_blocks: list | None) -> None:
+        self.K[li], self.mask[li] = _assemble(key_blocks)
+        if value_blocks is not None:
+            self.V[li] = _assemble(value_blocks)[0]
+
     def _summaries(self) -> None:
-        self.S = {}
-        for li, Kt in self.K.items():
-            M = self.mask[li]
-            tot = (Kt * M.unsqueeze(-1).to(Kt.dtype)).sum(1)
-            cnt = M.sum(1, keepdim=True).clamp_min(1).to(Kt.dtype)
-            self.S[li] = l2(tot / cnt)
+        self.S = {li: masked_mean_l2(self.K[li], self.mask[li]) for li in self.K}
         self._paged = {}
 
     # ------------------------------------------------------------------ properties
@@ -105,51 +124,47 @@ class Library:
     # ------------------------------------------------------------------ ops
     def to(self, device=None, dtype=None) -> "Library":
         """Move / cast in place (the mask stays bool); returns self."""
-        for li in list(self.K):
-            self.K[li] = self.K[li].to(device=device, dtype=dtype)
-            self.S[li] = self.S[li].to(device=device, dtype=dtype)
+        for table in (self.K, self.S) + ((self.V,) if self.V is not None else ()):
+            for li in table:
+                table[li] = table[li].to(device=device, dtype=dtype)
+        for li in self.mask:
             self.mask[li] = self.mask[li].to(device=device)
-            if self.V is not None:
-                self.V[li] = self.V[li].to(device=device, dtype=dtype)
         self._paged = {}
         return self
 
     def subset(self, idx) -> "Library":
-        """The Library of chunks `idx` alone (re-trimmed to their longest chunk, S recomputed)."""
-        idx = [int(i) for i in (idx if hasattr(idx, "__iter__") else [idx])]
-        if not idx:
-            raise ValueError("empty subset")
-        new = object.__new__(Library)
-        new.depths, new.reader_layers, new.rho_of = self.depths, self.reader_layers, dict(self.rho_of)
-        new.center = getattr(self, "center", None)
-        new.chunk_meta = [self.chunk_meta[i] for i in idx]
-        new.K, new.mask = {}, {}
-        new.V = {} if self.V is not None else None
+        """The Library of chunks `idx` alone: their valid rows reassembled (trimmed to the longest
+        of them) and their summaries recomputed."""
+        picks = [int(i) for i in idx] if hasattr(idx, "__iter__") else [int(idx)]
+        if not picks:
+            raise ValueError("subset needs at least one chunk index")
+        out = Library.__new__(type(self))
+        out.depths, out.reader_layers, out.rho_of = self.depths, self.reader_layers, dict(self.rho_of)
+        out.center = self.center
+        out.chunk_meta = [self.chunk_meta[i] for i in picks]
+        out.K, out.mask, out.S = {}, {}, {}
+        out.V = {} if self.V is not None else None
         for li in self.K:
-            sel = torch.tensor(idx, device=self.K[li].device)
-            M = self.mask[li].index_select(0, sel)
-            n = int(M.sum(-1).max())
-            new.mask[li] = M[:, :n].clone()
-            new.K[li] = self.K[li].index_select(0, sel)[:, :n].clone()
-            if new.V is not None:
-                new.V[li] = self.V[li].index_select(0, sel)[:, :n].clone()
-        new._summaries()
-        return new
+            n = self.n_valid(li).tolist()
+            kb = [self.K[li][i, :n[i]] for i in picks]
+            vb = [self.V[li][i, :n[i]] for i in picks] if self.V is not None else None
+            out._set_layer(li, kb, vb)
+        out._summaries()
+        return out
 
     @staticmethod
     def from_doc_cache(cache: dict, reader_model, depths=None, device=None, dtype=torch.float32,
                        center: dict | None = None) -> "Library":
         """From a document cache dict {"depths", "chunks": [{"K": {rho: rows}, "start", "n_tokens"}],
-        "doc_id", "encoder"} for the given reader model."""
-        depths = sorted(float(r) for r in (depths or cache["depths"]))
-        rmap = rho_layer_map(reader_model, depths)
+        "doc_id", "encoder"} for the given reader model (depth rho -> its reader layer)."""
+        use = sorted(float(r) for r in (depths if depths else cache["depths"]))
+        layer_of = rho_layer_map(reader_model, use)
         if device is None:
-            device = reader_model.device if hasattr(reader_model, "device") else "cpu"
-        meta = [{"doc_id": cache.get("doc_id", ""), "start": int(c.get("start", 0)),
-                 "n_tokens": int(c.get("n_tokens", 0)), "encoder": cache.get("encoder", "")}
-                for c in cache["chunks"]]
-        return Library(cache["chunks"], [rmap[r] for r in depths], depths, device, dtype, meta=meta,
-                       center=center)
+            device = getattr(reader_model, "device", "cpu")
+        doc, enc = cache.get("doc_id", ""), cache.get("encoder", "")
+        meta = [dict(doc_id=doc, start=int(ch.get("start", 0)), n_tokens=int(ch.get("n_tokens", 0)), encoder=enc)
+                for ch in cache["chunks"]]
+        return Library(cache["chunks"], [layer_of[r] for r in use], use, device, dtype, meta=meta, center=center)
 
     # ------------------------------------------------------------------ device pool
     def paged(self, li: int, device):
@@ -161,13 +176,11 @@ class Library:
         if device.type == "cuda" and device.index is None:
             device = torch.device("cuda", torch.cuda.current_device())
         key = (li, device)
-        pl = self._paged.get(key)
-        if pl is None:
+        if key not in self._paged:
             V = self.V[li] if self.V is not None else None
-            pl = PagedLibrary.from_padded(self.K[li], self.mask[li], self.S[li].float(), device=device,
-                                          V=V, pad_to=PAGE_ALIGN)
-            self._paged[key] = pl
-        return pl
+            self._paged[key] = PagedLibrary.from_padded(self.K[li], self.mask[li], self.S[li].float(),
+                                                        device=device, V=V, pad_to=PAGE_ALIGN)
+        return self._paged[key]
 
 
-__all__ = ["Library", "l2", "PAGE_ALIGN"]
+__all__ = ["Library", "l2", "masked_mean_l2", "PAGE_ALIGN"]

@@ -12,8 +12,7 @@ import torch
 
 import oracle as O
 from kv_skill_v2_amd.depth import DEPTHS, DepthCollisionError, injection_layers, rho_layer_map
-from kv_skill_v2_amd.interface import (EncoderLens, ModelInterface, count_params, interface_param_groups,
-                                       load_interface, make_interface, save_interface)
+from kv_skill_v2_amd.interface import ModelInterface, load_interface, make_interface, save_interface
 from kv_skill_v2_amd.library import Library
 from kv_skill_v2_amd.selector import LayerSelector, rms_norm
 from tiny import TinyLM, skill_rho
@@ -292,14 +291,10 @@ def test_make_interface_noop_and_shapes():
     with pytest.raises(ValueError):
         make_interface(40, 24, [2, 2, 4])
     low = make_interface(40, 24, LAYERS8, rank=8)
-    assert count_params(low)["A"] == 40 * 8 + 8 * 24
-
-
-def test_encoder_lens():
-    lens = EncoderLens(24, 16)
-    assert lens(torch.randn(3, 5, 24)).shape == (3, 5, 16)
-    with pytest.raises(ValueError):
-        lens(torch.randn(3, 16))
+    assert sum(p.numel() for p in low.A.parameters()) == 40 * 8 + 8 * 24
+    hn2 = rms_norm(torch.randn(3, 40))
+    q = low.query(hn2)
+    assert torch.allclose(q, O.query(hn2, low.A[1].weight @ low.A[0].weight), atol=1e-6)
 
 
 def test_save_load_roundtrip(tmp_path):
@@ -318,17 +313,6 @@ def test_save_load_roundtrip(tmp_path):
     assert extra == {"step": 7}
     with pytest.raises(ValueError):
         load_interface(path, 40, 32, LAYERS8)
-
-
-def test_param_groups():
-    itf = make_interface(40, 24, LAYERS8)
-    sel = LayerSelector(40, [1, 3], k=1)
-    groups = interface_param_groups(itf, 1e-3, selector=sel, selector_lr=5e-3)
-    ids = [id(p) for g in groups for p in g["params"]]
-    assert len(ids) == len(set(ids)) == len(list(itf.parameters())) + len(list(sel.parameters()))
-    assert groups[-1]["name"] == "selector" and groups[-1]["lr"] == 5e-3
-    ga = interface_param_groups(itf, 1e-3, lr_A=1e-2)
-    assert [g["name"] for g in ga] == ["interface", "interface_A"] and ga[1]["lr"] == 1e-2
 
 
 def test_decode_reader_auto_chunk():

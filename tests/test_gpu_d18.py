@@ -148,9 +148,9 @@ def test_lib_read_matches_oracle_and_incremental(dev):
         one = d18.lib_read(itf, li, x, ops_[1:2])
         f1 = d18.lib_read(itf, li, x, ops_, force=1)
         assert float((one["y"] - f1["y"]).abs().max()) < 1e-5
-        qr = d18.question_route({li: (got["r"], got["rmax"], got["n"])}, slice(2, 5))
-        assert torch.allclose(qr["lse"] - qr["lse_norm"], got["n"].log(), atol=1e-5)
-        assert bool((qr["max"] <= qr["lse"] + 1e-5).all())
+        # the route statistics: logsumexp bounds the max score, and exceeds it by at most log N_d
+        assert bool((got["rmax"] <= got["r"] + 1e-5).all())
+        assert bool((got["r"] - got["rmax"] <= got["n"].log().view(1, 1, 1, -1) + 1e-5).all())
 
 
 def test_lib_reader_patch_matches_oracle_patch(dev, monkeypatch):
