@@ -638,8 +638,8 @@ def main():
     read_temp, route_temp = 12.0, 10.0
 
     def step():
-        _, idx, wsel = ops.route_topk(q, lib, qg, top_k=top_k, route_temp=route_temp)
-        return ops.library_read_decode(q, lib, idx, wsel, qg, read_temp=read_temp, nsplit=args.nsplit)
+        return ops.route_read_decode(q, lib, qg, top_k=top_k, route_temp=route_temp, read_temp=read_temp,
+                                     nsplit=args.nsplit)[3]
 
     # Algorithmic bytes of the read: each routed page's valid slot rows once (K = V tied), the
     # query rows and the output rows.  Routing is deterministic, so read it once off the clock.
@@ -655,20 +655,20 @@ def main():
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    # Eager steps with HIP events around the read launch: the read kernel's own duration (the
-    # roofline figure) and the eager step time.
+    # Eager steps with HIP events around the whole routed read on its stream (the q . S dots, the
+    # read kernel with the top-k in its prologue, and the merge): the roofline figure counts the
+    # step's algorithmic bytes (routed pages, S, q and r) over that span, and the eager step time.
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(args.steps)]
     t0 = time.perf_counter()
     for i in range(args.steps):
-        _, idx, wsel = ops.route_topk(q, lib, qg, top_k=top_k, route_temp=route_temp)
         ev[i][0].record(stream)
-        ops.library_read_decode(q, lib, idx, wsel, qg, read_temp=read_temp, nsplit=args.nsplit)
+        step()
         ev[i][1].record(stream)
     torch.cuda.synchronize()
     ms_eager = (time.perf_counter() - t0) * 1e3 / args.steps
     read_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
-    achieved = read_bytes / (read_ms * 1e-3) / 1e9
+    achieved = (read_bytes + route_bytes) / (read_ms * 1e-3) / 1e9
 
     # The step (routing + read, 4 launches) captured once in a HIP graph and replayed: the host
     # launch overhead between the kernels (measured ~11 us per eager step) goes away.  Every
@@ -737,13 +737,14 @@ def main():
                    "route_temp": route_temp, "accumulate": "fp32", "page_table": "seeded shuffle",
                    "nsplit": args.nsplit or ops.default_nsplit(B * idx_h.shape[1], P.pages.shape[1]),
                    "timing": timing, "ms_per_step_eager": ms_eager, "ms_per_step_graph": ms_graph},
-        "roofline": {"bound": "hbm", "kernel": "decode_read_kernel (+ merge_kernel when two-pass)",
+        "roofline": {"bound": "hbm",
+                     "kernel": "route_dots_kernel + decode_read_kernel (top-k in its prologue) + merge_kernel",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic["bytes_per_launch"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
-                     "algorithmic_bytes": read_bytes, "avg_launch_ms": read_ms,
-                     "routed_slots": routed_slots, "route_bytes": route_bytes},
+                     "algorithmic_bytes": read_bytes + route_bytes, "avg_launch_ms": read_ms,
+                     "routed_slots": routed_slots, "read_bytes": read_bytes, "route_bytes": route_bytes},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

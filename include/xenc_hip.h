@@ -106,6 +106,25 @@ int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
                              void* workspace, size_t workspace_bytes, int max_rows, void* stream);
 
 /*
+ * Routing and the decode read in one call: xenc_route_topk's outputs (w_dense, idx, w_sel) and
+ * xenc_library_read_decode's r, same arguments as the two calls together, same results bit for
+ * bit.  When every library has at most 64 chunks (ldw <= 64) and the rows do not share libraries
+ * (the page-grouped order needs the routed chunks first), the top-k + softmax runs in the read
+ * kernel's prologue instead of a kernel of its own: the q . S dots go to the workspace first, each
+ * read workgroup ranks its row's dots itself, and the workgroup of the row's first routed slot
+ * writes the dense weights.  Otherwise it makes the two calls.  Workspace as for
+ * xenc_library_read_decode.
+ * Replaces LibraryInjector.route and the read of _branch (xenc/injector.py:220-265) for decode rows.
+ */
+int xenc_route_read_decode(const float* q, long long ldq, int M, int d, const float* S,
+                           const void* pages, int slots_per_page, long long page_stride,
+                           const int* chunk_page, const int* chunk_nvalid, const int* chunk_ptr,
+                           const int* q_group, int G, int top_k, float route_temp,
+                           float* w_dense, long long ldw, int* idx, float* w_sel, int kk,
+                           float read_temp, int softmax, int nsplit, float* r, long long ldr,
+                           void* workspace, size_t workspace_bytes, int max_rows, void* stream);
+
+/*
  * Allocation-free variant of xenc_library_read_decode: the same read, the same arguments without
  * the workspace.  Its partials, page order and arrival counters live in a file-scope device array
  * of XENC_DECODE_SCRATCH_BYTES bytes (64 MiB) that each GPU the library runs on holds until the

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _lock = threading.Lock()
 _lib = None
@@ -42,6 +42,15 @@ SIGNATURES = {
         c_void_p, c_longlong, c_int, c_int,          # q, ldq, M, d
         c_void_p, c_int, c_longlong,                 # pages, slots_per_page, page_stride
         c_void_p, c_void_p, c_void_p, c_void_p, c_int,  # chunk_page, chunk_nvalid, chunk_ptr, q_group, G
+        c_void_p, c_void_p, c_int,                   # idx, w_sel, kk
+        c_float, c_int, c_int,                       # read_temp, softmax, nsplit
+        c_void_p, c_longlong,                        # r, ldr
+        c_void_p, c_size_t, c_int, c_void_p]),       # workspace, bytes, max_rows, stream
+    "xenc_route_read_decode": (c_int, [
+        c_void_p, c_longlong, c_int, c_int, c_void_p,  # q, ldq, M, d, S
+        c_void_p, c_int, c_longlong,                 # pages, slots_per_page, page_stride
+        c_void_p, c_void_p, c_void_p, c_void_p, c_int,  # chunk_page, chunk_nvalid, chunk_ptr, q_group, G
+        c_int, c_float, c_void_p, c_longlong,        # top_k, route_temp, w_dense, ldw
         c_void_p, c_void_p, c_int,                   # idx, w_sel, kk
         c_float, c_int, c_int,                       # read_temp, softmax, nsplit
         c_void_p, c_longlong,                        # r, ldr

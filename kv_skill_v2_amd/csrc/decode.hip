@@ -30,17 +30,29 @@
 #include <algorithm>
 #include <mutex>
 
-#include "xenc_common.h"
+#include "route_select.h"
 
-// Waves per workgroup and slots per wave step (for d <= 2048 / above).  Chosen by measurement.
-#ifndef XENC_DECODE_NW
-#define XENC_DECODE_NW 8
+// Waves per workgroup and slots per wave step (for d <= 2048 / above).  Chosen by measurement:
+// large two-pass launches take NW_STREAM waves (the kernel holds 179 VGPRs, two waves per SIMD,
+// so two 4-wave workgroups share a CU and one's prologue / tail overlaps the other's streaming:
+// B = 64 batched decode 0.197 -> 0.188 ms per step); small launches (the in-kernel merge) and
+// page-grouped runs keep NW_WIDE (one row x 4 pages: 36.5 against 38.4 us).
+#ifndef XENC_DECODE_NW_STREAM
+#define XENC_DECODE_NW_STREAM 4
+#endif
+#ifndef XENC_DECODE_NW_WIDE
+#define XENC_DECODE_NW_WIDE 8
 #endif
 #ifndef XENC_DECODE_SPT
 #define XENC_DECODE_SPT 4
 #endif
 #ifndef XENC_DECODE_SPT_WIDE
 #define XENC_DECODE_SPT_WIDE 2
+#endif
+// Minimum waves per SIMD the compiler must fit the read kernel's registers for (4: two 8-wave
+// workgroups per CU).
+#ifndef XENC_DECODE_MIN_WAVES
+#define XENC_DECODE_MIN_WAVES 1
 #endif
 // Measured and not kept (B = 64 batched decode, same box): two register tiles per wave with the
 // next one loading while the current one is consumed (184-185 us, no change), and score dots with
@@ -63,6 +75,42 @@ struct DecodeWorkspace {
   float2* part_ml;  // [units]    (max in log2 units, sum) per partial; sum 0 = empty
   float* part_acc;  // [units, d] un-normalised value sums
 };
+
+// Routing folded into the read (dots != nullptr): dots [M, ldw] (in the workspace) hold the raw
+// q . S dots of every row's chunks (route_dots_kernel), ldw <= 64.  Each workgroup ranks its row's
+// chunks itself (select_topk_softmax_rank, the routing kernels' own selection) to find the chunk of
+// its routed slot; split 0 of each slot publishes idx / w_sel, and the workgroup of (row, slot 0,
+// split 0) writes the row's dense weights into w_dense.
+struct RouteFuse {
+  const float* dots;
+  float* w_dense;
+  int ldw;
+  int top_k;
+  float route_temp;
+};
+
+// LDS of the fused selection: the row's dots (reused for the exponentials), the 64-bit keys,
+// the dense weights and the kept (index, weight) list by rank.
+struct SelectLds {
+  float x[kWave];
+  unsigned long long keys[kWave];
+  float w[kWave];
+  int idx[kWave];
+  float sel[kWave];
+};
+
+// Wave-level: the top-k + softmax of row m (library g) into sl (dense weights zeroed first).
+__device__ __forceinline__ void select_row(const RouteFuse& rf, int m, int C, int kk, SelectLds& sl, int lane) {
+  sl.w[lane] = 0.f;
+  if (lane < C) sl.x[lane] = rf.dots[(long long)m * rf.ldw + lane];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  select_topk_softmax_rank(sl.x, sl.keys, C, rf.top_k, kk, rf.route_temp, sl.w, sl.idx, sl.sel, lane);
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // Merge the k*nsplit partials of query m into r[m] (run by merge_kernel, or by the last
 // workgroup of the query in the in-kernel merge).
@@ -252,17 +300,19 @@ __device__ __forceinline__ void consume_tile(u32x4 (&kv)[SPT][CB], const TileCtx
 }
 
 template <int CB, int SPT, int NW>
-__global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
+__global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_kernel(
     const float* __restrict__ q, long long ldq, int d, const _Float16* __restrict__ pages,
     long long page_stride, int slots_per_page, const int* __restrict__ chunk_page,
     const int* __restrict__ chunk_nvalid, const int* __restrict__ chunk_ptr,
-    const int* __restrict__ q_group, int G, const int* __restrict__ idx,
-    const float* __restrict__ w_sel, int kk, int nsplit, int split_slots, float scale2,
-    int softmax, float* __restrict__ r, long long ldr, DecodeWorkspace ws, int fused_merge,
-    int grouped) {
+    const int* __restrict__ q_group, int G, int* idx, float* w_sel, int kk, int nsplit,
+    int split_slots, float scale2, int softmax, float* __restrict__ r, long long ldr,
+    DecodeWorkspace ws, int fused_merge, int grouped, RouteFuse rf) {
+  // idx / w_sel: read (routed in advance) or written by split 0 of each slot (routing folded in),
+  // so neither is declared read-only.
   extern __shared__ float red[];  // [NW/2][d] wave-merge tree; reused by the merge
   __shared__ float wml[NW][2];
   __shared__ int is_last;
+  __shared__ SelectLds sl[NW];   // one per wave (routing folded into the read)
 
   // Launch position -> logical unit: in page-grouped runs the XCD-major position indexes the
   // page-ranked entries; otherwise the unit is the block index.
@@ -275,15 +325,38 @@ __global__ __launch_bounds__(NW* kWave) void decode_read_kernel(
   // Wave index as a provably uniform value, so row offsets stay in SGPRs (buffer soffset).
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
 
-  const int cl = idx[mj];
   const int g = min(max(q_group[m], 0), G - 1);
   const int cbeg = chunk_ptr[g];
+  const int C_g = chunk_ptr[g + 1] - cbeg;
   int nv = 0;
   long long pbase = 0;
-  if (cl >= 0 && cl < chunk_ptr[g + 1] - cbeg) {  // out-of-range entries read nothing
-    const int gc = cbeg + cl;
-    nv = min(chunk_nvalid[gc], slots_per_page);
-    pbase = (long long)chunk_page[gc] * page_stride;
+  if (rf.dots) {  // uniform: routing folded into the read
+    // Every wave ranks the row's chunks itself (its own LDS, no workgroup barrier) while the
+    // valid counts and pages of all the row's chunks load, one per lane; the routed chunk's are
+    // then taken from its lane.
+    const int j = mj - m * kk;
+    const int C = min(C_g, rf.ldw);
+    const int lnv = lane < C ? chunk_nvalid[cbeg + lane] : 0;
+    const int lpg = lane < C ? chunk_page[cbeg + lane] : 0;
+    select_row(rf, m, C, kk, sl[wv], lane);
+    const int cl = __builtin_amdgcn_readfirstlane(sl[wv].idx[j]);
+    if (cl >= 0 && cl < C) {
+      nv = min(__builtin_amdgcn_readlane(lnv, cl), slots_per_page);
+      pbase = (long long)__builtin_amdgcn_readlane(lpg, cl) * page_stride;
+    }
+    if (s == 0 && threadIdx.x == 0) {   // thread 0 stores: its release below covers them
+      idx[mj] = cl;
+      w_sel[mj] = sl[0].sel[j];
+    }
+    if (s == 0 && j == 0 && wv == 0)
+      for (int c = lane; c < rf.ldw; c += kWave) rf.w_dense[(long long)m * rf.ldw + c] = c < C ? sl[0].w[c] : 0.f;
+  } else {
+    const int cl = idx[mj];
+    if (cl >= 0 && cl < C_g) {  // out-of-range entries read nothing
+      const int gc = cbeg + cl;
+      nv = min(chunk_nvalid[gc], slots_per_page);
+      pbase = (long long)chunk_page[gc] * page_stride;
+    }
   }
   const int s0 = s * split_slots;
   const int s1 = min(nv, s0 + split_slots);
@@ -487,8 +560,10 @@ __global__ void fill_zero_kernel(int* p, int n) {
 
 static size_t host_align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Workspace: [counters: max_rows ints | page order: M * kk ints | (m, l) per partial | acc per
-// partial], each region 256-B aligned.
+// Workspace: [counters: max_rows ints | page order / routing dots: M * max(kk, 64) words |
+// (m, l) per partial | acc per partial], each region 256-B aligned.  The second region holds the
+// page order of page-grouped runs, or the q . S dots when the routing is folded into the read
+// (never both in one call).
 // The counter region depends only on the capacity max_rows, never on the call's row count, so
 // counters zeroed once stay in place (and zero) whatever sizes later calls use.
 static DecodeWorkspace carve(void* base, int max_rows, int M, int kk, int nsplit) {
@@ -498,26 +573,26 @@ static DecodeWorkspace carve(void* base, int max_rows, int M, int kk, int nsplit
   ws.counters = reinterpret_cast<int*>(p);
   p += host_align256((size_t)max_rows * sizeof(int));
   ws.order = reinterpret_cast<int*>(p);
-  p += host_align256((size_t)M * kk * sizeof(int));
+  p += host_align256((size_t)M * std::max(kk, kWave) * sizeof(int));
   ws.part_ml = reinterpret_cast<float2*>(p);
   p += host_align256(units * sizeof(float2));
   ws.part_acc = reinterpret_cast<float*>(p);
   return ws;
 }
 
-template <int CB>
+template <int CB, int NW>
 static void launch_read(dim3 grid, size_t lds, hipStream_t st, const float* q, long long ldq,
                         int d, const _Float16* pages, long long page_stride, int spp,
                         const int* chunk_page, const int* chunk_nvalid, const int* chunk_ptr,
                         const int* q_group, int G, const int* idx, const float* w_sel, int kk,
                         int nsplit, int split_slots, float scale2, int softmax, float* r,
-                        long long ldr, const DecodeWorkspace& ws, int fused_merge, int grouped) {
-  constexpr int NW = XENC_DECODE_NW;
+                        long long ldr, const DecodeWorkspace& ws, int fused_merge, int grouped,
+                        const RouteFuse& rf) {
   constexpr int SPT = CB <= 4 ? XENC_DECODE_SPT : (CB == 5 ? XENC_DECODE_SPT_WIDE : 1);
   hipLaunchKernelGGL((decode_read_kernel<CB, SPT, NW>), grid, dim3(NW * kWave), lds, st, q, ldq,
                      d, pages, page_stride, spp, chunk_page, chunk_nvalid, chunk_ptr, q_group, G,
-                     idx, w_sel, kk, nsplit, split_slots, scale2, softmax, r, ldr, ws, fused_merge,
-                     grouped);
+                     const_cast<int*>(idx), const_cast<float*>(w_sel), kk, nsplit, split_slots, scale2,
+                     softmax, r, ldr, ws, fused_merge, grouped, rf);
 }
 
 // Launches of at least this many workgroups merge in a second kernel; smaller ones (few query
@@ -528,14 +603,15 @@ constexpr long long kTwoPassUnits = 256;
 
 using namespace xenc;
 
-static size_t workspace_need(int max_rows, long long entries, long long units, int d) {
-  return host_align256((size_t)max_rows * sizeof(int)) + host_align256(entries * sizeof(int)) +
+static size_t workspace_need(int max_rows, long long rows, int kk, long long units, int d) {
+  return host_align256((size_t)max_rows * sizeof(int)) +
+         host_align256((size_t)rows * std::max(kk, kWave) * sizeof(int)) +
          host_align256(units * sizeof(float2)) + host_align256(units * d * sizeof(float));
 }
 
 extern "C" size_t xenc_decode_workspace_bytes(int max_rows, int kk, int nsplit, int d) {
   if (max_rows <= 0 || kk <= 0 || nsplit <= 0 || d <= 0) return 0;
-  return workspace_need(max_rows, (long long)max_rows * kk, (long long)max_rows * kk * nsplit, d);
+  return workspace_need(max_rows, max_rows, kk, (long long)max_rows * kk * nsplit, d);
 }
 
 extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_bytes, int max_rows,
@@ -557,7 +633,7 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
                        const int* chunk_nvalid, const int* chunk_ptr, const int* q_group, int G,
                        const int* idx, const float* w_sel, int kk, float read_temp, int softmax,
                        int nsplit, float* r, long long ldr, void* workspace, size_t workspace_bytes,
-                       int max_rows, int short_code, hipStream_t st) {
+                       int max_rows, int short_code, hipStream_t st, const RouteFuse& rf = RouteFuse{}) {
   if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || slots_per_page <= 0) return XENC_EINVAL;
   if (M > max_rows) return short_code;
   if (d % 8 != 0 || d > 8 * 512) return XENC_EINVAL;
@@ -573,17 +649,17 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
     return XENC_EALIGN;
   const long long units = (long long)M * kk * nsplit;
   if (units > 0x7fffffffLL) return XENC_EINVAL;
-  if (workspace_bytes < workspace_need(max_rows, (long long)M * kk, units, d)) return short_code;
-  // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
-  const size_t lds =
-      std::max((size_t)std::max(XENC_DECODE_NW / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
-  if (lds > 64 * 1024) return XENC_EINVAL;
-
-  const DecodeWorkspace ws = carve(workspace, max_rows, M, kk, nsplit);
+  if (workspace_bytes < workspace_need(max_rows, M, kk, units, d)) return short_code;
   const int fused = units < kTwoPassUnits ? 1 : 0;
   // Page-grouped runs when rows share libraries and there are enough entries to matter.
   const long long entries = (long long)M * kk;
-  const int grouped = (M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
+  const int grouped = (!rf.dots && M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
+  const int nw = (fused || grouped) ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
+  // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
+  const size_t lds = std::max((size_t)std::max(nw / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
+  if (lds > 64 * 1024) return XENC_EINVAL;
+
+  const DecodeWorkspace ws = carve(workspace, max_rows, M, kk, nsplit);
   const int split_slots = (slots_per_page + nsplit - 1) / nsplit;
   const float scale2 = read_temp * kLog2e;
   const _Float16* pg = static_cast<const _Float16*>(pages);
@@ -594,11 +670,18 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
   const dim3 grid((unsigned)units);
   const int cb = (d + 511) / 512;
   switch (cb) {
-#define XENC_CASE(N)                                                                           \
-  case N:                                                                                      \
-    launch_read<N>(grid, lds, st, q, ldq, d, pg, page_stride, slots_per_page, chunk_page,      \
-                   chunk_nvalid, chunk_ptr, q_group, G, idx, w_sel, kk, nsplit, split_slots,   \
-                   scale2, softmax, r, ldr, ws, fused, grouped);                               \
+#define XENC_CASE(N)                                                                              \
+  case N:                                                                                         \
+    if (nw == XENC_DECODE_NW_STREAM)                                                              \
+      launch_read<N, XENC_DECODE_NW_STREAM>(grid, lds, st, q, ldq, d, pg, page_stride,            \
+                                            slots_per_page, chunk_page, chunk_nvalid, chunk_ptr,  \
+                                            q_group, G, idx, w_sel, kk, nsplit, split_slots,      \
+                                            scale2, softmax, r, ldr, ws, fused, grouped, rf);     \
+    else                                                                                          \
+      launch_read<N, XENC_DECODE_NW_WIDE>(grid, lds, st, q, ldq, d, pg, page_stride,              \
+                                          slots_per_page, chunk_page, chunk_nvalid, chunk_ptr,    \
+                                          q_group, G, idx, w_sel, kk, nsplit, split_slots,        \
+                                          scale2, softmax, r, ldr, ws, fused, grouped, rf);       \
     break;
     XENC_CASE(1) XENC_CASE(2) XENC_CASE(3) XENC_CASE(4)
     XENC_CASE(5) XENC_CASE(6) XENC_CASE(7) XENC_CASE(8)
@@ -672,7 +755,7 @@ extern "C" int xenc_library_read_decode_noalloc(const float* q, long long ldq, i
   if (M > kScratchRows) return XENC_ESCRATCH;
   if (M == 0) return XENC_OK;
   const long long units = (long long)M * kk * nsplit;
-  if (workspace_need(kScratchRows, (long long)M * kk, units, d) > (size_t)XENC_DECODE_SCRATCH_BYTES)
+  if (workspace_need(kScratchRows, M, kk, units, d) > (size_t)XENC_DECODE_SCRATCH_BYTES)
     return XENC_ESCRATCH;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   void* ws = nullptr;
@@ -681,4 +764,46 @@ extern "C" int xenc_library_read_decode_noalloc(const float* q, long long ldq, i
   return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid,
                      chunk_ptr, q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr, ws,
                      (size_t)XENC_DECODE_SCRATCH_BYTES, kScratchRows, XENC_ESCRATCH, st);
+}
+
+// ---------------------------------------------------------------- routing + read in one call
+extern "C" int xenc_route_read_decode(const float* q, long long ldq, int M, int d, const float* S,
+                                      const void* pages, int slots_per_page, long long page_stride,
+                                      const int* chunk_page, const int* chunk_nvalid,
+                                      const int* chunk_ptr, const int* q_group, int G, int top_k,
+                                      float route_temp, float* w_dense, long long ldw, int* idx,
+                                      float* w_sel, int kk, float read_temp, int softmax, int nsplit,
+                                      float* r, long long ldr, void* workspace,
+                                      size_t workspace_bytes, int max_rows, void* stream) {
+  if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || ldw <= 0) return XENC_EINVAL;
+  if (M == 0) return XENC_OK;
+  if (!S || !w_dense || !idx || !w_sel) return XENC_ENULL;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const long long entries = (long long)M * kk;
+  // The read ranks a row's chunks itself when a library has at most 64 and the rows do not share
+  // libraries enough for the page-grouped order (which needs the routed chunks before the read).
+  const bool fold = ldw <= kWave && kk <= kWave && !(M > G && entries >= 128 && entries <= kOrderMax);
+  if (!fold) {
+    const int rc = xenc_route_topk(q, ldq, M, d, S, chunk_ptr, q_group, G, top_k, route_temp, w_dense, ldw,
+                                   idx, w_sel, kk, stream);
+    if (rc != XENC_OK) return rc;
+    return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid,
+                       chunk_ptr, q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr,
+                       workspace, workspace_bytes, max_rows, XENC_EWORKSPACE, st);
+  }
+  if (d % 8 != 0 || d > 4096 || ldq < d || ldq % 4 != 0) return XENC_EINVAL;
+  if (!q || !chunk_ptr || !q_group) return XENC_ENULL;
+  if (!aligned16(q) || !aligned16(S)) return XENC_EALIGN;
+  if (M > max_rows) return XENC_EWORKSPACE;
+  if (nsplit < 1 || nsplit > 64) return XENC_EINVAL;
+  if (!workspace) return XENC_ENULL;
+  if (!aligned16(workspace)) return XENC_EALIGN;
+  if (workspace_bytes < workspace_need(max_rows, M, kk, (long long)M * kk * nsplit, d)) return XENC_EWORKSPACE;
+  float* dots = reinterpret_cast<float*>(carve(workspace, max_rows, M, kk, nsplit).order);
+  const int rc = launch_route_dots(q, ldq, M, d, S, chunk_ptr, q_group, G, dots, (int)ldw, st);
+  if (rc != XENC_OK) return rc;
+  const RouteFuse rf{dots, w_dense, (int)ldw, top_k, route_temp};
+  return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid, chunk_ptr,
+                     q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr, workspace,
+                     workspace_bytes, max_rows, XENC_EWORKSPACE, st, rf);
 }

@@ -12,7 +12,7 @@
 // library stream in parallel instead of one dependent dot at a time.  Each dot is finished
 // with a fixed xor-butterfly: the fp32 summation order is the same on every call.  Dots land in
 // LDS; wave 0 then selects the top_k (a rank count up to 64 chunks, else wave arg-max rounds).
-#include "xenc_common.h"
+#include "route_select.h"
 
 namespace xenc {
 
@@ -89,75 +89,6 @@ __device__ __forceinline__ void select_topk_softmax_reg(const float* dots, int C
     irow[lane] = mine_c;
     selrow[lane] = wr;
     wrow[mine_c] = wr;
-  }
-  for (int r = nsel + lane; r < kk; r += kWave) {
-    irow[r] = -1;
-    selrow[r] = 0.f;
-  }
-}
-
-// Rank variant for C <= 64 (one chunk per lane): the top-k is a rank count instead of k dependent
-// wave arg-max rounds.  Lane l publishes the 64-bit key (order_key(logit_l) << 32) | ~l, logit =
-// dot * route_temp as the reference ranks it: a larger key is a larger logit, or the same logit
-// at a lower index.  Every lane then counts the keys above its own (LDS broadcast reads, one
-// 64-bit compare per chunk, no branches): the ranks are a permutation of [0, C), and the lane of
-// rank r < nsel is round r of the arg-max variant.  The softmax max is the rank-0 logit (the
-// max over the kept lanes when dense); the exponentials go to LDS by position and are summed in
-// position order.  LDS: dots[64] (read, then reused for the exponentials), keys[64] (8-byte
-// aligned, in the taken / order scratch of at least 128 words).
-__device__ __forceinline__ void select_topk_softmax_rank(float* dots, unsigned long long* keys, int C,
-                                                         int top_k, int kk, float route_temp,
-                                                         float* wrow, int* irow, float* selrow,
-                                                         int lane) {
-  const bool dense = top_k <= 0 || top_k >= C;
-  const int nsel = min(dense ? C : top_k, kk);
-  const float x = lane < C ? dots[lane] * route_temp : 0.f;
-  const unsigned long long key =
-      lane < C ? ((unsigned long long)order_key(x) << 32) | (unsigned)~lane : 0ull;
-  const int C8 = (C + 7) & ~7;              // keys past C are 0: below every real key
-  if (lane < C8) keys[lane] = key;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int rank = 0;
-  for (int j = 0; j < C8; j += 8) {
-    unsigned long long kj[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) kj[u] = keys[j + u];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) rank += kj[u] > key ? 1 : 0;
-  }
-  const int pos = dense ? lane : rank;
-  const bool has = lane < C && pos < nsel;
-  // Softmax max: the top logit (position 0) under top-k; the max over the kept lanes when dense.
-  float* es = dots;                          // the kept exponentials by position, 0 up to nsel8
-  if (!dense && pos == 0 && lane < C) es[0] = x;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  const float lmax = dense ? wave_max(has ? x : -INFINITY) : es[0];
-  const float e = has ? expf(x - lmax) : 0.f;
-  const int nsel8 = (nsel + 7) & ~7;
-  __builtin_amdgcn_wave_barrier();           // every lane has read es[0]
-  if (has) es[pos] = e;
-  if (lane >= nsel && lane < nsel8) es[lane] = 0.f;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  float sum = 0.f;                           // position order
-  for (int r = 0; r < nsel8; r += 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = es[r + u];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) sum += v[u];
-  }
-  const float inv = 1.f / sum;
-  if (has) {
-    const float wr = e * inv;
-    irow[pos] = lane;
-    selrow[pos] = wr;
-    wrow[lane] = wr;
   }
   for (int r = nsel + lane; r < kk; r += kWave) {
     irow[r] = -1;
@@ -494,6 +425,25 @@ __global__ __launch_bounds__(8 * kWave) void route_dots_kernel(
   if (lane == 0) w_dense[(long long)m * ldw + c] = a;
 }
 
+int launch_route_dots(const float* q, long long ldq, int M, int d, const float* S, const int* chunk_ptr,
+                      const int* q_group, int G, float* w_dense, int ldw, hipStream_t st) {
+  const dim3 grid(M, (unsigned)((ldw + 7) / 8));
+  switch ((d + 255) / 256) {
+#define XENC_DOTS(N)                                                                             \
+  case N:                                                                                        \
+    hipLaunchKernelGGL(route_dots_kernel<N>, grid, dim3(8 * kWave), 0, st, q, ldq, d, S,         \
+                       chunk_ptr, q_group, G, w_dense, ldw);                                     \
+    break;
+    XENC_DOTS(1) XENC_DOTS(2) XENC_DOTS(3) XENC_DOTS(4) XENC_DOTS(5) XENC_DOTS(6)
+    XENC_DOTS(7) XENC_DOTS(8) XENC_DOTS(9) XENC_DOTS(10) XENC_DOTS(11) XENC_DOTS(12)
+    XENC_DOTS(13) XENC_DOTS(14) XENC_DOTS(15) XENC_DOTS(16)
+#undef XENC_DOTS
+    default:
+      return XENC_EINVAL;
+  }
+  return XENC_OK;
+}
+
 }  // namespace xenc
 
 using namespace xenc;
@@ -516,20 +466,8 @@ extern "C" int xenc_route_topk(const float* q, long long ldq, int M, int d, cons
   // Fewer rows than about one per CU: one wave per (row, chunk), then the wave top-k per row.
   const size_t sel_lds = (size_t)kSelectWaves * 3 * select_lds_stride((int)ldw) * sizeof(float);
   if (M < kSplitRouteRows && sel_lds <= 64 * 1024) {
-    const dim3 grid(M, (unsigned)((ldw + 7) / 8));
-    switch (cb4) {
-#define XENC_DOTS(N)                                                                             \
-  case N:                                                                                        \
-    hipLaunchKernelGGL(route_dots_kernel<N>, grid, dim3(NW * kWave), 0, st, q, ldq, d, S,        \
-                       chunk_ptr, q_group, G, w_dense, (int)ldw);                                \
-    break;
-      XENC_DOTS(1) XENC_DOTS(2) XENC_DOTS(3) XENC_DOTS(4) XENC_DOTS(5) XENC_DOTS(6)
-      XENC_DOTS(7) XENC_DOTS(8) XENC_DOTS(9) XENC_DOTS(10) XENC_DOTS(11) XENC_DOTS(12)
-      XENC_DOTS(13) XENC_DOTS(14) XENC_DOTS(15) XENC_DOTS(16)
-#undef XENC_DOTS
-      default:
-        return XENC_EINVAL;
-    }
+    const int rc = launch_route_dots(q, ldq, M, d, S, chunk_ptr, q_group, G, w_dense, (int)ldw, st);
+    if (rc != XENC_OK) return rc;
     hipLaunchKernelGGL(route_rows_select_kernel, dim3((M + kSelectWaves - 1) / kSelectWaves),
                        dim3(kSelectWaves * kWave), sel_lds, st, M, chunk_ptr, nullptr, q_group, G,
                        top_k, route_temp, w_dense, (int)ldw, idx, w_sel, kk);

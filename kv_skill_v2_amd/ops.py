@@ -393,6 +393,27 @@ def library_read_decode(q: torch.Tensor, lib_: PagedLibrary, idx: torch.Tensor, 
                                        idx, w_sel, float(read_temp), bool(softmax), ns, ws, rows)
 
 
+def route_read_decode(q: torch.Tensor, lib_: PagedLibrary, q_group=None, top_k: int = 0,
+                      route_temp: float = 10.0, read_temp: float = 12.0, softmax: bool = True,
+                      nsplit: int | None = None):
+    """(w [M, cmax], idx [M, kk], w_sel [M, kk], r [M, d]): route_topk and library_read_decode in
+    one operator call (xenc::route_read), equal to them bit for bit.  When every library has at
+    most 64 chunks and the rows do not share libraries, the top-k + softmax runs in the read
+    kernel's prologue: one launch fewer per step (LibraryInjector.route and the read of _branch,
+    xenc/injector.py:220-265)."""
+    q = _query(q, lib_.d)
+    M = q.shape[0]
+    if lib_.values is not None:
+        raise ValueError("the decode kernel reads K = V tied pages; untied values take the prefill path")
+    g = _groups(lib_, M, q_group)
+    kk = lib_.kept(int(top_k))
+    ns = int(nsplit) if nsplit is not None else default_nsplit(M * kk, lib_.slots_per_page)
+    ws, rows = _WORKSPACES.get(q.device, stream_handle(q.device), max(M, 1), kk, ns, lib_.d)
+    return torch.ops.xenc.route_read(q, lib_.S, lib_.pages, lib_.chunk_page, lib_.chunk_nvalid, lib_.chunk_ptr, g,
+                                     int(top_k), float(route_temp), lib_.cmax, kk, float(read_temp), bool(softmax),
+                                     ns, ws, rows)
+
+
 # ---------------------------------------------------------------------------------------------
 # Prefill / registration read (MFMA) and the autograd of routing + read
 ROWS_SCORES, ROWS_READOUT, ROWS_ROUTE_BWD = 128, 128, 16
@@ -922,7 +943,7 @@ def d18_read(qd: torch.Tensor, qo: torch.Tensor, ops, Kown: torch.Tensor, Vown: 
     return {"o": out.reshape(T, Hq * hd), "w": w, "r": r, "rmax": rmax, "n": n}
 
 
-__all__ = ["PagedLibrary", "route_topk", "library_read_decode", "default_nsplit", "RowPlan", "row_plan",
+__all__ = ["PagedLibrary", "route_topk", "library_read_decode", "route_read_decode", "default_nsplit", "RowPlan", "row_plan",
            "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "route_differentiable",
            "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS",
            "build_pages", "write_back", "select_scores", "topk_rows", "gather_library", "selector_weights",

@@ -10,6 +10,8 @@ dispatcher, FakeTensor tracing and torch.compile see ordinary operators:
     xenc::library_read           paged split-K read of the routed pages -> r [M, d]; writes its
                                  workspace (the read of LibraryInjector._branch,
                                  xenc/injector.py:236-265)
+    xenc::route_read             both of the above in one call (the top-k inside the read kernel
+                                 when every library has at most 64 chunks)
     xenc::route_rows             routing of many rows grouped by library (fp32 MFMA tiles), also
                                  emitting the rows as fp16; differentiable in q
     xenc::library_prefill_fwd    the MFMA read of many rows -> (r [M, d], p); differentiable in q
@@ -87,6 +89,35 @@ def library_read(q: Tensor, pages: Tensor, chunk_page: Tensor, chunk_nvalid: Ten
 def _(q, pages, chunk_page, chunk_nvalid, chunk_ptr, q_group, idx, w_sel, read_temp, softmax, nsplit,
       workspace, max_rows):
     return q.new_empty(q.shape[0], pages.shape[-1])
+
+
+# ----------------------------------------------------------------------------- decode routing + read
+@custom_op("xenc::route_read", mutates_args=("workspace",))
+def route_read(q: Tensor, S: Tensor, pages: Tensor, chunk_page: Tensor, chunk_nvalid: Tensor, chunk_ptr: Tensor,
+               q_group: Tensor, top_k: int, route_temp: float, cmax: int, kk: int, read_temp: float, softmax: bool,
+               nsplit: int, workspace: Tensor, max_rows: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """Routing and the read of few rows in one call -> (w [M, cmax], idx [M, kk], w_sel [M, kk], r [M, d]);
+    the top-k runs inside the read kernel when every library has at most 64 chunks."""
+    M, d = q.shape
+    w = torch.empty(M, cmax, dtype=torch.float32, device=q.device)
+    idx = torch.empty(M, kk, dtype=torch.int32, device=q.device)
+    wsel = torch.empty(M, kk, dtype=torch.float32, device=q.device)
+    r = torch.empty(M, pages.shape[-1], dtype=torch.float32, device=q.device)
+    if M:
+        check(lib().xenc_route_read_decode(
+            ptr(q), q.stride(0), M, d, ptr(S), ptr(pages), pages.shape[1], pages.stride(0), ptr(chunk_page),
+            ptr(chunk_nvalid), ptr(chunk_ptr), ptr(q_group), chunk_ptr.numel() - 1, top_k, route_temp, ptr(w),
+            w.stride(0), ptr(idx), ptr(wsel), kk, read_temp, int(softmax), nsplit, ptr(r), r.stride(0),
+            ptr(workspace), workspace.numel(), max_rows, _st(q)), "xenc_route_read_decode")
+    return w, idx, wsel, r
+
+
+@route_read.register_fake
+def _(q, S, pages, chunk_page, chunk_nvalid, chunk_ptr, q_group, top_k, route_temp, cmax, kk, read_temp, softmax,
+      nsplit, workspace, max_rows):
+    M = q.shape[0]
+    return (q.new_empty(M, cmax), q.new_empty(M, kk, dtype=torch.int32), q.new_empty(M, kk),
+            q.new_empty(M, pages.shape[-1]))
 
 
 # ----------------------------------------------------------------------------- many-row routing
@@ -269,5 +300,5 @@ def _(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale, nsplit
     return None
 
 
-__all__ = ["route_topk", "library_read", "route_rows", "route_backward_", "library_prefill_fwd",
+__all__ = ["route_topk", "library_read", "route_read", "route_rows", "route_backward_", "library_prefill_fwd",
            "library_prefill_bwd_dq", "paged_decode_joint", "kept_width"]

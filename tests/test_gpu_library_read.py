@@ -371,3 +371,85 @@ def test_empty_inputs(dev):
     r2, p = ops.prefill_forward(q, torch.zeros(0, 3, device=dev), lib, plan)
     assert r2.shape == (0, 128) and p.shape == (3 * 64 // 8, 0, 8)
     torch.cuda.synchronize()
+
+
+# ------------------------------------------------------------------ routing folded into the read
+FOLD_CASES = [
+    # (chunks per library, rows -> library, d, N, top_k, nsplit): fused prologue unless noted
+    ([12, 30, 64, 8] * 16, list(range(64)), 2048, 512, 8, 1),      # the batched decode's shape, two-pass merge
+    ([16], [0], 2048, 512, 4, None),                                # one query row, in-kernel merge
+    ([5, 9, 3], [2, 0, 1], 256, 128, 0, 2),                        # dense routing
+    ([5, 9, 3], [1, 1, 2], 256, 128, 7, 3),                        # top_k >= C for some libraries
+    ([70, 20], [0, 1], 128, 64, 4, 1),                             # more than 64 chunks: two calls
+    ([40, 33], [0, 1, 0, 1, 0, 1, 0, 1, 0, 1, 0, 1, 0, 1, 0, 1], 256, 64, 8, 1),  # shared libraries: page-grouped
+]
+
+
+@pytest.mark.parametrize("counts,qg,d,N,top_k,nsplit", FOLD_CASES)
+@pytest.mark.parametrize("softmax", [True, False])
+def test_route_read_equals_route_then_read(dev, counts, qg, d, N, top_k, nsplit, softmax):
+    """xenc_route_read_decode (the top-k in the read kernel's prologue when it can) equals
+    xenc_route_topk followed by xenc_library_read_decode bit for bit: w, idx, w_sel and r; and r
+    matches the fp64 oracle."""
+    say("route + read folded", dict(libs=len(counts), rows=len(qg), d=d, N=N, top_k=top_k, nsplit=nsplit,
+                                    softmax=softmax))
+    P = synth.pool(counts, N, d, device=dev, tail_lo=1)
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    q = synth.queries(len(qg), d, device=dev, seed=41)
+    g = torch.tensor(qg, dtype=torch.int32, device=dev)
+    w1, i1, s1 = ops.route_topk(q, lib, g, top_k=top_k)
+    r1 = ops.library_read_decode(q, lib, i1, s1, g, softmax=softmax, nsplit=nsplit)
+    w2, i2, s2, r2 = ops.route_read_decode(q, lib, g, top_k=top_k, softmax=softmax, nsplit=nsplit)
+    torch.cuda.synchronize()
+    assert torch.equal(i1, i2) and torch.equal(s1, s2) and torch.equal(w1, w2)
+    assert torch.equal(r1, r2), float((r1 - r2).abs().max())
+    for m in range(0, len(qg), max(1, len(qg) // 8)):
+        K, M, S = P.library(qg[m])
+        ref, _ = O.branch_read(q[m].double().cpu().view(1, 1, -1), K.double().cpu(), M.cpu(), S.double().cpu(),
+                               top_k=top_k, read_softmax=softmax)
+        assert float((r2[m].double().cpu() - ref.view(-1)).abs().max()) < 2e-3, m
+
+
+def test_route_read_exact_ties_and_graph(dev):
+    """Libraries with duplicated summary keys (exact logit ties: the lower chunk wins, as in the
+    separate routing kernel), then the folded step captured in a HIP graph and replayed for new
+    query rows, equal to eager bit for bit."""
+    say("route + read folded: ties and graph")
+    P = synth.pool([10, 12, 9, 16], 256, 512, device=dev, tail_lo=1)
+    S = P.S.clone()
+    ptr_h = P.chunk_ptr.cpu().tolist()
+    for gi in range(4):
+        a = ptr_h[gi]
+        S[a + 3] = S[a + 1]
+        S[a + 5] = S[a + 1]
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, S.contiguous(),
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    g = torch.arange(4, dtype=torch.int32, device=dev)
+    q_in = S[torch.tensor(ptr_h[:4], device=dev) + 1].clone() * 0.9 + synth.queries(4, 512, device=dev, seed=2) * 0.1
+    q_in = q_in / q_in.norm(dim=-1, keepdim=True)
+    w1, i1, s1 = ops.route_topk(q_in, lib, g, top_k=2)
+    _, i2, s2, _ = ops.route_read_decode(q_in, lib, g, top_k=2)
+    assert torch.equal(i1, i2) and torch.equal(s1, s2)
+
+    def step(q):
+        return ops.route_read_decode(q, lib, g, top_k=3)
+
+    step(q_in)
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step(q_in)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = step(q_in)
+    for seed in (3, 4, 5):
+        q_new = synth.queries(4, 512, device=dev, seed=seed)
+        q_in.copy_(q_new)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = step(q_new.clone())
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip(outs, ref)), seed

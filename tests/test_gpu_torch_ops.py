@@ -31,7 +31,7 @@ def _pool(dev, counts=(5, 3), N=128, d=256, seed=0):
 
 
 def test_opcheck_route_and_decode_read(dev):
-    say("opcheck route_topk / library_read")
+    say("opcheck route_topk / library_read / route_read")
     P, lib = _pool(dev)
     q = synth.queries(6, lib.d, device=dev, seed=3)
     qg = torch.tensor([0, 1, 1, 0, 1, 0], dtype=torch.int32, device=dev)
@@ -42,6 +42,9 @@ def test_opcheck_route_and_decode_read(dev):
     ws, rows = ops._WORKSPACES.get(dev, torch.cuda.current_stream(dev).cuda_stream, 6, kk, 2, lib.d)
     rargs = (q, lib.pages, lib.chunk_page, lib.chunk_nvalid, lib.chunk_ptr, qg, idx, wsel, 12.0, True, 2, ws, rows)
     torch.library.opcheck(torch.ops.xenc.library_read.default, rargs, test_utils=CHECKS)
+    fargs = (q, lib.S, lib.pages, lib.chunk_page, lib.chunk_nvalid, lib.chunk_ptr, qg, 2, 10.0, lib.cmax, kk, 12.0,
+             True, 2, ws, rows)
+    torch.library.opcheck(torch.ops.xenc.route_read.default, fargs, test_utils=CHECKS)
     r = torch.ops.xenc.library_read(*rargs).cpu().double()
     for m, g in enumerate(qg.tolist()):
         K, M, S = P.library(g)
