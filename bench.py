@@ -124,6 +124,50 @@ def cpu_baseline(P, q, top_k, n_seq, reps):
 MFMA_FP16_PEAK_TFLOPS = 2500.0
 
 
+def measured_mfma_peak(dev) -> float:
+    """fp16 MFMA TFLOP/s the device sustains on a pure register-operand MFMA loop
+    (xenc_calibrate_mfma: 2 waves per SIMD on every CU, random operands), best of 3 after a
+    warm-up: the ceiling the vendor peak's clock does not hold under sustained load."""
+    from kv_skill_v2_amd._lib import check, lib, stream_handle
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    src = (torch.rand(65536 * 8, generator=torch.Generator().manual_seed(1)) - 0.5).to(torch.float16).to(dev)
+    waves, rounds = 8, 4000
+    out = torch.empty(cus * waves * 64, dtype=torch.float32, device=dev)
+    L, st = lib(), stream_handle(dev)
+    best = 0.0
+    for rep in range(4):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        check(L.xenc_calibrate_mfma(src.data_ptr(), 65536, waves, cus, rounds, out.data_ptr(), st),
+              "xenc_calibrate_mfma")
+        e1.record()
+        torch.cuda.synchronize()
+        if rep:
+            best = max(best, cus * waves * rounds * 16 * 32768.0 / (e0.elapsed_time(e1) * 1e-3) / 1e12)
+    return best
+
+
+def measured_stream_peak(dev, gib: int = 2) -> float:
+    """HBM GB/s of a nontemporal 16-byte streaming read over `gib` GiB (xenc_calibrate_stream),
+    best of 3 after a warm-up: the read rate the decode kernels stream pages at."""
+    from kv_skill_v2_amd._lib import check, lib, stream_handle
+    buf = torch.ones(gib << 30, dtype=torch.uint8, device=dev)
+    blocks = (gib << 30) >> 21          # 2 MiB per workgroup, like a page of the batched decode
+    out = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    L, st = lib(), stream_handle(dev)
+    best = 0.0
+    for rep in range(4):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        check(L.xenc_calibrate_stream(buf.data_ptr(), buf.numel(), blocks, out.data_ptr(), st), "xenc_calibrate_stream")
+        e1.record()
+        torch.cuda.synchronize()
+        if rep:
+            best = max(best, buf.numel() / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    del buf
+    return best
+
+
 def bench_prefill(args):
     """Prefill/registration read: 4 documents x 2048 query rows, each document a Library of 32 x 512
     slots (ragged tail), d_s = 2048, dense routing (every chunk read), fp16 MFMA with fp32
@@ -180,6 +224,7 @@ def bench_prefill(args):
     flops = 4.0 * T * nvalid * d                  # per direction, all documents
     fwd_tf = flops / (fwd_ms * 1e-3) / 1e12
     bwd_tf = flops / (bwd_ms * 1e-3) / 1e12
+    mfma_meas = measured_mfma_peak(dev)
 
     cpu = None
     if args.cpu_sample > 0:
@@ -211,7 +256,8 @@ def bench_prefill(args):
         "roofline": {"bound": "mfma", "kernel": "scores_kernel + readout_kernel (fwd)",
                      "achieved": fwd_tf, "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS, "traffic": None,
-                     "algorithmic_flops": flops},
+                     "algorithmic_flops": flops, "measured_peak": mfma_meas,
+                     "frac_of_measured": fwd_tf / mfma_meas if mfma_meas else None},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
@@ -713,6 +759,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     traffic = traffic_from_profile(args.workload)
+    stream_meas = measured_stream_peak(dev)
 
     cpu = None
     if args.cpu_sample > 0:
@@ -744,7 +791,8 @@ def main():
                      "traffic": traffic["bytes_per_launch"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
                      "algorithmic_bytes": read_bytes + route_bytes, "avg_launch_ms": read_ms,
-                     "routed_slots": routed_slots, "read_bytes": read_bytes, "route_bytes": route_bytes},
+                     "routed_slots": routed_slots, "read_bytes": read_bytes, "route_bytes": route_bytes,
+                     "measured_peak": stream_meas, "frac_of_measured": achieved / stream_meas},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

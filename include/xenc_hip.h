@@ -370,6 +370,19 @@ int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_docs, const f
                   int top_k, int force, const float* wfix, int nsplit, float* out, float* w,
                   float* r, float* rmax, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * ---- Calibration (roofline denominators measured on the device; no counterpart in the reference)
+ * xenc_calibrate_mfma: cus * waves_per_cu waves (waves_per_cu a multiple of 4) each run `rounds`
+ *   rounds of 16 independent v_mfma_f32_32x32x16_f16 on operands read once from src (fp16, n_src
+ *   16-byte vectors); out receives one float per lane (cus * waves_per_cu * 64 floats).
+ *   FLOPs per launch: cus * waves_per_cu * rounds * 16 * 32768.
+ * xenc_calibrate_stream: `blocks` workgroups of 256 threads read `bytes` of src once with 16-byte
+ *   nontemporal loads (workgroup b a contiguous 1/blocks of it); out receives blocks * 256 floats.
+ */
+int xenc_calibrate_mfma(const void* src, int n_src, int waves_per_cu, int cus, int rounds, float* out,
+                        void* stream);
+int xenc_calibrate_stream(const void* src, long long bytes, int blocks, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

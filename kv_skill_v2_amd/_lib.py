@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 _lock = threading.Lock()
 _lib = None
@@ -62,6 +62,8 @@ SIGNATURES = {
         c_void_p, c_void_p, c_int,                   # idx, w_sel, kk
         c_float, c_int, c_int,                       # read_temp, softmax, nsplit
         c_void_p, c_longlong, c_void_p]),            # r, ldr, stream
+    "xenc_calibrate_mfma": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p]),
+    "xenc_calibrate_stream": (c_int, [c_void_p, c_longlong, c_int, c_void_p, c_void_p]),
     "xenc_cast_rows_f16": (c_int, [c_void_p, c_longlong, c_int, c_int, c_void_p, c_void_p]),
     "xenc_fragment_pages": (c_int, [c_void_p, c_longlong, c_int, c_int, c_int, c_void_p, c_void_p]),
     "xenc_build_pages": (c_int, [c_void_p, c_void_p, c_int, c_int, c_void_p, c_int, c_int, c_void_p,
