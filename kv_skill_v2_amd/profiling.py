@@ -48,19 +48,25 @@ def _copy_kernel(vals: list[tuple[str, float]]) -> float:
 
 
 def traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int) -> dict:
+    """Scaled HBM bytes per launch of `kernel`; a comma-separated list sums the per-dispatch means
+    of each kernel (the kernels one step launches once each)."""
     f = _counter(fetch_csv, "FETCH_SIZE")
     w = _counter(write_csv, "WRITE_SIZE")
-    fk = [v for n, v in f if kernel in n]
-    wk = [v for n, v in w if kernel in n]
-    if not fk or not wk:
-        raise SystemExit(f"kernel {kernel!r} not found in the counter files")
     fetch_scale = copy_bytes / (_copy_kernel(f) * 1024.0)
     write_scale = copy_bytes / (_copy_kernel(w) * 1024.0)
-    fetch_b = statistics.mean(fk) * 1024.0 * fetch_scale
-    write_b = statistics.mean(wk) * 1024.0 * write_scale
+    per, fetch_b, write_b, disp = {}, 0.0, 0.0, 0
+    for name in kernel.split(","):
+        fk = [v for n, v in f if name in n]
+        wk = [v for n, v in w if name in n]
+        if not fk or not wk:
+            raise SystemExit(f"kernel {name!r} not found in the counter files")
+        fb = statistics.mean(fk) * 1024.0 * fetch_scale
+        wb = statistics.mean(wk) * 1024.0 * write_scale
+        per[name] = {"fetch_bytes": fb, "write_bytes": wb, "dispatches": len(fk)}
+        fetch_b, write_b, disp = fetch_b + fb, write_b + wb, max(disp, len(fk))
     return {"kernel": kernel, "fetch_bytes": fetch_b, "write_bytes": write_b,
             "bytes_per_launch": fetch_b + write_b, "fetch_scale": fetch_scale,
-            "write_scale": write_scale, "dispatches": len(fk)}
+            "write_scale": write_scale, "dispatches": disp, "per_kernel": per}
 
 
 def main(argv=None):
