@@ -46,6 +46,8 @@ def _check(out, ref):
     (40, 512, 1000, 1, "shared"),           # 5 batches of 8 rows, d_out not a multiple of 32
     (64, 2560, 5120, 8, "per_group"),       # the multi-depth shape
     (17, 12, 7, 3, "shared"),               # tiny d and d_out
+    (300, 100, 70, 3, "per_group"),         # libraries of ~100 rows: several 32-row passes each
+    (4096, 32, 20, 2, "none"),              # the row limit
 ])
 def test_write_back_matches_oracle(dev, M, d, d_out, G, bias_kind):
     say("write-back", dict(M=M, d=d, d_out=d_out, G=G, bias=bias_kind))
@@ -53,10 +55,12 @@ def test_write_back_matches_oracle(dev, M, d, d_out, G, bias_kind):
     r = torch.randn(M, d, generator=g)
     W = torch.randn(G, d_out, d, generator=g) / d ** 0.5 if G > 1 else torch.randn(d_out, d, generator=g) / d ** 0.5
     groups = None
-    if G > 1:
+    if G > 2:
         # depth 1 unused; depth 0 serves 20 rows (three batches); the rest spread
         pool = [0] * 20 + [2 + (m % (G - 2)) for m in range(M - 20)]
         groups = torch.tensor(pool[:M], dtype=torch.int32)[torch.randperm(M, generator=g)]
+    elif G == 2:
+        groups = torch.randint(0, 2, (M,), generator=g, dtype=torch.int32)
     bias = None
     if bias_kind == "shared":
         bias = torch.randn(d_out, generator=g)
