@@ -293,7 +293,8 @@ def bench_multi_depth(args):
     gate_b = torch.full((L,), -2.0, device=dev)
     log_gain = torch.zeros(L, device=dev)
     hn = rms_norm(h)
-    md = MultiDepthDecode(lib, Bw, gate_w, gate_b, log_gain, sel.log_alpha, k_sel=c["k_sel"], top_k=k)
+    md = MultiDepthDecode(lib, Bw, gate_w, gate_b, log_gain, sel.log_alpha, k_sel=c["k_sel"], top_k=k,
+                          nsplit=args.nsplit)
 
     def step():
         return md(z, q_all, h, hn)

@@ -290,6 +290,24 @@ int xenc_gate_scale(int M, int d, const float* hn, long long ldh, const int* row
                     const float* log_gain, float gain_scale, float* scale, void* stream);
 
 /*
+ * xenc_multi_depth_prepare: the per-token work of a multi-depth decode step in one launch.  Per
+ *   token b < B: xenc_selector_weights on z[b] (n depths, top k) into w / idx / w_sel; for each
+ *   kept depth p = idx[b, j]: q_rows[b*k + j] = q_all[p * q_depth_stride + b * q_token_stride ..
+ *   + d) (the query row of that depth), and scale[b*k + j] = gain_scale * exp(log_gain[p]) *
+ *   sigmoid(<hn[b], gate_w> + gate_b[p]) (xenc_gate_scale with row_token = b, row_pos = p; hn fp32
+ *   [B, ldh] with d_r columns; gate_b and log_gain hold n entries).  Every output equals the
+ *   separate entry points' bit for bit.  Composes LayerSelector._weights_from_logits
+ *   (xenc/selector.py:59-67), the per-layer query of the branch (xenc/injector.py:220-229 run at
+ *   each kept layer) and itf_gate / itf_gain (xenc/injector.py:59-69).
+ */
+int xenc_multi_depth_prepare(const float* z, long long ldz, int B, int n, int k, const float* q_all,
+                             long long q_depth_stride, long long q_token_stride, int d, const float* hn,
+                             long long ldh, int d_r, const float* gate_w, const float* gate_b,
+                             const float* log_gain, float gain_scale, float* w, long long ldw, int* idx,
+                             float* w_sel, long long ld_sel, float* q_rows, long long ldr, float* scale,
+                             void* stream);
+
+/*
  * ---- Slot top-k selection read (D8)
  * xenc_select_scores: scores[b, i] = pool over query heads h of <q[b, h], keys[i, h / G]>
  *   (G = n_q / n_kv; pool_mean = 0: max, 1: mean), -inf where valid[i] == 0 (valid may be NULL).

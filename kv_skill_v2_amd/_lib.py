@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 _lock = threading.Lock()
 _lib = None
@@ -106,6 +106,13 @@ SIGNATURES = {
     "xenc_gate_scale": (c_int, [
         c_int, c_int, c_void_p, c_longlong, c_void_p, c_void_p, c_int,  # M, d, hn, ldh, row_token, row_pos, n_pos
         c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p]),    # gate_w, gate_b, log_gain, gain_scale, scale, stream
+    "xenc_multi_depth_prepare": (c_int, [
+        c_void_p, c_longlong, c_int, c_int, c_int,   # z, ldz, B, n, k
+        c_void_p, c_longlong, c_longlong, c_int,     # q_all, q_depth_stride, q_token_stride, d
+        c_void_p, c_longlong, c_int,                 # hn, ldh, d_r
+        c_void_p, c_void_p, c_void_p, c_float,       # gate_w, gate_b, log_gain, gain_scale
+        c_void_p, c_longlong, c_void_p, c_void_p, c_longlong,  # w, ldw, idx, w_sel, ld_sel
+        c_void_p, c_longlong, c_void_p, c_void_p]),  # q_rows, ldr, scale, stream
     "xenc_select_scores": (c_int, [
         c_void_p, c_int, c_int, c_int, c_int,        # q, B, n_q, n_kv, hd
         c_void_p, c_int, c_void_p, c_int,            # keys, S, valid, pool_mean

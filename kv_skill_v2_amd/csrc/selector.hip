@@ -11,6 +11,9 @@
 //   gate_scale_kernel        scale[m] = gain_scale * exp(log_gain[p]) *
 //                            sigmoid(<hn[t], gate_w> + gate_b[p]), t = row_token[m],
 //                            p = row_pos[m]: the per-row factor of delta = scale * B(r)
+//   multi_depth_prepare_kernel  selector_weights and gate_scale for the multi-depth decode step
+//                            in one launch: per token the selector top-k, the kept depths' query
+//                            rows gathered and their row scales
 // Every sum runs in a fixed order (deterministic).
 #include "xenc_common.h"
 
@@ -19,14 +22,11 @@ namespace {
 
 constexpr int kSelMaxN = 256;   // candidates per row (4 per lane)
 
-// One wave per row.
-__global__ __launch_bounds__(256) void selector_weights_kernel(
-    const float* __restrict__ z, long long ldz, int B, int n, int k, float* __restrict__ w,
-    long long ldw, int* __restrict__ idx, float* __restrict__ w_sel, long long lds) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int b = blockIdx.x * 4 + threadIdx.x / kWave;
-  if (b >= B) return;  // wave-uniform
-  const float* zr = z + (long long)b * ldz;
+// Top-k + softmax of one row of logits zr (n candidates) by one wave: dense weights into wr
+// (n entries), the kept (index, weight) pairs in rank order into idx / w_sel.
+__device__ __forceinline__ void select_weights_row(const float* __restrict__ zr, int n, int k, int lane,
+                                                   float* __restrict__ wr, int* __restrict__ idx,
+                                                   float* __restrict__ w_sel) {
   // Candidate c carries the 64-bit key (order_key(z_c) << 32) | ~c: a larger key is a larger
   // logit (NaN above +inf, as topk ranks it) or the same logit at a lower index.  Every real
   // candidate's key is nonzero, taken and padding entries are 0, so each of the k <= n rounds
@@ -66,7 +66,6 @@ __global__ __launch_bounds__(256) void selector_weights_kernel(
   const float e = lane < k ? __expf(kept_v - m) : 0.f;
   const float s = wave_sum(e);
   const float wk = e / s;
-  float* wr = w + (long long)b * ldw;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int c = lane + u * kWave;
@@ -76,9 +75,20 @@ __global__ __launch_bounds__(256) void selector_weights_kernel(
   __builtin_amdgcn_wave_barrier();
   if (lane < k) {
     wr[kept_i] = wk;
-    idx[(long long)b * lds + lane] = kept_i;
-    w_sel[(long long)b * lds + lane] = wk;
+    idx[lane] = kept_i;
+    w_sel[lane] = wk;
   }
+}
+
+// One wave per row.
+__global__ __launch_bounds__(256) void selector_weights_kernel(
+    const float* __restrict__ z, long long ldz, int B, int n, int k, float* __restrict__ w,
+    long long ldw, int* __restrict__ idx, float* __restrict__ w_sel, long long lds) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int b = blockIdx.x * 4 + threadIdx.x / kWave;
+  if (b >= B) return;  // wave-uniform
+  select_weights_row(z + (long long)b * ldz, n, k, lane, w + (long long)b * ldw, idx + (long long)b * lds,
+                     w_sel + (long long)b * lds);
 }
 
 // Workgroup sum of one float per thread (kRowThreads threads), fixed order.
@@ -180,6 +190,46 @@ __global__ __launch_bounds__(kRowThreads) void gate_scale_kernel(
   }
 }
 
+// The multi-depth step's per-token work in one launch, one workgroup per token b: the selector
+// top-k of z[b] (select_weights_row, wave 0), then the query row of each kept depth copied from
+// q_all into q_rows[b*k + j], and the row scale of each kept depth from the token's gate dot
+// (row_dot, the gate_scale_kernel sum).  Each output is bit-identical to the separate kernel's.
+__global__ __launch_bounds__(kRowThreads) void multi_depth_prepare_kernel(
+    const float* __restrict__ z, long long ldz, int n, int k, const float* __restrict__ q_all,
+    long long q_depth_stride, long long q_token_stride, int d, const float* __restrict__ hn,
+    long long ldh, int d_r, const float* __restrict__ gate_w, const float* __restrict__ gate_b,
+    const float* __restrict__ log_gain, float gain_scale, float* __restrict__ w, long long ldw,
+    int* __restrict__ idx, float* __restrict__ w_sel, long long lds, float* __restrict__ q_rows,
+    long long ldr, float* __restrict__ scale, int vec4_q, int vec4_h) {
+  __shared__ float red[kRowThreads / kWave];
+  __shared__ int kept[64];
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (threadIdx.x < kWave) {
+    select_weights_row(z + (long long)b * ldz, n, k, lane, w + (long long)b * ldw, idx + (long long)b * lds,
+                       w_sel + (long long)b * lds);
+    if (lane < k) kept[lane] = idx[(long long)b * lds + lane];
+  }
+  // The gate dot does not depend on the selection: it runs while wave 0 selects (row_dot's
+  // barriers also publish kept[]).
+  const float s = row_dot(hn + (long long)b * ldh, gate_w, d_r, vec4_h, red, Fma());
+  for (int j = 0; j < k; ++j) {
+    const int p = kept[j];
+    const float* src = q_all + (long long)p * q_depth_stride + (long long)b * q_token_stride;
+    float* dst = q_rows + ((long long)b * k + j) * ldr;
+    if (vec4_q) {
+      for (int i = threadIdx.x; i < d / 4; i += kRowThreads)
+        reinterpret_cast<f32x4*>(dst)[i] = reinterpret_cast<const f32x4*>(src)[i];
+    } else {
+      for (int e = threadIdx.x; e < d; e += kRowThreads) dst[e] = src[e];
+    }
+    if (threadIdx.x == 0) {
+      const float g = 1.f / (1.f + __expf(-(s + gate_b[p])));
+      scale[(long long)b * k + j] = gain_scale * __expf(log_gain[p]) * g;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace xenc
 
@@ -222,5 +272,29 @@ extern "C" int xenc_gate_scale(int M, int d, const float* hn, long long ldh, con
   hipLaunchKernelGGL(gate_scale_kernel, dim3(M), dim3(kRowThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), M, d, hn, ldh, row_token, row_pos, n_pos,
                      gate_w, gate_b, log_gain, gain_scale, scale, vec4);
+  return check_launch();
+}
+
+extern "C" int xenc_multi_depth_prepare(const float* z, long long ldz, int B, int n, int k,
+                                        const float* q_all, long long q_depth_stride,
+                                        long long q_token_stride, int d, const float* hn, long long ldh,
+                                        int d_r, const float* gate_w, const float* gate_b,
+                                        const float* log_gain, float gain_scale, float* w, long long ldw,
+                                        int* idx, float* w_sel, long long ld_sel, float* q_rows,
+                                        long long ldr, float* scale, void* stream) {
+  if (B < 0 || n <= 0 || n > kSelMaxN || k <= 0 || k > n || k > kWave || ldz < n || ldw < n ||
+      ld_sel < k || d <= 0 || d_r <= 0 || ldh < d_r || ldr < d)
+    return XENC_EINVAL;
+  if (q_depth_stride < 0 || q_token_stride < 0) return XENC_EINVAL;
+  if (B == 0) return XENC_OK;
+  if (!z || !q_all || !hn || !gate_w || !gate_b || !log_gain || !w || !idx || !w_sel || !q_rows || !scale)
+    return XENC_ENULL;
+  const int vec4_q = (d % 4 == 0 && q_depth_stride % 4 == 0 && q_token_stride % 4 == 0 && ldr % 4 == 0 &&
+                      aligned16(q_all) && aligned16(q_rows)) ? 1 : 0;
+  const int vec4_h = (d_r % 4 == 0 && ldh % 4 == 0 && aligned16(hn) && aligned16(gate_w)) ? 1 : 0;
+  hipLaunchKernelGGL(multi_depth_prepare_kernel, dim3(B), dim3(kRowThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), z, ldz, n, k, q_all, q_depth_stride,
+                     q_token_stride, d, hn, ldh, d_r, gate_w, gate_b, log_gain, gain_scale, w, ldw, idx,
+                     w_sel, ld_sel, q_rows, ldr, scale, vec4_q, vec4_h);
   return check_launch();
 }

@@ -5,13 +5,13 @@ every candidate layer and multiplies the update of every unselected layer by zer
 selector's top-k runs first, and only the (token, selected depth) rows are routed, read and
 written back:
 
-    1. selector weights: top-k of the logits z [B, L] per token, softmax over the kept ones
-       (xenc_selector_weights; ties go to the lower depth);
-    2. the query row of each (token, kept depth) pair, gathered from q_all [L, B, d];
-    3. routing over the chunks of that row's depth library (xenc_route_topk);
-    4. the paged split-K read of the routed pages (xenc_library_read_decode);
-    5. gate * gain per row (xenc_gate_scale), the depth's B streamed once (xenc_write_back);
-    6. the matched-norm rescale times the selector weight, summed over a token's kept depths
+    1. per token, in one launch (xenc_multi_depth_prepare): the selector's top-k of the logits
+       z [B, L] with a softmax over the kept ones (ties go to the lower depth), the query row of
+       each kept depth gathered from q_all [L, B, d], and gate * gain of each (token, depth) row;
+    2. routing over the chunks of that row's depth library (xenc_route_topk);
+    3. the paged split-K read of the routed pages (xenc_library_read_decode);
+    4. the depth's B streamed once with the row scale folded in (xenc_write_back);
+    5. the matched-norm rescale times the selector weight, summed over a token's kept depths
        (xenc_selector_apply).
 
 The depth libraries are one pool (`PagedLibrary` with one library per depth); the row's library
@@ -51,6 +51,7 @@ class MultiDepthDecode:
     route_temp: float = 10.0
     read_temp: float = 12.0
     gain_scale: float = 1.0
+    nsplit: int | None = None   # slot splits per routed page of the read (None: the read's default)
 
     def __post_init__(self):
         L = self.lib.n_libraries
@@ -58,32 +59,19 @@ class MultiDepthDecode:
             raise ValueError(f"B_w must be [{L}, d_r, {self.lib.d}]")
         if not 1 <= self.k_sel <= L:
             raise ValueError(f"k_sel={self.k_sel} must lie in [1, {L}]")
-        self._tokens = {}
-
-    def _token_rows(self, B: int, device) -> tuple:
-        """(token of each row int64, the same int32) for a batch of B, built once per batch size."""
-        key = (B, device)
-        t = self._tokens.get(key)
-        if t is None:
-            tok = torch.arange(B, device=device).repeat_interleave(self.k_sel)
-            t = self._tokens[key] = (tok, tok.to(torch.int32))
-        return t
 
     def __call__(self, z: torch.Tensor, q_all: torch.Tensor, h: torch.Tensor, hn: torch.Tensor):
         """z fp32 [B, L] selector logits, q_all fp32 [L, B, d] each depth's query rows, h fp32
         [B, d_r] the residual and hn its RMS norm.  Returns (out [B, d_r], idx [B*k_sel, kk]
         routed chunks, depth [B*k_sel] int32): row b*k_sel + j is token b's j-th kept depth."""
-        B = z.shape[0]
         k = self.k_sel
         with torch.no_grad():
-            _, top, wtop = ops.selector_weights(z, k)
+            _, top, wtop, qr, scale = ops.multi_depth_prepare(z, k, q_all, hn, self.gate_w, self.gate_b,
+                                                              self.log_gain, self.gain_scale)
             depth = top.reshape(-1)
-            token, token32 = self._token_rows(B, z.device)
-            qr = q_all[depth.long(), token]
             _, idx, wsel = ops.route_topk(qr, self.lib, depth, top_k=self.top_k, route_temp=self.route_temp)
-            r = ops.library_read_decode(qr, self.lib, idx, wsel, depth, read_temp=self.read_temp)
-            scale = ops.gate_scale(hn, self.gate_w, self.gate_b, self.log_gain, self.gain_scale,
-                                   token32, depth)
+            r = ops.library_read_decode(qr, self.lib, idx, wsel, depth, read_temp=self.read_temp,
+                                        nsplit=self.nsplit)
             upd = ops.write_back(r, self.B_w, depth, None, scale)
             out = ops.selector_apply(upd, h, wtop.reshape(-1), self.log_alpha, k=k)
         return out, idx, depth

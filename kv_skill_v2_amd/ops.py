@@ -528,6 +528,42 @@ def gate_scale(hn: torch.Tensor, gate_w: torch.Tensor, gate_b: torch.Tensor, log
     return out
 
 
+def multi_depth_prepare(z: torch.Tensor, k: int, q_all: torch.Tensor, hn: torch.Tensor,
+                        gate_w: torch.Tensor, gate_b: torch.Tensor, log_gain: torch.Tensor,
+                        gain_scale: float = 1.0):
+    """The per-token work of a multi-depth decode step in one launch (xenc_multi_depth_prepare):
+    z fp32 [B, L] selector logits, q_all fp32 [L, B, d] each depth's query rows, hn fp32 [B, d_r].
+    Returns (w [B, L], top int32 [B, k], wtop [B, k], q_rows [B*k, d], scale [B*k]): the
+    selector_weights outputs, q_rows[b*k + j] = q_all[top[b, j], b] and scale[b*k + j] =
+    gate_scale(hn, ..., row_token=b, row_pos=top[b, j]) — each equal to the separate calls."""
+    for t, n in ((z, "z"), (q_all, "q_all"), (hn, "hn"), (gate_w, "gate_w"), (gate_b, "gate_b"),
+                 (log_gain, "log_gain")):
+        _require_device(t, n)
+    if z.dtype != torch.float32 or z.dim() != 2 or z.stride(1) != 1:
+        raise ValueError("z must be fp32 [B, L] with unit column stride")
+    B, L = z.shape
+    if q_all.dtype != torch.float32 or q_all.dim() != 3 or q_all.shape[:2] != (L, B) or q_all.stride(2) != 1:
+        raise ValueError(f"q_all must be fp32 [{L}, {B}, d] with unit column stride")
+    if hn.dtype != torch.float32 or hn.dim() != 2 or hn.shape[0] != B or hn.stride(1) != 1:
+        raise ValueError(f"hn must be fp32 [{B}, d_r] with unit column stride")
+    d, d_r = q_all.shape[2], hn.shape[1]
+    gw, gb, lg = (t.detach().float().reshape(-1).contiguous() for t in (gate_w, gate_b, log_gain))
+    if gw.numel() != d_r or gb.numel() != L or lg.numel() != L:
+        raise ValueError(f"gate_w must have {d_r} entries and gate_b / log_gain one per depth ({L})")
+    dev = z.device
+    w = torch.empty(B, L, dtype=torch.float32, device=dev)
+    top = torch.empty(B, k, dtype=torch.int32, device=dev)
+    wtop = torch.empty(B, k, dtype=torch.float32, device=dev)
+    q_rows = torch.empty(B * k, d, dtype=torch.float32, device=dev)
+    scale = torch.empty(B * k, dtype=torch.float32, device=dev)
+    check(lib().xenc_multi_depth_prepare(ptr(z), z.stride(0), B, L, int(k), ptr(q_all), q_all.stride(0),
+                                         q_all.stride(1), d, ptr(hn), hn.stride(0), d_r, ptr(gw), ptr(gb),
+                                         ptr(lg), float(gain_scale), ptr(w), w.stride(0), ptr(top), ptr(wtop),
+                                         k, ptr(q_rows), q_rows.stride(0), ptr(scale), stream_handle(dev)),
+          "xenc_multi_depth_prepare")
+    return w, top, wtop, q_rows, scale
+
+
 def select_scores(q: torch.Tensor, keys: torch.Tensor, valid: torch.Tensor | None = None,
                   pool: str = "max") -> torch.Tensor:
     """Pooled selection scores [B, S] on xenc_select_scores: q fp32 [B, n_q, hd] (one position),
@@ -946,5 +982,5 @@ def d18_read(qd: torch.Tensor, qo: torch.Tensor, ops, Kown: torch.Tensor, Vown: 
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "route_read_decode", "default_nsplit", "RowPlan", "row_plan",
            "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "route_differentiable",
            "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS",
-           "build_pages", "write_back", "select_scores", "topk_rows", "gather_library", "selector_weights",
+           "build_pages", "write_back", "multi_depth_prepare", "select_scores", "topk_rows", "gather_library", "selector_weights",
            "selector_apply", "gate_scale", "D18Operators", "d18_pack", "d18_read", "d18_nsplit"]

@@ -114,6 +114,34 @@ def test_gate_scale_matches_epilogue(dev):
     assert float((s2.cpu().double().unsqueeze(-1) * r2 - ep).abs().max()) < 1e-5
 
 
+@pytest.mark.parametrize("B,L,k,d,d_r,ties,vec4", [(32, 8, 2, 2560, 5120, False, True),
+                                                   (7, 8, 3, 36, 20, True, True),
+                                                   (5, 12, 2, 30, 18, False, False)])
+def test_multi_depth_prepare_equals_separate_calls(dev, B, L, k, d, d_r, ties, vec4):
+    """xenc_multi_depth_prepare: the selector outputs, the gathered query rows and the row scales
+    equal xenc_selector_weights, q_all[top, token] and xenc_gate_scale bit for bit (also with
+    tied logits, a strided q_all and rows whose sizes force the scalar copy / dot)."""
+    say("multi-depth prepare", dict(B=B, L=L, k=k, d=d, d_r=d_r, ties=ties, vec4=vec4))
+    g = torch.Generator().manual_seed(B * L + d)
+    z = (torch.randint(-2, 3, (B, L), generator=g).float() if ties else torch.randn(B, L, generator=g)).to(dev)
+    q_big = torch.randn(L, B, d + (0 if vec4 else 3), generator=g).to(dev)
+    q_all = q_big[:, :, :d]                       # strided over tokens and depths when padded
+    hn = torch.randn(B, d_r, generator=g).to(dev)
+    gate_w = (torch.randn(d_r, generator=g) / d_r ** 0.5).to(dev)
+    gate_b = torch.randn(L, generator=g).to(dev)
+    log_gain = (0.1 * torch.randn(L, generator=g)).to(dev)
+    w, top, wtop, q_rows, scale = ops.multi_depth_prepare(z, k, q_all, hn, gate_w, gate_b, log_gain, 0.7)
+    w2, top2, wtop2 = ops.selector_weights(z, k)
+    assert torch.equal(w, w2) and torch.equal(top, top2) and torch.equal(wtop, wtop2)
+    depth = top.reshape(-1).long()
+    token = torch.arange(B, device=dev).repeat_interleave(k)
+    assert torch.equal(q_rows, q_all[depth, token])
+    scale2 = ops.gate_scale(hn, gate_w, gate_b, log_gain, 0.7, token.int(), depth.int())
+    assert torch.equal(scale, scale2)
+    with pytest.raises(ValueError):
+        ops.multi_depth_prepare(z, k, q_all, hn, gate_w, gate_b[:-1], log_gain, 0.7)
+
+
 def test_selector_guards(dev):
     say("selector guards")
     with pytest.raises(ValueError):
