@@ -163,7 +163,9 @@ int xenc_library_read_decode_noalloc(const float* q, long long ldq, int M, int d
  * with lane l of block (db, nb) = K[16nb + 8(l/32) + e][32db + l%32].  page_stride is the stride
  * of one page in the copy (>= slots*d).
  *
- * xenc_prefill_scores(mode=0): p = masked softmax_n(temp * <x_t, K[c,n]>) per (row, chunk).
+ * xenc_prefill_scores(mode=0): p = masked softmax_n(temp * <x_t, K[c,n]>) per (row, chunk); when
+ *     gamma is not NULL also gamma[t, c] = logsumexp_n(temp * <x_t, K[c,n]>) over the valid slots
+ *     (the per-chunk normaliser, used to join sub-pages of a page longer than 512 slots).
  * xenc_prefill_scores(mode=1): x = upstream gradient g; u = <g_t, K[c,n]>;
  *     gamma[t,c] = sum_n p u  (= dL/dw[t,c] through the read) and
  *     ds[t, c, n] = temp * w[t,c] * p * (u - gamma[t,c]).

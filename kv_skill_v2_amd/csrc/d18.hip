@@ -33,7 +33,6 @@ constexpr int kD18MaxG = 8;
 constexpr int kD18MaxHd = 256;
 constexpr int kD18MaxDocs = 64;
 constexpr int kD18MaxSplits = 32;
-constexpr float kLn2 = 0.6931471805599453f;
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));

@@ -113,7 +113,8 @@ __global__ __launch_bounds__(256) void fragment_pages_kernel(const _Float16* __r
 // coalesced 1 KiB load each), refilled for the next k-step as soon as they are consumed; the 128
 // query rows are shared by all waves and staged through LDS (two swizzled stages, one barrier
 // per k-step).
-// MODE 0 (forward): writes p = masked softmax over the chunk's slots (fp16, octet-major).
+// MODE 0 (forward): writes p = masked softmax over the chunk's slots (fp16, octet-major), and
+//                    when gamma is given gamma[t, c] = log-sum-exp of the row's scaled scores.
 // MODE 1 (backward): reads p, writes dS = read_temp * w[t,c] * p * (U - gamma) (octet-major)
 //                    and gamma[t, c] = sum_n p U.
 // MODE 2 (forward, linear read): writes p = S / sqrt(n_valid) on valid slots, 0 on the others.
@@ -321,6 +322,11 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
       for (int w2 = 0; w2 < 8; ++w2) s += red[w2][nt * 32 + l32];
       rsum[nt] = 1.f / s;
+      // Optional: the log-sum-exp of the row's scaled scores over the chunk's valid slots
+      // (natural log; rmax and s are in log2 units).
+      const int t = row0 + nt * 32 + l32;
+      if (gamma && wv == 0 && hl == 0 && t < rend)
+        gamma[(long long)t * ldg + c] = (rmax[nt] + __log2f(s)) * kLn2;
     }
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt) {

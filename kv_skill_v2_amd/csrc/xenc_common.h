@@ -140,6 +140,7 @@ __device__ __forceinline__ unsigned order_key(float x) {
 }
 
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2).  Tile b is
 // remapped so that XCD x runs a contiguous range of logical tiles; the logical order then puts

@@ -281,6 +281,14 @@ class PagedLibrary:
             self._frag[key] = t
         return t
 
+    def sub_pages(self) -> "SubPages":
+        """This pool split into pages of at most SUB_SPAN slots for the MFMA kernels (see
+        SubPages), built on first use and kept with the pool."""
+        t = self._frag.get("sub")
+        if t is None:
+            t = self._frag["sub"] = _build_sub_pages(self)
+        return t
+
     def plan(self, rows_per_library) -> "RowPlan":
         """Row plan for this pool, cached per row-count tuple (avoids small host->device copies
         on every step of a fixed-shape loop)."""
@@ -812,10 +820,148 @@ def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int 
                  read_temp: float = 12.0, route_temp: float = 10.0, read_softmax: bool = True):
     """(r [M, d], w [M, cmax]) with autograd through both routing and the read (MFMA path).  The
     routing pass also writes the fp16 rows the read takes, so q is read from HBM once."""
-    lib_.check_prefill()
+    if not prefill_ok(lib_) and not _mfma_pages_ok(lib_):
+        lib_.check_prefill()
     w, _, _, qh = route_differentiable(q, lib_, plan, int(top_k), float(route_temp), emit_f16=True)
-    r, _ = prefill_forward(q, w, lib_, plan, float(read_temp), bool(read_softmax), qh=qh)
+    if prefill_ok(lib_):
+        r, _ = prefill_forward(q, w, lib_, plan, float(read_temp), bool(read_softmax), qh=qh)
+    else:   # pages longer than 512 slots
+        r = read_sub_pages(q, w, lib_, plan, float(read_temp), bool(read_softmax), qh=qh)
     return r, w
+
+
+# ----------------------------------------------------------------------------- pages > 512 slots
+SUB_SPAN = 512   # slots per sub-page: the MFMA scores tile covers one page of at most this many
+
+
+@dataclass
+class SubPages:
+    """A pool whose pages are longer than SUB_SPAN slots, re-paged for the MFMA kernels: chunk c
+    becomes ceil(n_c / SUB_SPAN) sub-chunks (sub-chunk j holds its slots SUB_SPAN j .. SUB_SPAN
+    (j + 1) - 1), the sub-chunks of a library in chunk order.
+
+    lib     the re-paged pool (untied values re-paged alike)
+    tied    the same pool with the keys as values (the gradient of a sub-chunk's log-sum-exp)
+    parent  int64 [G, cmax_sub]: the local chunk of each local sub-chunk (0 past a library's end)
+    valid   bool [G, cmax_sub]: the sub-chunk exists
+    ratio   fp32 [G, cmax_sub]: sqrt(n_sub / n_chunk), the linear read's 1 / sqrt(n) per chunk"""
+
+    lib: PagedLibrary
+    tied: PagedLibrary
+    parent: torch.Tensor
+    valid: torch.Tensor
+    ratio: torch.Tensor
+
+
+def _build_sub_pages(lib_: PagedLibrary) -> SubPages:
+    span, N, d, dev = SUB_SPAN, lib_.slots_per_page, lib_.d, lib_.device
+    blocks = -(-N // span)
+    cpage = lib_.chunk_page.cpu().tolist()
+    src_page, src_block, nv_sub, n_sub, parent_local = [], [], [], [], []
+    for n in lib_.nvalid:
+        n_sub.append(-(-n // span))
+    c0 = 0
+    for nch in lib_.n_chunks:
+        for c in range(nch):
+            gc = c0 + c
+            for j in range(n_sub[gc]):
+                src_page.append(cpage[gc])
+                src_block.append(j)
+                nv_sub.append(min(span, lib_.nvalid[gc] - j * span))
+                parent_local.append(c)
+        c0 += nch
+    sp_t, sb_t = (torch.tensor(x, dtype=torch.int64, device=dev) for x in (src_page, src_block))
+
+    def repage(src):
+        padded = torch.nn.functional.pad(src, (0, 0, 0, blocks * span - N)) if blocks * span != N else src
+        return padded.view(src.shape[0], blocks, span, d)[sp_t, sb_t].contiguous()
+
+    pages = repage(lib_.pages)
+    values = repage(lib_.values) if lib_.values is not None else None
+    subs_per_lib, c0 = [], 0
+    for nch in lib_.n_chunks:
+        subs_per_lib.append(sum(n_sub[c0:c0 + nch]))
+        c0 += nch
+    ptr_ = [0]
+    for k in subs_per_lib:
+        ptr_.append(ptr_[-1] + k)
+    parent_global = torch.tensor([g for g, k in enumerate(n_sub) for _ in range(k)], dtype=torch.int64, device=dev)
+    P = len(src_page)
+    sub = PagedLibrary(pages, torch.arange(P, dtype=torch.int32, device=dev), _i32(nv_sub, dev), _i32(ptr_, dev),
+                       lib_.S[parent_global].contiguous(), n_chunks=subs_per_lib, nvalid=nv_sub, values=values,
+                       d_valid=lib_.d_valid)
+    tied = PagedLibrary(pages, sub.chunk_page, sub.chunk_nvalid, sub.chunk_ptr, sub.S, n_chunks=subs_per_lib,
+                        nvalid=nv_sub, d_valid=lib_.d_valid)
+    tied._frag, tied._plans = sub._frag, sub._plans   # the key-side fragment copies are the same
+    G, cmax_sub = lib_.n_libraries, max(subs_per_lib)
+    parent = torch.zeros(G, cmax_sub, dtype=torch.int64)
+    valid = torch.zeros(G, cmax_sub, dtype=torch.bool)
+    ratio = torch.zeros(G, cmax_sub, dtype=torch.float32)
+    i = 0
+    c0 = 0
+    for g, (nch, k) in enumerate(zip(lib_.n_chunks, subs_per_lib)):
+        for j in range(k):
+            pc = parent_local[i]
+            parent[g, j], valid[g, j] = pc, True
+            ratio[g, j] = math.sqrt(nv_sub[i] / lib_.nvalid[c0 + pc])
+            i += 1
+        c0 += nch
+    return SubPages(sub, tied, parent.to(dev), valid.to(dev), ratio.to(dev))
+
+
+class _SubPageLse(torch.autograd.Function):
+    """a [M, cmax_sub] = logsumexp_n(read_temp * q . K[j, n]) per (row, sub-chunk) (operator
+    xenc::library_prefill_lse); backward: dq = read_temp * sum_j g_j sum_n p[j, n] K[j, n], the
+    read of the tied sub-pages with weights g (xenc::library_prefill_fwd)."""
+
+    @staticmethod
+    def forward(ctx, q, qh, sp: SubPages, splan: RowPlan, read_temp: float):
+        L = sp.lib
+        lse = torch.ops.xenc.library_prefill_lse(q, qh, L.fragment_pages(0), L.chunk_ptr, L.chunk_page,
+                                                 L.chunk_nvalid, splan.row_ptr, splan.score_tiles, splan.n_score,
+                                                 L.slots_per_page, float(read_temp), L.cmax)
+        ctx.save_for_backward(q)
+        ctx.sp, ctx.splan, ctx.read_temp = sp, splan, float(read_temp)
+        return lse
+
+    @staticmethod
+    def backward(ctx, g):
+        (q,) = ctx.saved_tensors
+        g = torch.nan_to_num(g, nan=0.0, posinf=0.0, neginf=0.0).contiguous()
+        with torch.no_grad():
+            o, _ = prefill_forward(q, g, ctx.sp.tied, ctx.splan, ctx.read_temp, True)
+        return o * ctx.read_temp, None, None, None, None
+
+
+def read_sub_pages(q: torch.Tensor, w: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, read_temp: float = 12.0,
+                   softmax: bool = True, qh: torch.Tensor | None = None) -> torch.Tensor:
+    """r [M, d]: the read of a pool with pages longer than SUB_SPAN slots on the MFMA kernels,
+    differentiable in q and w like prefill_forward.  A chunk's masked softmax over its n slots
+    splits over its sub-chunks j: r = sum_c w_c sum_j pi_j o_j, o_j the softmax read of sub-chunk
+    j and pi = softmax over the chunk's sub-chunks of their log-sum-exps a_j (linear read: pi_j =
+    sqrt(n_j / n) undoes the sub-chunk's own 1 / sqrt(n_j)).  The sub-chunk weights W = w pi feed
+    the ordinary read of the re-paged pool (xenc/injector.py:239-265 for any page length)."""
+    sp = lib_.sub_pages()
+    splan = sp.lib.plan(plan.rows)
+    rg = torch.repeat_interleave(torch.arange(len(plan.rows), device=q.device),
+                                 torch.as_tensor(plan.rows, device=q.device))
+    par, val = sp.parent[rg], sp.valid[rg]
+    W = w.to(torch.float32).gather(1, par) * val
+    if softmax:
+        a = _SubPageLse.apply(q, qh, sp, splan, read_temp).masked_fill(~val, float("-inf"))
+        amax = torch.full(w.shape, float("-inf"), device=q.device).scatter_reduce(1, par, a.detach(), "amax")
+        e = torch.exp(a - amax.gather(1, par)).masked_fill(~val, 0.0)
+        den = torch.zeros(w.shape, device=q.device).scatter_add(1, par, e)
+        W = W * e / den.gather(1, par).clamp_min(torch.finfo(torch.float32).tiny)
+    else:
+        W = W * sp.ratio[rg]
+    r, _ = prefill_forward(q, W.contiguous(), sp.lib, splan, float(read_temp), bool(softmax), qh=qh)
+    return r
+
+
+def _mfma_pages_ok(lib_: PagedLibrary) -> bool:
+    """The MFMA kernels can read this pool, directly or as sub-pages."""
+    return lib_.d % 64 == 0 and lib_.slots_per_page % 64 == 0
 
 
 # Above this many query rows on one library the MFMA prefill path reads it (each page once per
@@ -857,19 +1003,22 @@ def read_rows(q: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, w_sel: torch.
     LibraryInjector._branch, xenc/injector.py:239-265).
 
     With autograd (q or w requires grad), untied values, or more than DECODE_MAX_ROWS rows it runs
-    the MFMA prefill path (differentiable in q and w); otherwise the split-K decode path."""
+    the MFMA prefill path (differentiable in q and w; pages longer than 512 slots as sub-pages,
+    read_sub_pages); otherwise, and for forward reads of tied pages longer than 512 slots, the
+    split-K decode path."""
     _single(lib_)
     qp = _pad_rows(q, lib_)
     M = qp.shape[0]
     grad = torch.is_grad_enabled() and (q.requires_grad or w.requires_grad)
     mfma = grad or lib_.values is not None or M > DECODE_MAX_ROWS
-    if mfma and not prefill_ok(lib_):
-        if grad or lib_.values is not None:
-            raise ValueError("a differentiable or untied-value read takes pages of <= 512 slots "
-                             f"(got {lib_.slots_per_page})")
+    if mfma and not prefill_ok(lib_) and not (grad or lib_.values is not None):
         mfma = False        # a forward read of larger pages: the split-K decode path takes any size
-    if mfma:
+    if mfma and prefill_ok(lib_):
         r, _ = prefill_forward(qp, w, lib_, lib_.plan([M]), float(read_temp), bool(read_softmax))
+    elif mfma:
+        if not _mfma_pages_ok(lib_):
+            lib_.check_prefill()
+        r = read_sub_pages(qp, w, lib_, lib_.plan([M]), float(read_temp), bool(read_softmax))
     else:
         r = library_read_decode(qp, lib_, idx, w_sel, None, read_temp, read_softmax)
     return r[:, :lib_.d_valid] if lib_.d != lib_.d_valid else r
@@ -982,5 +1131,5 @@ def d18_read(qd: torch.Tensor, qo: torch.Tensor, ops, Kown: torch.Tensor, Vown: 
 __all__ = ["PagedLibrary", "route_topk", "library_read_decode", "route_read_decode", "default_nsplit", "RowPlan", "row_plan",
            "cast_f16", "prefill_forward", "prefill_backward", "route_backward", "route_topk_rows", "route_differentiable",
            "library_read", "route_rows", "read_rows", "branch_read", "unpack_p", "DECODE_MAX_ROWS",
-           "build_pages", "write_back", "multi_depth_prepare", "select_scores", "topk_rows", "gather_library", "selector_weights",
+           "build_pages", "write_back", "multi_depth_prepare", "read_sub_pages", "SubPages", "SUB_SPAN", "select_scores", "topk_rows", "gather_library", "selector_weights",
            "selector_apply", "gate_scale", "D18Operators", "d18_pack", "d18_read", "d18_nsplit"]

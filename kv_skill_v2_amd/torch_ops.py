@@ -14,6 +14,8 @@ dispatcher, FakeTensor tracing and torch.compile see ordinary operators:
                                  when every library has at most 64 chunks)
     xenc::route_rows             routing of many rows grouped by library (fp32 MFMA tiles), also
                                  emitting the rows as fp16; differentiable in q
+    xenc::library_prefill_lse    per (row, chunk) log-sum-exp of the read's scores (the join of the
+                                 sub-pages of pages longer than 512 slots)
     xenc::library_prefill_fwd    the MFMA read of many rows -> (r [M, d], p); differentiable in q
                                  and w (its backward is the next operator plus the route term)
     xenc::library_prefill_bwd_dq (dq through the read, gamma = dL/dw) from the upstream gradient
@@ -251,6 +253,33 @@ def _(q, qh, w, frag_k_scores, frag_v_readout, frag_v_scores, frag_k_readout, ch
     return q.new_empty(M, d), q.new_empty(w.shape[1] * slots // 8, M, 8, dtype=torch.float16)
 
 
+@custom_op("xenc::library_prefill_lse", mutates_args=())
+def library_prefill_lse(q: Tensor, qh: Optional[Tensor], frag_k_scores: Tensor, chunk_ptr: Tensor,
+                        chunk_page: Tensor, chunk_nvalid: Tensor, row_ptr: Tensor, score_tiles: Tensor,
+                        n_score: int, slots: int, read_temp: float, cmax: int) -> Tensor:
+    """lse [M, cmax] fp32: logsumexp_n(read_temp * q . K[c, n]) over the valid slots of each of the
+    row's chunks (the forward scores pass; -inf for chunks a row's library does not have)."""
+    M, d = q.shape
+    G = chunk_ptr.numel() - 1
+    L, st = lib(), _st(q)
+    if qh is None or qh.numel() == 0:
+        qh = torch.empty(M, d, dtype=torch.float16, device=q.device)
+        check(L.xenc_cast_rows_f16(ptr(q), q.stride(0), M, d, ptr(qh), st), "xenc_cast_rows_f16")
+    p = torch.empty(cmax * slots // 8, M, 8, dtype=torch.float16, device=q.device)
+    lse = torch.full((M, cmax), float("-inf"), dtype=torch.float32, device=q.device)
+    check(L.xenc_prefill_scores(0, ptr(qh), d, ptr(row_ptr), ptr(score_tiles), G, n_score, ptr(frag_k_scores),
+                                slots, frag_k_scores.stride(0), ptr(chunk_ptr), ptr(chunk_page), ptr(chunk_nvalid),
+                                read_temp, None, 0, ptr(p), M, None, ptr(lse), lse.stride(0), st),
+          "xenc_prefill_scores")
+    return lse
+
+
+@library_prefill_lse.register_fake
+def _(q, qh, frag_k_scores, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles, n_score, slots, read_temp,
+      cmax):
+    return q.new_empty(q.shape[0], cmax)
+
+
 _PREFILL_TENSORS = ("frag_v_scores", "frag_k_readout", "chunk_ptr", "chunk_page", "chunk_nvalid", "row_ptr",
                     "score_tiles", "readout_tiles")
 
@@ -300,5 +329,6 @@ def _(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale, nsplit
     return None
 
 
-__all__ = ["route_topk", "library_read", "route_read", "route_rows", "route_backward_", "library_prefill_fwd",
+__all__ = ["route_topk", "library_read", "route_read", "route_rows", "route_backward_", "library_prefill_lse",
+           "library_prefill_fwd",
            "library_prefill_bwd_dq", "paged_decode_joint", "kept_width"]
