@@ -12,8 +12,9 @@
 // units being the D documents and the own rows, each cut into S key ranges so that a few rows
 // (decode) still spread over the GPU; it streams its keys once for all G query heads (GQA) with
 // an online softmax in the log2 domain, and for a document also the max / sum of the keys past
-// `skip`.  A key row of hd elements is read by hd / EPL lanes (16-byte loads); lane groups merge
-// by shuffles and the 4 waves through LDS, in a fixed order.  d18_merge_kernel: one workgroup per
+// `skip`.  Scores of 16 keys x the G heads are one MFMA tile (fp16 operands split into hi + lo
+// parts, fp32 accumulation); the value sums run on the VALU in fp32; the 4 waves merge through
+// LDS in a fixed order.  d18_merge_kernel: one workgroup per
 // (row, query head, 64 output dims) merges the splits, joins each document with the own rows
 // (o_d), forms r, rmax and the routing weights, and sums w_d o_d.  Deterministic: every sum runs
 // in a fixed order.
@@ -40,10 +41,9 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 template <typename T> struct D18Elem { static constexpr int EPL = 8; };   // 16-bit keys
 template <> struct D18Elem<float> { static constexpr int EPL = 4; };
 
-// 16 bytes of T at p (16-byte aligned) as EPL fp32 values.
+// 16 bytes of T (loaded as v) as EPL fp32 values.
 template <typename T>
-__device__ __forceinline__ void load_f32(const T* p, float (&f)[D18Elem<T>::EPL]) {
-  const u32x4_t v = *reinterpret_cast<const u32x4_t*>(p);
+__device__ __forceinline__ void cvt_f32(const u32x4_t& v, float (&f)[D18Elem<T>::EPL]) {
   if constexpr (sizeof(T) == 4) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
@@ -62,161 +62,232 @@ __device__ __forceinline__ void load_f32(const T* p, float (&f)[D18Elem<T>::EPL]
   }
 }
 
+// 16 bytes of T at p (16-byte aligned) as EPL fp32 values.
+template <typename T>
+__device__ __forceinline__ void load_f32(const T* p, float (&f)[D18Elem<T>::EPL]) {
+  cvt_f32<T>(*reinterpret_cast<const u32x4_t*>(p), f);
+}
+
 // 2^(m - M) with m = -inf (an empty state) -> 0, also when M = -inf.
 __device__ __forceinline__ float rescale(float m, float M) {
   return m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
 }
 
-// LDS of one unit: per wave and query head the state (m, l, mc, lc) and the accumulator.
+typedef _Float16 d18_half8 __attribute__((ext_vector_type(8)));
+constexpr int kD18Tile = 16;   // keys per score tile (the MFMA's 16 rows)
+
+// LDS of one unit: per wave the probabilities of its current key tile [key][head] and the heads'
+// rescale factors, then per wave and query head the state (m, l, mc, lc) and the accumulator.
+constexpr int kD18KPad = 4;    // words of padding per staged row (conflict-free MFMA-layout reads)
+constexpr int kD18KRow = kD18MaxHd + kD18KPad;   // words per staged key row (fp32 keys fill it)
+// LDS of one unit: the query fragments (fp16 hi / lo rows of the 16 padded heads), per wave the
+// raw key rows of its current tile and the tile's probabilities [key][head] with the heads'
+// rescale factors, then per wave and query head the state (m, l, mc, lc) and the accumulator.
 struct D18Lds {
+  _Float16 qh[16][kD18MaxHd + 8], ql[16][kD18MaxHd + 8];
+  unsigned k[kD18PartWaves][kD18Tile][kD18KRow];
+  float p[kD18PartWaves][kD18Tile][16];
+  float alpha[kD18PartWaves][16];
   float st[kD18PartWaves][kD18MaxG][4];
   float acc[kD18PartWaves][kD18MaxG][kD18MaxHd];
 };
 
-// One key split (n keys, the first at index j_base of its unit; n <= 0: empty) for the G query
-// heads q[g * hd ...] of a kv head, hd = HD.  A key row is read by TPR = HD / EPL lanes; each lane
-// group keeps kD18Kif keys in flight (all their K / V loads issued before any is used).  Keys at
-// unit index >= skip_c (skip_c >= 0) also enter the content max / sum (mc, lc).  Writes
-// ml_out[g] = (m, l, mc, lc) (log2 domain, scores scaled by scale_log2) and acc_out[g * HD + e]
-// (unnormalised).
-constexpr int kD18Kif = 4;
+// x = hi + lo in fp16 with |x - hi - lo| <= 2^-22 |x| (for |x| in fp16's normal range).
+__device__ __forceinline__ _Float16 f16_hi(float x) { return (_Float16)x; }
+__device__ __forceinline__ _Float16 f16_lo(float x) { return (_Float16)(x - (float)(_Float16)x); }
 
+__device__ __forceinline__ void wave_sync_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// The G query rows q[g * HD ...] of a kv head, scaled to the log2 domain, into LDS as fp16
+// hi + lo rows (padded heads 0): the B operand of the scores, read by every wave.  Ends with a
+// workgroup barrier.
+template <int HD>
+__device__ __forceinline__ void stage_q(const float* __restrict__ q, int G, float scale_log2, D18Lds& lds) {
+  for (int i = threadIdx.x; i < 16 * HD; i += kD18PartThreads) {
+    const int g = i / HD, e = i % HD;
+    const float x = g < G ? q[g * HD + e] * scale_log2 : 0.f;
+    lds.qh[g][e] = f16_hi(x);
+    lds.ql[g][e] = f16_lo(x);
+  }
+  __syncthreads();
+}
+
+// One key split (n keys, the first at index j_base of its unit; n <= 0: empty) for the G query
+// heads of a kv head (staged by stage_q), hd = HD.  Wave wv takes the 16-key tiles wv, wv + 4, ...
+// Scores on the matrix cores: S^T [16 keys x 16 heads] = K_tile . Q^T with
+// v_mfma_f32_16x16x32_f16 (A = keys: lane holds key lane % 16 at dims 32 kb + 8 (lane / 16) + e;
+// B = queries: head lane % 16, same dims), q split into fp16 hi + lo (two products; fp32 keys also
+// split: three), so the scores keep fp32 accuracy.  Lane (k4 = lane / 16, head = lane % 16) then
+// holds the scores of keys 4 k4 .. 4 k4 + 3 for its head: the online softmax per head is an
+// in-lane step plus two xor shuffles, and the wave's (m, l) per head is uniform over the wave.
+// The probabilities go through LDS to the value lanes: a V row of hd elements is read by
+// TPR = HD / EPL lanes (16-byte loads), and acc[g][e] += p[key][g] v[e] in fp32.
+// A tile's K and V rows load row-contiguous (16-byte loads, TPR lanes a row): the K rows go
+// through LDS into the MFMA layout (loaded in that layout, every 16 lanes would touch 16 rows),
+// the V rows stay in registers as loaded.  Rows past n re-read row n - 1 (their scores are
+// masked).  (Loading the next tile during this one measured no faster: 18.1 against 17.4 us.)
+// Keys at unit index >= skip_c (skip_c >= 0) also enter the content max / sum (mc, lc).  Writes
+// ml_out[g] = (m, l, mc, lc) (log2 domain) and acc_out[g * HD + e] (unnormalised).
 template <typename TK, int HD, int GP>
-__device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
-                                         const TK* __restrict__ K, const TK* __restrict__ V, long long s_n,
-                                         int n, int j_base, int skip_c, float scale_log2,
-                                         float4* __restrict__ ml_out, float* __restrict__ acc_out, D18Lds& lds) {
+__device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const TK* __restrict__ V, long long s_n,
+                                         int n, int j_base, int skip_c, float4* __restrict__ ml_out,
+                                         float* __restrict__ acc_out, D18Lds& lds) {
   constexpr int EPL = D18Elem<TK>::EPL;
-  constexpr int TPR = HD / EPL;              // lanes per key row: a power of two <= 64
-  constexpr int KPW = kWave / TPR;           // keys per wave and load slot
-  constexpr int STEP = kD18PartWaves * KPW * kD18Kif;
+  constexpr int TPR = HD / EPL;              // lanes per row: a power of two <= 64
+  constexpr int KPI = kWave / TPR;           // rows per wave load
+  constexpr int NI = kD18Tile / KPI > 0 ? kD18Tile / KPI : 1;   // loads per tile (K or V)
+  constexpr int KB = HD / 32;                // MFMA k steps
+  constexpr int WPR = HD * (int)sizeof(TK) / 4;   // words per key row
+  constexpr bool kF32 = sizeof(TK) == 4;
+  static_assert(KPI <= kD18Tile, "a tile holds at least one wave load of rows");
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = threadIdx.x / kWave;
-  const int grp = lane / TPR, e0 = (lane % TPR) * EPL;
-  float qv[GP][EPL];
-  float m[GP], l[GP], mc[GP], lc[GP], acc[GP][EPL];
+  const int hs = lane % 16, k4 = lane / 16;              // score layout
+  const int grp = lane / TPR, e0 = (lane % TPR) * EPL;   // load / value layout
+  const int w0 = e0 * (int)sizeof(TK) / 4;               // this lane's first word of a row
+  float acc[GP][EPL];
 #pragma unroll
-  for (int g = 0; g < GP; ++g) {
+  for (int g = 0; g < GP; ++g)
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-      qv[g][e] = g < G ? q[g * HD + e0 + e] : 0.f;
-      acc[g][e] = 0.f;
-    }
-    m[g] = mc[g] = -INFINITY;
-    l[g] = lc[g] = 0.f;
-  }
-  // Keys j0 .. j0 + STEP - 1: issue the K / V loads of lane group grp (rows past n re-read the
-  // last row and are masked when consumed).
-  auto load_step = [&](float (&kf)[kD18Kif][EPL], float (&vf)[kD18Kif][EPL], int j0) {
-#pragma unroll
-    for (int i = 0; i < kD18Kif; ++i) {
-      const int j = j0 + (i * kD18PartWaves + wv) * KPW + grp;
-      const long long row = (long long)(j < n ? j : n - 1) * s_n + e0;   // n >= 1 here
-      load_f32<TK>(K + row, kf[i]);
-      load_f32<TK>(V + row, vf[i]);
-    }
-  };
+    for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+  float m = -INFINITY, l = 0.f, mc = -INFINITY, lc = 0.f;   // head hs
   // Content statistics of the split: none (own rows, or every key before skip_c), all (every key
   // at or past skip_c: then they equal (m, l) and are copied at the end), or per key (the split
   // that holds key skip_c).  Workgroup-uniform.
   const int cmode = skip_c < 0 || j_base + n <= skip_c ? 0 : j_base >= skip_c ? 1 : 2;
-  // The lane group's kD18Kif keys of a step enter the online softmax as one block: one max
-  // update and one rescale of the accumulator per query head.
-  auto consume_step = [&](const float (&kf)[kD18Kif][EPL], const float (&vf)[kD18Kif][EPL], int j0) {
-    float sc[kD18Kif][GP];
-    bool ok[kD18Kif], cont[kD18Kif];
+  auto load_rows = [&](const TK* base, int t0, u32x4_t (&r)[NI]) {
 #pragma unroll
-    for (int i = 0; i < kD18Kif; ++i) {
-      const int j = j0 + (i * kD18PartWaves + wv) * KPW + grp;
-      ok[i] = j < n;
-      cont[i] = ok[i] && j_base + j >= skip_c;
+    for (int i = 0; i < NI; ++i)
+      r[i] = *reinterpret_cast<const u32x4_t*>(base + (long long)min(t0 + i * KPI + grp, n - 1) * s_n + e0);
+  };
+  for (int t0 = wv * kD18Tile; t0 < n; t0 += kD18PartWaves * kD18Tile) {
+    {
+      u32x4_t kr[NI], vr[NI];
+      load_rows(K, t0, kr);
+      load_rows(V, t0, vr);
+      // The tile's K rows to LDS.
+#pragma unroll
+      for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4_t*>(&lds.k[wv][i * KPI + grp][w0]) = kr[i];
+      wave_sync_lds();
+      f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const d18_half8 qh = *reinterpret_cast<const d18_half8*>(&lds.qh[hs][32 * kb + 8 * k4]);
+        const d18_half8 ql = *reinterpret_cast<const d18_half8*>(&lds.ql[hs][32 * kb + 8 * k4]);
+        d18_half8 ka, kl;
+        if constexpr (kF32) {
+          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][32 * kb + 8 * k4]);
+          const f32x4_t b = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][32 * kb + 8 * k4 + 4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            ka[e] = f16_hi(a[e]);
+            kl[e] = f16_lo(a[e]);
+            ka[4 + e] = f16_hi(b[e]);
+            kl[4 + e] = f16_lo(b[e]);
+          }
+        } else {
+          const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(&lds.k[wv][hs][(32 * kb + 8 * k4) / 2]);
+          float f[8];
+          cvt_f32<TK>(kv, f);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ka[e] = (_Float16)f[e];
+        }
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh, sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, sc, 0, 0, 0);
+        if constexpr (kF32) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, sc, 0, 0, 0);
+      }
+      // Online softmax of head hs over the tile's keys t0 + 4 k4 + r.
+      bool ok[4];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        ok[r] = t0 + 4 * k4 + r < n;
+        if (ok[r]) mx = fmaxf(mx, sc[r]);
+      }
+      mx = fmaxf(mx, shfl_xor(mx, 16));
+      mx = fmaxf(mx, shfl_xor(mx, 32));
+      const float mn = fmaxf(m, mx);
+      const float a = rescale(m, mn);
+      float pr[4], ps = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pr[r] = ok[r] ? __builtin_amdgcn_exp2f(sc[r] - mn) : 0.f;
+        ps += pr[r];
+      }
+      ps += shfl_xor(ps, 16);
+      ps += shfl_xor(ps, 32);
+      l = l * a + ps;
+      m = mn;
+      if (cmode == 2) {
+        float mcx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) mcx = fmaxf(mcx, sc[r]);
+        mcx = fmaxf(mcx, shfl_xor(mcx, 16));
+        mcx = fmaxf(mcx, shfl_xor(mcx, 32));
+        const float mcn = fmaxf(mc, mcx);
+        float cs = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) cs += __builtin_amdgcn_exp2f(sc[r] - mcn);
+        cs += shfl_xor(cs, 16);
+        cs += shfl_xor(cs, 32);
+        lc = lc * rescale(mc, mcn) + cs;
+        mc = mcn;
+      }
+      // Probabilities and rescale factors to the value lanes.
+#pragma unroll
+      for (int r = 0; r < 4; ++r) lds.p[wv][4 * k4 + r][hs] = pr[r];
+      if (k4 == 0) lds.alpha[wv][hs] = a;
+      wave_sync_lds();
 #pragma unroll
       for (int g = 0; g < GP; ++g) {
-        float p = 0.f;
+        const float ag = lds.alpha[wv][g];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) p = fmaf(qv[g][e], kf[i][e], p);
-        sc[i][g] = group_sum<TPR>(p) * scale_log2;
+        for (int e = 0; e < EPL; ++e) acc[g][e] *= ag;
       }
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int key = i * KPI + grp;
+        float vf[EPL];
+        cvt_f32<TK>(vr[i], vf);
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+          const float pg = lds.p[wv][key][g];
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pg, vf[e], acc[g][e]);
+        }
+      }
+      wave_sync_lds();   // the next tile's keys and probabilities overwrite these
     }
-#pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      float mn = m[g];
-#pragma unroll
-      for (int i = 0; i < kD18Kif; ++i) mn = ok[i] ? fmaxf(mn, sc[i][g]) : mn;
-      const float a = rescale(m[g], mn);
-      float b[kD18Kif];
-#pragma unroll
-      for (int i = 0; i < kD18Kif; ++i) b[i] = ok[i] ? __builtin_amdgcn_exp2f(sc[i][g] - mn) : 0.f;
-      float ls = l[g] * a;
-#pragma unroll
-      for (int i = 0; i < kD18Kif; ++i) ls += b[i];
-      l[g] = ls;
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        float x = acc[g][e] * a;
-#pragma unroll
-        for (int i = 0; i < kD18Kif; ++i) x = fmaf(b[i], vf[i][e], x);
-        acc[g][e] = x;
-      }
-      m[g] = mn;
-      if (cmode == 2) {
-        float mcn = mc[g];
-#pragma unroll
-        for (int i = 0; i < kD18Kif; ++i) mcn = cont[i] ? fmaxf(mcn, sc[i][g]) : mcn;
-        float lcs = lc[g] * rescale(mc[g], mcn);
-#pragma unroll
-        for (int i = 0; i < kD18Kif; ++i) lcs += cont[i] ? __builtin_amdgcn_exp2f(sc[i][g] - mcn) : 0.f;
-        lc[g] = lcs;
-        mc[g] = mcn;
-      }
-    }
-  };
-  float kf[kD18Kif][EPL], vf[kD18Kif][EPL];
-  for (int j0 = 0; j0 < n; j0 += STEP) {
-    load_step(kf, vf, j0);
-    consume_step(kf, vf, j0);
   }
   if (cmode == 1) {
-#pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      mc[g] = m[g];
-      lc[g] = l[g];
-    }
+    mc = m;
+    lc = l;
   }
-  // Lane groups of the wave (same columns, different keys): butterfly merge.
+  // Lane groups of the wave (same dims, different keys) share the wave's state: their sums add.
 #pragma unroll
-  for (int o = TPR; o < kWave; o <<= 1) {
+  for (int o = TPR; o < kWave; o <<= 1)
 #pragma unroll
-    for (int g = 0; g < GP; ++g) {
-      const float m2 = shfl_xor(m[g], o), l2 = shfl_xor(l[g], o);
-      const float mc2 = shfl_xor(mc[g], o), lc2 = shfl_xor(lc[g], o);
-      const float M = fmaxf(m[g], m2);
-      const float a = rescale(m[g], M), b = rescale(m2, M);
+    for (int g = 0; g < GP; ++g)
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        const float acc2 = shfl_xor(acc[g][e], o);
-        acc[g][e] = acc[g][e] * a + acc2 * b;
-      }
-      l[g] = l[g] * a + l2 * b;
-      m[g] = M;
-      const float Mc = fmaxf(mc[g], mc2);
-      lc[g] = lc[g] * rescale(mc[g], Mc) + lc2 * rescale(mc2, Mc);
-      mc[g] = Mc;
-    }
-  }
+      for (int e = 0; e < EPL; ++e) acc[g][e] += shfl_xor(acc[g][e], o);
   // The 4 waves through LDS, summed in wave order.
   if (grp == 0) {
 #pragma unroll
-    for (int g = 0; g < GP; ++g) {
+    for (int g = 0; g < GP; ++g)
 #pragma unroll
       for (int e = 0; e < EPL; ++e) lds.acc[wv][g][e0 + e] = acc[g][e];
-      if (lane == 0) {
-        lds.st[wv][g][0] = m[g];
-        lds.st[wv][g][1] = l[g];
-        lds.st[wv][g][2] = mc[g];
-        lds.st[wv][g][3] = lc[g];
-      }
-    }
+  }
+  if (lane < G) {
+    lds.st[wv][lane][0] = m;
+    lds.st[wv][lane][1] = l;
+    lds.st[wv][lane][2] = mc;
+    lds.st[wv][lane][3] = lc;
   }
   __syncthreads();
   for (int i = threadIdx.x; i < G * HD; i += kD18PartThreads) {
@@ -224,10 +295,10 @@ __device__ __forceinline__ void d18_unit(const float* __restrict__ q, int G,
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kD18PartWaves; ++w) M = fmaxf(M, lds.st[w][g][0]);
-    float a = 0.f;
+    float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kD18PartWaves; ++w) a += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
-    acc_out[i] = a;
+    for (int w = 0; w < kD18PartWaves; ++w) s += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
+    acc_out[i] = s;
   }
   if ((int)threadIdx.x < G) {
     const int g = threadIdx.x;
@@ -264,21 +335,22 @@ __global__ __launch_bounds__(kD18PartThreads) void d18_partials_kernel(
   const int u = blockIdx.y / S, sp = blockIdx.y % S;
   const int G = hq / hkv;
   const long long slot = (((long long)th * (n_docs + 1) + u) * S + sp) * G;
+  // The query rows go to LDS first: they do not wait on the document offsets.
+  stage_q<HD>(u < n_docs ? qd + (((long long)u * T + t) * hq + (long long)h * G) * HD
+                         : qo + ((long long)t * hq + (long long)h * G) * HD,
+              G, scale_log2, lds);
   if (u < n_docs) {
     const int n0 = doc_ptr[u], N = doc_ptr[u + 1] - n0;
     const int chunk = (N + S - 1) / S;
     const int lo = sp * chunk, n = min(N - lo, chunk);
-    const float* q = qd + (((long long)u * T + t) * hq + (long long)h * G) * HD;
     const long long off = (long long)h * s_dh + (long long)(n0 + lo) * s_dn;
-    d18_unit<TD, HD, GP>(q, G, kd + off, vd + off, s_dn, n, lo, N > skip ? skip : 0, scale_log2, part_ml + slot,
-                     part_acc + slot * HD, lds);
+    d18_unit<TD, HD, GP>(G, kd + off, vd + off, s_dn, n, lo, N > skip ? skip : 0, part_ml + slot,
+                         part_acc + slot * HD, lds);
   } else {
     const int chunk = (P + T + S - 1) / S;
     const int lo = sp * chunk, n = min(P + t + 1 - lo, chunk);
-    const float* q = qo + ((long long)t * hq + (long long)h * G) * HD;
     const long long off = (long long)h * s_oh + (long long)lo * s_on;
-    d18_unit<float, HD, GP>(q, G, ko + off, vo + off, s_on, n, lo, -1, scale_log2, part_ml + slot,
-                        part_acc + slot * HD, lds);
+    d18_unit<float, HD, GP>(G, ko + off, vo + off, s_on, n, lo, -1, part_ml + slot, part_acc + slot * HD, lds);
   }
 }
 
