@@ -700,16 +700,29 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(2)
-    if args.workload == "prefill":
-        return bench_prefill(args)
-    if args.workload == "op_b":
-        return bench_op_b(args)
-    if args.workload == "multi_depth":
-        return bench_multi_depth(args)
-    if args.workload == "pool_build":
-        return bench_pool_build(args)
-    if args.workload == "d18":
-        return bench_d18(args)
+    fn = {"prefill": bench_prefill, "op_b": bench_op_b, "multi_depth": bench_multi_depth,
+          "pool_build": bench_pool_build, "d18": bench_d18}.get(args.workload, bench_decode)
+    fn(args)
+    if args.calibration_copy_mib > 0:
+        calibration_copy(torch.device("cuda:0"), args.calibration_copy_mib)
+
+
+def calibration_copy(dev, mib: int):
+    """Three device-to-device copies of `mib` MiB after the workload: the blit kernel
+    (`__amd_rocclr_copyBuffer`) reads and writes a known byte count, which scales the rocprofv3
+    FETCH_SIZE / WRITE_SIZE readings of the workload's kernels in the same run."""
+    n = mib * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.float16, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
+
+def bench_decode(args):
+    """Batched (or single-sequence) paged decode step: route over every chunk of each sequence's
+    Library, top-k, the paged split-K read of the routed pages and the LSE merge."""
     from kv_skill_v2_amd import ops, synth
 
     dev = torch.device("cuda:0")
@@ -786,14 +799,6 @@ def main():
     timing = "hip_graph" if graph_ok and ms_graph < ms_eager else "eager"
     ms_step = ms_graph if timing == "hip_graph" else ms_eager
 
-    if args.calibration_copy_mib > 0:
-        n = args.calibration_copy_mib * (1 << 20) // 2
-        src = torch.ones(n, dtype=torch.float16, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
     traffic = traffic_from_profile(args.workload)
     stream_meas = measured_stream_peak(dev)
 

@@ -41,7 +41,7 @@ enum {
 
 const char* xenc_strerror(int code);
 int xenc_last_hip_error(void);
-/* ABI version: bumped whenever a signature below changes. */
+/* ABI version: bumped whenever a signature or a calling contract below changes. */
 int xenc_abi_version(void);
 
 /*
@@ -378,9 +378,10 @@ int xenc_own_rows_write(int N, int hkv, int d, const void* k_new, const void* v_
  * at N_d + P + t, own rows at P + t).  Outputs w, r, rmax [hkv][G][T][D] fp32, out [T][hq][hd]
  * fp32.  Each document's keys and the own rows are read in nsplit ranges (1..32) by separate
  * workgroups and merged in order.  Limits: 1 <= D <= 64, G <= 8, hd in {32, 64, 128, 256};
- * strides multiples of 16 bytes; doc_ptr int32 [D + 1] on the device.  workspace >=
- * xenc_d18_workspace_bytes(T, hq, D, hd, nsplit) bytes of device memory (no zeroing needed).
- * Replaces the per-document loop of lib_read (xenc/d18_library.py:63-90).
+ * strides multiples of 16 bytes, row strides >= hd; doc_ptr int32 [D + 1] on the device.
+ * workspace >= xenc_d18_workspace_bytes(T, hq, D, hd, nsplit) bytes of device memory, 16-byte
+ * aligned (no zeroing needed).  Replaces the per-document loop of lib_read
+ * (xenc/d18_library.py:63-90).
  */
 size_t xenc_d18_workspace_bytes(int T, int hq, int n_docs, int hd, int nsplit);
 int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_docs, const float* qd,

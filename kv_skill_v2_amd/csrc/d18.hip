@@ -12,12 +12,17 @@
 // units being the D documents and the own rows, each cut into S key ranges so that a few rows
 // (decode) still spread over the GPU; it streams its keys once for all G query heads (GQA) with
 // an online softmax in the log2 domain, and for a document also the max / sum of the keys past
-// `skip`.  Scores of 16 keys x the G heads are one MFMA tile (fp16 operands split into hi + lo
-// parts, fp32 accumulation); the value sums run on the VALU in fp32; the 4 waves merge through
-// LDS in a fixed order.  d18_merge_kernel: one workgroup per
-// (row, query head, 64 output dims) merges the splits, joins each document with the own rows
-// (o_d), forms r, rmax and the routing weights, and sums w_d o_d.  Deterministic: every sum runs
-// in a fixed order.
+// `skip`.  Scores of 16 keys x the G heads are MFMA tiles (the query split into parts so that
+// the products keep fp32 accuracy: bf16 keys as stored against three bf16 parts of the query,
+// fp16 / fp32 keys against fp16 hi + lo); for 16-bit values P.V runs on the matrix cores too (the
+// weights split into parts the same way), for the fp32 own rows on the VALU; the running max
+// moves only by steps of more than 2^8, so most tiles skip the accumulator rescale; the 4 waves
+// merge through LDS in a fixed order.  d18_merge_kernel: one workgroup per (row, query head, 64 output dims)
+// merges the splits (each split's state and accumulator requested in one round of loads), joins
+// each document with the own rows (o_d), forms r, rmax and the routing weights, and sums
+// w_d o_d.  (Merging where the splits are produced, by the last workgroup of a unit and of a
+// row to arrive on a counter, measured slower: each level adds an L2 write-back, an atomic and
+// two rounds of loads to the critical path.)  Deterministic: every sum runs in a fixed order.
 #include <algorithm>
 
 #include "xenc_common.h"
@@ -25,15 +30,14 @@
 namespace xenc {
 namespace {
 
-constexpr int kD18Threads = 256;                      // merge kernel
+constexpr int kD18Threads = 256;   // one wave per SIMD (512 threads cap a wave at 256 registers
+                                   // and spill)
 constexpr int kD18Waves = kD18Threads / kWave;
-constexpr int kD18PartThreads = 256;                  // partials kernel (one wave per SIMD: 512 threads
-                                                      // cap a wave at 256 registers and spill)
-constexpr int kD18PartWaves = kD18PartThreads / kWave;
 constexpr int kD18MaxG = 8;
 constexpr int kD18MaxHd = 256;
 constexpr int kD18MaxDocs = 64;
 constexpr int kD18MaxSplits = 32;
+constexpr int kD18BufWord3 = 0x00020000;   // raw buffer descriptor word 3 (b128 loads ignore format)
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -62,34 +66,30 @@ __device__ __forceinline__ void cvt_f32(const u32x4_t& v, float (&f)[D18Elem<T>:
   }
 }
 
-// 16 bytes of T at p (16-byte aligned) as EPL fp32 values.
-template <typename T>
-__device__ __forceinline__ void load_f32(const T* p, float (&f)[D18Elem<T>::EPL]) {
-  cvt_f32<T>(*reinterpret_cast<const u32x4_t*>(p), f);
-}
-
 // 2^(m - M) with m = -inf (an empty state) -> 0, also when M = -inf.
 __device__ __forceinline__ float rescale(float m, float M) {
   return m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m - M);
 }
 
 typedef _Float16 d18_half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 d18_bf8 __attribute__((ext_vector_type(8)));
 constexpr int kD18Tile = 16;   // keys per score tile (the MFMA's 16 rows)
 
-// LDS of one unit: per wave the probabilities of its current key tile [key][head] and the heads'
-// rescale factors, then per wave and query head the state (m, l, mc, lc) and the accumulator.
+constexpr float kD18Lazy = 8.f;   // log2 headroom of the running max (weights <= 2^8)
 constexpr int kD18KPad = 4;    // words of padding per staged row (conflict-free MFMA-layout reads)
 constexpr int kD18KRow = kD18MaxHd + kD18KPad;   // words per staged key row (fp32 keys fill it)
-// LDS of one unit: the query fragments (fp16 hi / lo rows of the 16 padded heads), per wave the
-// raw key rows of its current tile and the tile's probabilities [key][head] with the heads'
-// rescale factors, then per wave and query head the state (m, l, mc, lc) and the accumulator.
+
+// LDS of a partials workgroup: the query fragments (the parts of the 16 padded heads' rows: bf16
+// keys three bf16 parts, other keys fp16 hi / lo), per wave the raw key (and 16-bit value) rows of
+// its current tile and the tile's probabilities [key][head] with the heads' rescale factors, then
+// per wave and query head the state (m, l, mc, lc) and the accumulator.
 struct D18Lds {
-  _Float16 qh[16][kD18MaxHd + 8], ql[16][kD18MaxHd + 8];
-  unsigned k[kD18PartWaves][kD18Tile][kD18KRow];
-  float p[kD18PartWaves][kD18Tile][16];
-  float alpha[kD18PartWaves][16];
-  float st[kD18PartWaves][kD18MaxG][4];
-  float acc[kD18PartWaves][kD18MaxG][kD18MaxHd];
+  unsigned short q[3][16][kD18MaxHd + 8];
+  unsigned k[kD18Waves][kD18Tile][kD18KRow];
+  float p[kD18Waves][kD18Tile][16];
+  float alpha[kD18Waves][16];
+  float st[kD18Waves][kD18MaxG][4];
+  float acc[kD18Waves][kD18MaxG][kD18MaxHd];
 };
 
 // x = hi + lo in fp16 with |x - hi - lo| <= 2^-22 |x| (for |x| in fp16's normal range).
@@ -102,22 +102,78 @@ __device__ __forceinline__ void wave_sync_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// The G query rows q[g * HD ...] of a kv head, scaled to the log2 domain, into LDS as fp16
-// hi + lo rows (padded heads 0): the B operand of the scores, read by every wave.  Ends with a
-// workgroup barrier.
+struct D18Args {
+  int T, hq, hkv, n_docs, S, P, skip, top_k, force;
+  float scale_log2, beta;
+  const float* qd;
+  const float* qo;
+  const void* kd;
+  const void* vd;
+  long long s_dh, s_dn;
+  const float* ko;
+  const float* vo;
+  long long s_oh, s_on;
+  const float* wfix;
+  f32x4_t* part_ml;      // [T][hkv][D + 1][S][G] (m, l, mc, lc)
+  float* part_acc;       // [T][hkv][D + 1][S][G][hd]
+  float* out;            // [T][hq][hd]
+  float* w;              // w, r, rmax: [hkv][G][T][D]
+  float* r;
+  float* rmax;
+};
+
+// The query rows of the 16 padded heads: thread x holds q[g][e] for i = j * 256 + x (g = i / HD,
+// e = i % HD); heads past G hold a copy of head G - 1 (store_q writes them as 0).
+template <int HD> constexpr int kQPer = 16 * HD / kD18Threads;
+
 template <int HD>
-__device__ __forceinline__ void stage_q(const float* __restrict__ q, int G, float scale_log2, D18Lds& lds) {
-  for (int i = threadIdx.x; i < 16 * HD; i += kD18PartThreads) {
+__device__ __forceinline__ void load_q(const float* __restrict__ q, int G, float (&qv)[kQPer<HD>]) {
+#pragma unroll
+  for (int j = 0; j < kQPer<HD>; ++j) {
+    const int i = j * kD18Threads + threadIdx.x;
     const int g = i / HD, e = i % HD;
-    const float x = g < G ? q[g * HD + e] * scale_log2 : 0.f;
-    lds.qh[g][e] = f16_hi(x);
-    lds.ql[g][e] = f16_lo(x);
+    qv[j] = q[min(g, G - 1) * HD + e];   // unconditional: the loads issue back to back
   }
-  __syncthreads();
+}
+
+// The query rows, scaled to the log2 domain, into LDS (heads past G: 0): the B operand of the
+// scores, read by every wave.  For bf16 keys three bf16 parts (q = p0 + p1 + p2 to 2^-24 |q|), so
+// the bf16 keys enter the matrix cores as stored; for fp16 / fp32 keys fp16 hi + lo.
+template <typename TK, int HD>
+__device__ __forceinline__ void store_q(const float (&qv)[kQPer<HD>], int G, float scale_log2, D18Lds& lds) {
+#pragma unroll
+  for (int j = 0; j < kQPer<HD>; ++j) {
+    const int i = j * kD18Threads + threadIdx.x;
+    const int g = i / HD, e = i % HD;
+    const float x = g < G ? qv[j] * scale_log2 : 0.f;
+    if constexpr (__is_same(TK, __bf16)) {
+      const __bf16 p0 = (__bf16)x;
+      const float r1 = x - (float)p0;
+      const __bf16 p1 = (__bf16)r1;
+      lds.q[0][g][e] = __builtin_bit_cast(unsigned short, p0);
+      lds.q[1][g][e] = __builtin_bit_cast(unsigned short, p1);
+      lds.q[2][g][e] = __builtin_bit_cast(unsigned short, (__bf16)(r1 - (float)p1));
+    } else {
+      lds.q[0][g][e] = __builtin_bit_cast(unsigned short, f16_hi(x));
+      lds.q[1][g][e] = __builtin_bit_cast(unsigned short, f16_lo(x));
+    }
+  }
+}
+
+// Buffer descriptor over the rows t0 .. t0 + 15 of a split of n rows (row stride s_n elements):
+// loads past its last row return 0 without touching memory (none at all when t0 >= n).
+template <typename TK, int HD>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const TK* base, long long s_n, int t0, int n) {
+  const int nt = min(n - t0, kD18Tile);
+  const int bytes = nt > 0 ? (int)(((long long)(nt - 1) * s_n + HD) * (long long)sizeof(TK)) : 0;
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<TK*>(base + (long long)max(t0, 0) * s_n), 0, bytes,
+                                           kD18BufWord3);
 }
 
 // One key split (n keys, the first at index j_base of its unit; n <= 0: empty) for the G query
-// heads of a kv head (staged by stage_q), hd = HD.  Wave wv takes the 16-key tiles wv, wv + 4, ...
+// heads of a kv head (query rows q [G][HD]), hd = HD.  Wave wv takes the 16-key tiles wv, wv + 4,
+// ...  The first tile's K and V rows and the query rows are requested together, so the query's
+// latency overlaps the keys'; with 16-bit rows the second tile's rows are requested too.
 // Scores on the matrix cores: S^T [16 keys x 16 heads] = K_tile . Q^T with
 // v_mfma_f32_16x16x32_f16 (A = keys: lane holds key lane % 16 at dims 32 kb + 8 (lane / 16) + e;
 // B = queries: head lane % 16, same dims), q split into fp16 hi + lo (two products; fp32 keys also
@@ -126,62 +182,81 @@ __device__ __forceinline__ void stage_q(const float* __restrict__ q, int G, floa
 // in-lane step plus two xor shuffles, and the wave's (m, l) per head is uniform over the wave.
 // The probabilities go through LDS to the value lanes: a V row of hd elements is read by
 // TPR = HD / EPL lanes (16-byte loads), and acc[g][e] += p[key][g] v[e] in fp32.
-// A tile's K and V rows load row-contiguous (16-byte loads, TPR lanes a row): the K rows go
+// A tile's K and V rows load row-contiguous (16-byte buffer loads, TPR lanes a row): the K rows go
 // through LDS into the MFMA layout (loaded in that layout, every 16 lanes would touch 16 rows),
-// the V rows stay in registers as loaded.  Rows past n re-read row n - 1 (their scores are
-// masked).  (Loading the next tile during this one measured no faster: 18.1 against 17.4 us.)
-// Keys at unit index >= skip_c (skip_c >= 0) also enter the content max / sum (mc, lc).  Writes
-// ml_out[g] = (m, l, mc, lc) (log2 domain) and acc_out[g * HD + e] (unnormalised).
+// the V rows stay in registers as loaded.  Rows past n re-read the split's last row (their scores
+// are masked).  Keys at unit index >= skip_c (skip_c >= 0) also enter the content max / sum
+// (mc, lc).  Writes ml_out[g] = (m, l, mc, lc) (log2 domain) and acc_out[g * HD + e]
+// (unnormalised).  Ends with the query rows staged and every wave past the tiles.
 template <typename TK, int HD, int GP>
 __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const TK* __restrict__ V, long long s_n,
-                                         int n, int j_base, int skip_c, float4* __restrict__ ml_out,
+                                         int n, int j_base, int skip_c, const float* __restrict__ q,
+                                         float scale_log2, f32x4_t* __restrict__ ml_out,
                                          float* __restrict__ acc_out, D18Lds& lds) {
   constexpr int EPL = D18Elem<TK>::EPL;
   constexpr int TPR = HD / EPL;              // lanes per row: a power of two <= 64
   constexpr int KPI = kWave / TPR;           // rows per wave load
   constexpr int NI = kD18Tile / KPI > 0 ? kD18Tile / KPI : 1;   // loads per tile (K or V)
   constexpr int KB = HD / 32;                // MFMA k steps
-  constexpr int WPR = HD * (int)sizeof(TK) / 4;   // words per key row
   constexpr bool kF32 = sizeof(TK) == 4;
+  constexpr bool kPvMfma = !kF32;            // 16-bit values: P.V on the matrix cores
   static_assert(KPI <= kD18Tile, "a tile holds at least one wave load of rows");
   const int lane = threadIdx.x & (kWave - 1);
-  const int wv = threadIdx.x / kWave;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int hs = lane % 16, k4 = lane / 16;              // score layout
   const int grp = lane / TPR, e0 = (lane % TPR) * EPL;   // load / value layout
   const int w0 = e0 * (int)sizeof(TK) / 4;               // this lane's first word of a row
-  float acc[GP][EPL];
+  float acc[GP][EPL];       // VALU P.V: heads x this lane's EPL dims
+  f32x4_t accm[HD / 16];    // MFMA P.V: block b, heads 4 k4 .. + 3 at dim 32 (b / 2) + 2 hs + b % 2
 #pragma unroll
   for (int g = 0; g < GP; ++g)
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[g][e] = 0.f;
+#pragma unroll
+  for (int b = 0; b < HD / 16; ++b) accm[b] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f, mc = -INFINITY, lc = 0.f;   // head hs
+  float mt = -INFINITY;   // the exact max of head hs's scores (m trails it by < 2^8)
   // Content statistics of the split: none (own rows, or every key before skip_c), all (every key
   // at or past skip_c: then they equal (m, l) and are copied at the end), or per key (the split
   // that holds key skip_c).  Workgroup-uniform.
   const int cmode = skip_c < 0 || j_base + n <= skip_c ? 0 : j_base >= skip_c ? 1 : 2;
+  // Rows t0 .. t0 + 15 (clamped to the tile's last row); unconditional, in bounds by the descriptor.
   auto load_rows = [&](const TK* base, int t0, u32x4_t (&r)[NI]) {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc<TK, HD>(base, s_n, t0, n);
+    const int last = max(min(n - t0, kD18Tile) - 1, 0);
 #pragma unroll
-    for (int i = 0; i < NI; ++i)
-      r[i] = *reinterpret_cast<const u32x4_t*>(base + (long long)min(t0 + i * KPI + grp, n - 1) * s_n + e0);
+    for (int i = 0; i < NI; ++i) {
+      const unsigned off = (unsigned)(((long long)min(i * KPI + grp, last) * s_n + e0) * (long long)sizeof(TK));
+      r[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, 0);
+    }
   };
-  for (int t0 = wv * kD18Tile; t0 < n; t0 += kD18PartWaves * kD18Tile) {
-    {
-      u32x4_t kr[NI], vr[NI];
-      load_rows(K, t0, kr);
-      load_rows(V, t0, vr);
-      // The tile's K rows to LDS.
+  // One 16-key tile (its K and V rows in kr, vr; keys t0 .. t0 + 15 of the split).
+  auto tile = [&](const u32x4_t (&kr)[NI], const u32x4_t (&vr)[NI], int t0) {
+    // The tile's K rows to LDS (16-bit keys: the V rows beside them, words HD / 2 .. HD - 1).
 #pragma unroll
-      for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4_t*>(&lds.k[wv][i * KPI + grp][w0]) = kr[i];
-      wave_sync_lds();
-      f32x4_t sc = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4_t*>(&lds.k[wv][i * KPI + grp][w0]) = kr[i];
+    if constexpr (kPvMfma) {
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const d18_half8 qh = *reinterpret_cast<const d18_half8*>(&lds.qh[hs][32 * kb + 8 * k4]);
-        const d18_half8 ql = *reinterpret_cast<const d18_half8*>(&lds.ql[hs][32 * kb + 8 * k4]);
-        d18_half8 ka, kl;
+      for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4_t*>(&lds.k[wv][i * KPI + grp][HD / 2 + w0]) = vr[i];
+    }
+    wave_sync_lds();
+    // One accumulator per product, so the MFMA chains are independent; summed at the end.
+    f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = s0, s2 = s0;
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      const int qo = 32 * kb + 8 * k4;
+      if constexpr (__is_same(TK, __bf16)) {
+        const d18_bf8 kv = *reinterpret_cast<const d18_bf8*>(&lds.k[wv][hs][qo / 2]);
+        s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, *reinterpret_cast<const d18_bf8*>(&lds.q[0][hs][qo]), s0, 0, 0, 0);
+        s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, *reinterpret_cast<const d18_bf8*>(&lds.q[1][hs][qo]), s1, 0, 0, 0);
+        s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, *reinterpret_cast<const d18_bf8*>(&lds.q[2][hs][qo]), s2, 0, 0, 0);
+      } else {
+        const d18_half8 qh = *reinterpret_cast<const d18_half8*>(&lds.q[0][hs][qo]);
+        const d18_half8 ql = *reinterpret_cast<const d18_half8*>(&lds.q[1][hs][qo]);
         if constexpr (kF32) {
-          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][32 * kb + 8 * k4]);
-          const f32x4_t b = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][32 * kb + 8 * k4 + 4]);
+          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][qo]);
+          const f32x4_t b = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][qo + 4]);
+          d18_half8 ka, kl;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             ka[e] = f16_hi(a[e]);
@@ -189,66 +264,138 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
             ka[4 + e] = f16_hi(b[e]);
             kl[4 + e] = f16_lo(b[e]);
           }
+          s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh, s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, s1, 0, 0, 0);
+          s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, s2, 0, 0, 0);
         } else {
-          const u32x4_t kv = *reinterpret_cast<const u32x4_t*>(&lds.k[wv][hs][(32 * kb + 8 * k4) / 2]);
-          float f[8];
-          cvt_f32<TK>(kv, f);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) ka[e] = (_Float16)f[e];
+          const d18_half8 ka = *reinterpret_cast<const d18_half8*>(&lds.k[wv][hs][qo / 2]);
+          s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh, s0, 0, 0, 0);
+          s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, s1, 0, 0, 0);
         }
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh, sc, 0, 0, 0);
-        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, sc, 0, 0, 0);
-        if constexpr (kF32) sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, sc, 0, 0, 0);
       }
-      // Online softmax of head hs over the tile's keys t0 + 4 k4 + r.
-      bool ok[4];
-      float mx = -INFINITY;
+    }
+    const f32x4_t sc = (s0 + s1) + s2;
+    // Online softmax of head hs over the tile's keys t0 + 4 k4 + r.
+    bool ok[4];
+    float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        ok[r] = t0 + 4 * k4 + r < n;
-        if (ok[r]) mx = fmaxf(mx, sc[r]);
+    for (int r = 0; r < 4; ++r) {
+      ok[r] = t0 + 4 * k4 + r < n;
+      if (ok[r]) mx = fmaxf(mx, sc[r]);
+    }
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    // The running max moves only when the tile's max passes it by more than 2^8: the weights stay
+    // <= 256 and most tiles need no rescale of the accumulators (the state (m, l, acc) stays exact:
+    // a rescale is a power of two).
+    const float mn = mx > m + kD18Lazy ? mx : m;
+    mt = fmaxf(mt, mx);
+    const float a = rescale(m, mn);
+    const bool any_rescale = __ballot(m != -INFINITY && mn != m) != 0;   // wave-uniform
+    float pr[4], ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pr[r] = ok[r] ? __builtin_amdgcn_exp2f(sc[r] - mn) : 0.f;
+      ps += pr[r];
+    }
+    ps += shfl_xor(ps, 16);
+    ps += shfl_xor(ps, 32);
+    l = l * a + ps;
+    m = mn;
+    if (cmode == 2) {
+      float mcx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) mcx = fmaxf(mcx, sc[r]);
+      mcx = fmaxf(mcx, shfl_xor(mcx, 16));
+      mcx = fmaxf(mcx, shfl_xor(mcx, 32));
+      const float mcn = fmaxf(mc, mcx);
+      float cs = 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) cs += __builtin_amdgcn_exp2f(sc[r] - mcn);
+      cs += shfl_xor(cs, 16);
+      cs += shfl_xor(cs, 32);
+      lc = lc * rescale(mc, mcn) + cs;
+      mc = mcn;
+    }
+    if constexpr (kPvMfma) {
+      // P.V on the matrix cores, v_mfma_f32_16x16x32 (lane l: A row l % 16, B column l % 16, k
+      // slots 8 (l / 16) .. + 7): D[head][dim] += sum_k A[head][k] B[k][dim].  This lane's p (head
+      // hs, keys 4 k4 + r) fill its A slots as the parts of p: bf16 values [hi, mid] and [lo, 0]
+      // (two products, 24 bits of p), fp16 values [hi, lo] (one, 22 bits); the B slots carry the
+      // same 4 keys' V at the lane's dim twice.  The 32 dims of pair c are read as 16-bit pairs:
+      // lane hs takes dims 32 c + 2 hs (block 2 c) and 32 c + 2 hs + 1 (block 2 c + 1).  D lane l:
+      // heads 4 (l / 16) + r.
+      if (any_rescale) {
+        if (k4 == 0) lds.alpha[wv][hs] = a;
+        wave_sync_lds();
+        float al[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) al[r] = lds.alpha[wv][4 * k4 + r];
+#pragma unroll
+        for (int b = 0; b < HD / 16; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) accm[b][r] *= al[r];
       }
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
-      const float mn = fmaxf(m, mx);
-      const float a = rescale(m, mn);
-      float pr[4], ps = 0.f;
+      u32x4_t a1, a2;   // the A operand parts as packed 16-bit pairs
+      if constexpr (__is_same(TK, __bf16)) {
+        unsigned hi[4], mid[4], lo[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pr[r] = ok[r] ? __builtin_amdgcn_exp2f(sc[r] - mn) : 0.f;
-        ps += pr[r];
+        for (int r = 0; r < 4; ++r) {
+          const __bf16 h = (__bf16)pr[r];
+          const float rem = pr[r] - (float)h;
+          const __bf16 md = (__bf16)rem;
+          hi[r] = __builtin_bit_cast(unsigned short, h);
+          mid[r] = __builtin_bit_cast(unsigned short, md);
+          lo[r] = __builtin_bit_cast(unsigned short, (__bf16)(rem - (float)md));
+        }
+        a1 = u32x4_t{hi[0] | hi[1] << 16, hi[2] | hi[3] << 16, mid[0] | mid[1] << 16, mid[2] | mid[3] << 16};
+        a2 = u32x4_t{lo[0] | lo[1] << 16, lo[2] | lo[3] << 16, 0u, 0u};
+      } else {
+        unsigned hi[4], lo[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          hi[r] = __builtin_bit_cast(unsigned short, f16_hi(pr[r]));
+          lo[r] = __builtin_bit_cast(unsigned short, f16_lo(pr[r]));
+        }
+        a1 = u32x4_t{hi[0] | hi[1] << 16, hi[2] | hi[3] << 16, lo[0] | lo[1] << 16, lo[2] | lo[3] << 16};
       }
-      ps += shfl_xor(ps, 16);
-      ps += shfl_xor(ps, 32);
-      l = l * a + ps;
-      m = mn;
-      if (cmode == 2) {
-        float mcx = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) mcx = fmaxf(mcx, sc[r]);
-        mcx = fmaxf(mcx, shfl_xor(mcx, 16));
-        mcx = fmaxf(mcx, shfl_xor(mcx, 32));
-        const float mcn = fmaxf(mc, mcx);
-        float cs = 0.f;
+      for (int c = 0; c < HD / 32; ++c) {
+        unsigned w[4];   // keys 4 k4 + r, dims 32 c + 2 hs (low half) and + 1 (high half)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) cs += __builtin_amdgcn_exp2f(sc[r] - mcn);
-        cs += shfl_xor(cs, 16);
-        cs += shfl_xor(cs, 32);
-        lc = lc * rescale(mc, mcn) + cs;
-        mc = mcn;
+        for (int r = 0; r < 4; ++r) w[r] = lds.k[wv][4 * k4 + r][HD / 2 + 16 * c + hs];
+        const unsigned ev01 = (w[0] & 0xffffu) | (w[1] << 16), ev23 = (w[2] & 0xffffu) | (w[3] << 16);
+        const unsigned od01 = (w[0] >> 16) | (w[1] & 0xffff0000u), od23 = (w[2] >> 16) | (w[3] & 0xffff0000u);
+        const u32x4_t be = {ev01, ev23, ev01, ev23}, bo = {od01, od23, od01, od23};
+        if constexpr (__is_same(TK, __bf16)) {
+          const d18_bf8 x1 = __builtin_bit_cast(d18_bf8, a1), x2 = __builtin_bit_cast(d18_bf8, a2);
+          const d18_bf8 ye = __builtin_bit_cast(d18_bf8, be), yo = __builtin_bit_cast(d18_bf8, bo);
+          accm[2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, ye, accm[2 * c], 0, 0, 0);
+          accm[2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x1, yo, accm[2 * c + 1], 0, 0, 0);
+          accm[2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, ye, accm[2 * c], 0, 0, 0);
+          accm[2 * c + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(x2, yo, accm[2 * c + 1], 0, 0, 0);
+        } else {
+          const d18_half8 x1 = __builtin_bit_cast(d18_half8, a1);
+          accm[2 * c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, __builtin_bit_cast(d18_half8, be), accm[2 * c], 0, 0, 0);
+          accm[2 * c + 1] =
+              __builtin_amdgcn_mfma_f32_16x16x32_f16(x1, __builtin_bit_cast(d18_half8, bo), accm[2 * c + 1], 0, 0, 0);
+        }
       }
+    } else {
       // Probabilities and rescale factors to the value lanes.
 #pragma unroll
       for (int r = 0; r < 4; ++r) lds.p[wv][4 * k4 + r][hs] = pr[r];
       if (k4 == 0) lds.alpha[wv][hs] = a;
       wave_sync_lds();
+      if (any_rescale) {
 #pragma unroll
-      for (int g = 0; g < GP; ++g) {
-        const float ag = lds.alpha[wv][g];
+        for (int g = 0; g < GP; ++g) {
+          const float ag = lds.alpha[wv][g];
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) acc[g][e] *= ag;
+          for (int e = 0; e < EPL; ++e) acc[g][e] *= ag;
+        }
       }
 #pragma unroll
       for (int i = 0; i < NI; ++i) {
@@ -262,27 +409,84 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
           for (int e = 0; e < EPL; ++e) acc[g][e] = fmaf(pg, vf[e], acc[g][e]);
         }
       }
-      wave_sync_lds();   // the next tile's keys and probabilities overwrite these
+    }
+    wave_sync_lds();   // the next tile's keys and probabilities overwrite these
+  };
+  constexpr int kStep = kD18Waves * kD18Tile;   // a wave's next tile
+  const int t_first = wv * kD18Tile;
+  float qv[kQPer<HD>];
+  if constexpr (!kF32) {
+    // 16-bit rows: two tiles in registers, the next one loading while this one computes (loads
+    // past the split return 0 and touch no memory, so every load is unconditional).  The query
+    // loads go between the two tiles' loads, so staging the query waits for the first tile only.
+    u32x4_t k0[NI], v0[NI], k1[NI], v1[NI];
+    load_rows(K, t_first, k0);
+    load_rows(V, t_first, v0);
+    load_q<HD>(q, G, qv);
+    load_rows(K, t_first + kStep, k1);
+    load_rows(V, t_first + kStep, v1);
+    store_q<TK, HD>(qv, G, scale_log2, lds);
+    __syncthreads();
+    if (n <= t_first + 2 * kStep) {
+      // At most two tiles for this wave (a decode-sized split): straight-line code, so the wait
+      // for the second tile's loads comes only before the second tile (in a loop the back edge
+      // would make the first tile wait for both).
+      if (t_first < n) tile(k0, v0, t_first);
+      if (t_first + kStep < n) tile(k1, v1, t_first + kStep);
+    } else {
+      for (int t0 = t_first; t0 < n; t0 += 2 * kStep) {
+        tile(k0, v0, t0);
+        load_rows(K, t0 + 2 * kStep, k0);
+        load_rows(V, t0 + 2 * kStep, v0);
+        if (t0 + kStep >= n) break;
+        tile(k1, v1, t0 + kStep);
+        load_rows(K, t0 + 3 * kStep, k1);
+        load_rows(V, t0 + 3 * kStep, v1);
+      }
+    }
+  } else {
+    u32x4_t kr[NI], vr[NI];
+    load_rows(K, t_first, kr);
+    load_rows(V, t_first, vr);
+    load_q<HD>(q, G, qv);
+    store_q<TK, HD>(qv, G, scale_log2, lds);
+    __syncthreads();
+    for (int t0 = t_first; t0 < n; t0 += kStep) {
+      if (t0 != t_first) {
+        load_rows(K, t0, kr);
+        load_rows(V, t0, vr);
+      }
+      tile(kr, vr, t0);
     }
   }
-  if (cmode == 1) {
-    mc = m;
-    lc = l;
+  if (cmode == 1) {   // every key counts: the content max is the exact max, l rescaled to it
+    mc = mt;
+    lc = l * rescale(m, mt);
   }
-  // Lane groups of the wave (same dims, different keys) share the wave's state: their sums add.
+  if constexpr (kPvMfma) {
+    // The MFMA sums cover every key of the wave: heads 4 k4 + r (those < G) to LDS.
 #pragma unroll
-  for (int o = TPR; o < kWave; o <<= 1)
+    for (int r = 0; r < 4; ++r)
+      if (4 * k4 + r < G) {
 #pragma unroll
-    for (int g = 0; g < GP; ++g)
+        for (int b = 0; b < HD / 16; ++b) lds.acc[wv][4 * k4 + r][32 * (b / 2) + 2 * hs + (b % 2)] = accm[b][r];
+      }
+  } else {
+    // Lane groups of the wave (same dims, different keys) share the wave's state: their sums add.
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) acc[g][e] += shfl_xor(acc[g][e], o);
+    for (int o = TPR; o < kWave; o <<= 1)
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[g][e] += shfl_xor(acc[g][e], o);
+    if (grp == 0) {
+#pragma unroll
+      for (int g = 0; g < GP; ++g)
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) lds.acc[wv][g][e0 + e] = acc[g][e];
+    }
+  }
   // The 4 waves through LDS, summed in wave order.
-  if (grp == 0) {
-#pragma unroll
-    for (int g = 0; g < GP; ++g)
-#pragma unroll
-      for (int e = 0; e < EPL; ++e) lds.acc[wv][g][e0 + e] = acc[g][e];
-  }
   if (lane < G) {
     lds.st[wv][lane][0] = m;
     lds.st[wv][lane][1] = l;
@@ -290,192 +494,189 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
     lds.st[wv][lane][3] = lc;
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < G * HD; i += kD18PartThreads) {
+  for (int i = threadIdx.x; i < G * HD; i += kD18Threads) {
     const int g = i / HD, e = i % HD;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kD18PartWaves; ++w) M = fmaxf(M, lds.st[w][g][0]);
+    for (int w = 0; w < kD18Waves; ++w) M = fmaxf(M, lds.st[w][g][0]);
     float s = 0.f;
 #pragma unroll
-    for (int w = 0; w < kD18PartWaves; ++w) s += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
+    for (int w = 0; w < kD18Waves; ++w) s += lds.acc[w][g][e] * rescale(lds.st[w][g][0], M);
     acc_out[i] = s;
   }
   if ((int)threadIdx.x < G) {
     const int g = threadIdx.x;
     float M = -INFINITY, Mc = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kD18PartWaves; ++w) {
+    for (int w = 0; w < kD18Waves; ++w) {
       M = fmaxf(M, lds.st[w][g][0]);
       Mc = fmaxf(Mc, lds.st[w][g][2]);
     }
     float L = 0.f, Lc = 0.f;
 #pragma unroll
-    for (int w = 0; w < kD18PartWaves; ++w) {
+    for (int w = 0; w < kD18Waves; ++w) {
       L += lds.st[w][g][1] * rescale(lds.st[w][g][0], M);
       Lc += lds.st[w][g][3] * rescale(lds.st[w][g][2], Mc);
     }
-    ml_out[g] = make_float4(M, L, Mc, Lc);
+    ml_out[g] = f32x4_t{M, L, Mc, Lc};
   }
 }
 
-// Partials of split s of unit u of (row t, kv head h), blockIdx = (t * hkv + h, u * S + s); u < D
-// a document (keys split into S ranges of ceil(N_d / S)), u = D the own rows (S ranges of
-// ceil((P + T) / S), cut at row t's causal end P + t + 1).  Layout: part_ml [T][hkv][D + 1][S][G],
-// part_acc [T][hkv][D + 1][S][G][hd].
-template <typename TD, int HD, int GP>
-__global__ __launch_bounds__(kD18PartThreads) void d18_partials_kernel(
-    int hq, int hkv, int n_docs, int S, const float* __restrict__ qd, const float* __restrict__ qo,
-    const TD* __restrict__ kd, const TD* __restrict__ vd, long long s_dh, long long s_dn,
-    const int* __restrict__ doc_ptr, const float* __restrict__ ko, const float* __restrict__ vo,
-    long long s_oh, long long s_on, int P, int T, float scale_log2, int skip,
-    float4* __restrict__ part_ml, float* __restrict__ part_acc) {
-  __shared__ D18Lds lds;
-  const int th = blockIdx.x;
-  const int t = th / hkv, h = th % hkv;
-  const int u = blockIdx.y / S, sp = blockIdx.y % S;
-  const int G = hq / hkv;
-  const long long slot = (((long long)th * (n_docs + 1) + u) * S + sp) * G;
-  // The query rows go to LDS first: they do not wait on the document offsets.
-  stage_q<HD>(u < n_docs ? qd + (((long long)u * T + t) * hq + (long long)h * G) * HD
-                         : qo + ((long long)t * hq + (long long)h * G) * HD,
-              G, scale_log2, lds);
-  if (u < n_docs) {
-    const int n0 = doc_ptr[u], N = doc_ptr[u + 1] - n0;
-    const int chunk = (N + S - 1) / S;
-    const int lo = sp * chunk, n = min(N - lo, chunk);
-    const long long off = (long long)h * s_dh + (long long)(n0 + lo) * s_dn;
-    d18_unit<TD, HD, GP>(G, kd + off, vd + off, s_dn, n, lo, N > skip ? skip : 0, part_ml + slot,
-                         part_acc + slot * HD, lds);
-  } else {
-    const int chunk = (P + T + S - 1) / S;
-    const int lo = sp * chunk, n = min(P + t + 1 - lo, chunk);
-    const long long off = (long long)h * s_oh + (long long)lo * s_on;
-    d18_unit<float, HD, GP>(G, ko + off, vo + off, s_on, n, lo, -1, part_ml + slot, part_acc + slot * HD, lds);
+// Routing weight of document d (lane d; has = d < D) from r: one-hot at force, wfix, or the
+// softmax of beta * r over the top_k largest (ties to the lower index, ranked over 64-bit order
+// keys as the routing top-k does).  Called by whole waves.
+__device__ __forceinline__ float doc_weight(float r, bool has, int d, int D, float beta, int top_k, int force,
+                                            const float* __restrict__ wfix) {
+  if (force >= 0) return d == force ? 1.f : 0.f;
+  if (wfix) return has ? wfix[d] : 0.f;
+  const float logit = beta * r;
+  bool keep = has;
+  if (top_k > 0 && top_k < D) {
+    const unsigned long long key = has ? ((unsigned long long)order_key(logit) << 32) | (unsigned)~d : 0ull;
+    const unsigned hi = (unsigned)(key >> 32), lo = (unsigned)key;
+    int rank = 0;
+    for (int j = 0; j < D; ++j) {
+      const unsigned long long kj =
+          ((unsigned long long)(unsigned)__shfl((int)hi, j) << 32) | (unsigned)__shfl((int)lo, j);
+      rank += kj > key ? 1 : 0;
+    }
+    keep = has && rank < top_k;
   }
+  const float mx = wave_max(keep ? logit : -INFINITY);
+  const float e = keep ? expf(logit - mx) : 0.f;
+  return e / wave_sum(e);
+}
+
+// The S splits of unit u for query head g and the 64 dims of this lane's block: lane s < S holds
+// split s's state, lane e the S accumulator values of dim ec (all requested in one round).  The
+// unit's max M, the factors 2^(m_s - M) and the sums L, Lc come from wave reductions (a fixed
+// tree); the accumulator sums its splits in split order with the factors read back by readlane.
+struct D18UnitLoad {
+  f32x4_t st;
+  float v[kD18MaxSplits];
+};
+struct D18UnitSum {
+  f32x4_t st;   // (M, L, Mc, Lc), uniform over the wave
+  float acc;    // this lane's dim
+};
+
+__device__ __forceinline__ void load_unit(const D18Args& A, long long slot0, int G, int hd, int ec, int lane,
+                                          D18UnitLoad& L) {
+  const int S = A.S;   // split s at slot0 + s * G
+  L.st = lane < S ? A.part_ml[slot0 + (long long)lane * G] : f32x4_t{-INFINITY, 0.f, -INFINITY, 0.f};
+#pragma unroll
+  for (int s = 0; s < kD18MaxSplits; ++s)
+    L.v[s] = s < S ? A.part_acc[(slot0 + (long long)s * G) * hd + ec] : 0.f;
+}
+
+__device__ __forceinline__ D18UnitSum reduce_unit(const D18UnitLoad& L, int S) {
+  const float M = wave_max(L.st[0]), Mc = wave_max(L.st[2]);
+  const float f = rescale(L.st[0], M);
+  D18UnitSum r;
+  r.st = f32x4_t{M, wave_sum(L.st[1] * f), Mc, wave_sum(L.st[3] * rescale(L.st[2], Mc))};
+  float a = 0.f;
+#pragma unroll
+  for (int s = 0; s < kD18MaxSplits; ++s)
+    if (s < S) a = fmaf(L.v[s], readlane(f, s), a);
+  r.acc = a;
+  return r;
 }
 
 // One workgroup per (row t, kv head h, query head g) and block of 64 output dims:
-// blockIdx.x = (t * hkv + h) * G + g, blockIdx.y = dim block.  The S splits of every unit are
-// merged first (in split order): their rescale factors and the unit states go to LDS.  Wave 0
-// forms the routing weights (one lane per document; block 0 writes w, r, rmax).  Then wave v
-// merges the split accumulators of units v, v + 4, ... for the block's dims (lane = dim, all S
-// loads of two units in flight) into LDS, and wave 0 sums o[e] = sum_d w_d o_d[e], o_d the join
-// of document d and the own rows.
-// w, r, rmax: [hkv][G][T][D] (the reference's [Hkv, G, T, D]); out: [T][hq][hd].
+// blockIdx.x = (t * hkv + h) * G + g, blockIdx.y = dim block.  Wave v merges the splits of units
+// v, v + 4, ... (load_unit / reduce_unit) into LDS; wave 0 then forms r, rmax and the routing weights (one lane
+// per document; block 0 writes w, r, rmax) and sums o[e] = sum_d w_d o_d[e], o_d the join of
+// document d and the own rows: o_d = (a_d acc_d + b_d acc_own) / (a_d L_d + b_d L_own) with
+// a_d = 2^(M_d - M), b_d = 2^(M_own - M), M = max(M_d, M_own).
 constexpr int kD18MergeDims = kWave;
 
-__global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(
-    int T, int hq, int hkv, int hd, int n_docs, int S, const float4* __restrict__ part_ml,
-    const float* __restrict__ part_acc, float beta, int top_k, int force, const float* __restrict__ wfix,
-    float* __restrict__ out, float* __restrict__ w_out, float* __restrict__ r_out, float* __restrict__ rmax_out) {
+__global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(const D18Args A, int hd) {
+  __shared__ f32x4_t ust[kD18MaxDocs + 1];                 // per unit: (M, L, Mc, Lc)
+  __shared__ float ua[kD18MaxDocs + 1][kD18MergeDims];     // per unit: the merged accumulator
   __shared__ float wl[kD18MaxDocs];
-  __shared__ float4 ust[kD18MaxDocs + 1];                       // per unit: (M, L, Mc, Lc) over splits
-  __shared__ float fac[(kD18MaxDocs + 1) * kD18MaxSplits];      // 2^(m_split - M_unit)
-  __shared__ float4 sst[(kD18MaxDocs + 1) * kD18MaxSplits];     // the split states
-  __shared__ float ua[kD18MaxDocs + 1][kD18MergeDims];          // per unit: the merged accumulator
-  const int G = hq / hkv, U = n_docs + 1;
+  const int G = A.hq / A.hkv, U = A.n_docs + 1, D = A.n_docs;
   const int g = blockIdx.x % G, th = blockIdx.x / G;
-  const int t = th / hkv, h = th % hkv;
+  const int t = th / A.hkv, h = th % A.hkv;
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
-  // slot of (unit u, split s): ((th * U + u) * S + s) * G + g
-  auto slot = [&](int u, int sp) { return (((long long)th * U + u) * S + sp) * G + g; };
-  // Split states to LDS (one load per thread), then per unit the max / sums in split order.
-  for (int i = threadIdx.x; i < U * S; i += kD18Threads) sst[i] = part_ml[slot(i / S, i % S)];
-  __syncthreads();
-  for (int u = threadIdx.x; u < U; u += kD18Threads) {
-    float M = -INFINITY, Mc = -INFINITY;
-    for (int sp = 0; sp < S; ++sp) {
-      M = fmaxf(M, sst[u * S + sp].x);
-      Mc = fmaxf(Mc, sst[u * S + sp].z);
+  const int e = blockIdx.y * kD18MergeDims + lane;
+  const int ec = min(e, hd - 1);   // lanes past hd load a valid dim and store nothing
+  // Two units per wave in flight: units u0 and u0 + 4 of the wave's u0, u0 + 8, ...
+  for (int u0 = wv; u0 < U; u0 += 2 * kD18Waves) {
+    const int u1 = u0 + kD18Waves;
+    const bool two = u1 < U;   // wave-uniform
+    D18UnitLoad L0, L1;
+    load_unit(A, ((long long)th * U + u0) * A.S * G + g, G, hd, ec, lane, L0);
+    if (two) load_unit(A, ((long long)th * U + u1) * A.S * G + g, G, hd, ec, lane, L1);
+    const D18UnitSum m0 = reduce_unit(L0, A.S);
+    ua[u0][lane] = m0.acc;
+    if (lane == 0) ust[u0] = m0.st;
+    if (two) {
+      const D18UnitSum m1 = reduce_unit(L1, A.S);
+      ua[u1][lane] = m1.acc;
+      if (lane == 0) ust[u1] = m1.st;
     }
-    float L = 0.f, Lc = 0.f;
-    for (int sp = 0; sp < S; ++sp) {
-      const float4 st = sst[u * S + sp];
-      const float f = rescale(st.x, M);
-      fac[u * S + sp] = f;
-      L += st.y * f;
-      Lc += st.w * rescale(st.z, Mc);
-    }
-    ust[u] = make_float4(M, L, Mc, Lc);
   }
   __syncthreads();
-  if (wv == 0) {
+  if (wv != 0) return;
+  {
     const int d = lane;
-    const bool has = d < n_docs;
-    const float4 st = has ? ust[d] : make_float4(-INFINITY, 0.f, -INFINITY, 0.f);
-    const float r = st.w > 0.f ? st.z * kLn2 + logf(st.w) : -INFINITY;
-    float w;
-    if (force >= 0) {
-      w = d == force ? 1.f : 0.f;
-    } else if (wfix) {
-      w = has ? wfix[d] : 0.f;
-    } else {
-      const float logit = beta * r;
-      bool keep = has;
-      if (top_k > 0 && top_k < n_docs) {
-        // Rank by (logit, lower index first) over 64-bit order keys, as the routing top-k does.
-        const unsigned long long key =
-            has ? ((unsigned long long)order_key(logit) << 32) | (unsigned)~d : 0ull;
-        const unsigned hi = (unsigned)(key >> 32), lo = (unsigned)key;
-        int rank = 0;
-        for (int j = 0; j < n_docs; ++j) {
-          const unsigned long long kj = ((unsigned long long)(unsigned)__shfl((int)hi, j) << 32) |
-                                        (unsigned)__shfl((int)lo, j);
-          rank += kj > key ? 1 : 0;
-        }
-        keep = has && rank < top_k;
-      }
-      const float mx = wave_max(keep ? logit : -INFINITY);
-      const float e = keep ? expf(logit - mx) : 0.f;
-      w = e / wave_sum(e);
-    }
+    const bool has = d < D;
+    const f32x4_t st = has ? ust[d] : f32x4_t{-INFINITY, 0.f, -INFINITY, 0.f};
+    const float r = st[3] > 0.f ? st[2] * kLn2 + logf(st[3]) : -INFINITY;
+    const float w = doc_weight(r, has, d, D, A.beta, A.top_k, A.force, A.wfix);
     if (has) {
       if (blockIdx.y == 0) {
-        const long long o = (((long long)h * G + g) * T + t) * n_docs + d;
-        w_out[o] = w;
-        r_out[o] = r;
-        rmax_out[o] = st.w > 0.f ? st.z * kLn2 : -INFINITY;
+        const long long o = (((long long)h * G + g) * A.T + t) * D + d;
+        A.w[o] = w;
+        A.r[o] = r;
+        A.rmax[o] = st[3] > 0.f ? st[2] * kLn2 : -INFINITY;
       }
       wl[d] = w;
     }
   }
-  // Wave wv: the split sums of units wv, wv + 4, ... for dim e (in split order), all S loads of
-  // two units in flight.
-  const int e = blockIdx.y * kD18MergeDims + lane;
-  const int ec = min(e, hd - 1);   // lanes past hd load a valid dim and store nothing
-  for (int u0 = wv; u0 < U; u0 += 2 * kD18Waves) {
-    const int u1 = u0 + kD18Waves;
-    const bool two = u1 < U;   // wave-uniform
-    float v0[kD18MaxSplits], v1[kD18MaxSplits];
-#pragma unroll
-    for (int sp = 0; sp < kD18MaxSplits; ++sp) {
-      v0[sp] = sp < S ? part_acc[slot(u0, sp) * hd + ec] : 0.f;
-      v1[sp] = two && sp < S ? part_acc[slot(u1, sp) * hd + ec] : 0.f;
-    }
-    float a0 = 0.f, a1 = 0.f;
-#pragma unroll
-    for (int sp = 0; sp < kD18MaxSplits; ++sp)
-      if (sp < S) a0 = fmaf(v0[sp], fac[u0 * S + sp], a0);
-    ua[u0][lane] = a0;
-    if (two) {
-#pragma unroll
-      for (int sp = 0; sp < kD18MaxSplits; ++sp)
-        if (sp < S) a1 = fmaf(v1[sp], fac[u1 * S + sp], a1);
-      ua[u1][lane] = a1;
-    }
-  }
-  __syncthreads();   // ua and wl complete
-  if (wv == 0 && e < hd) {
-    const float4 so = ust[n_docs];
-    const float ao = ua[n_docs][lane];
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  if (e < hd) {
+    const f32x4_t so = ust[D];
+    const float ao = ua[D][lane];
     float o = 0.f;
-    for (int d = 0; d < n_docs; ++d) {
-      const float4 sd = ust[d];
-      const float M = fmaxf(sd.x, so.x);
-      const float a = rescale(sd.x, M), b = rescale(so.x, M);
-      o = fmaf(wl[d], (ua[d][lane] * a + ao * b) / (sd.y * a + so.y * b), o);
+    for (int d = 0; d < D; ++d) {
+      const f32x4_t sd = ust[d];
+      const float M = fmaxf(sd[0], so[0]);
+      const float a = rescale(sd[0], M), b = rescale(so[0], M);
+      o = fmaf(wl[d], (ua[d][lane] * a + ao * b) / (sd[1] * a + so[1] * b), o);
     }
-    out[((long long)t * hq + (long long)h * G + g) * hd + e] = o;
+    A.out[((long long)t * A.hq + (long long)h * G + g) * hd + e] = o;
+  }
+}
+
+// Partials of split s of unit u of (row t, kv head h): blockIdx = (t * hkv + h, u * S + s); u < D
+// a document (keys split into S ranges of ceil(N_d / S)), u = D the own rows (S ranges of
+// ceil((P + T) / S), cut at row t's causal end P + t + 1).
+template <typename TD, int HD, int GP>
+__global__ __launch_bounds__(kD18Threads) void d18_partials_kernel(const D18Args A, const int* __restrict__ doc_ptr) {
+  __shared__ D18Lds lds;
+  const int th = blockIdx.x;
+  const int t = th / A.hkv, h = th % A.hkv;
+  const int u = blockIdx.y / A.S, sp = blockIdx.y % A.S;
+  const int G = A.hq / A.hkv, U = A.n_docs + 1;
+  const long long slot = (((long long)th * U + u) * A.S + sp) * G;
+  if (u < A.n_docs) {
+    const int n0 = doc_ptr[u], N = doc_ptr[u + 1] - n0;
+    const int chunk = (N + A.S - 1) / A.S;
+    const int lo = sp * chunk, n = min(N - lo, chunk);
+    const long long off = (long long)h * A.s_dh + (long long)(n0 + lo) * A.s_dn;
+    d18_unit<TD, HD, GP>(G, static_cast<const TD*>(A.kd) + off, static_cast<const TD*>(A.vd) + off, A.s_dn, n, lo,
+                         N > A.skip ? A.skip : 0, A.qd + (((long long)u * A.T + t) * A.hq + (long long)h * G) * HD,
+                         A.scale_log2, A.part_ml + slot, A.part_acc + slot * HD, lds);
+  } else {
+    const int chunk = (A.P + A.T + A.S - 1) / A.S;
+    const int lo = sp * chunk, n = min(A.P + t + 1 - lo, chunk);
+    const long long off = (long long)h * A.s_oh + (long long)lo * A.s_on;
+    d18_unit<float, HD, GP>(G, A.ko + off, A.vo + off, A.s_on, n, lo, -1,
+                            A.qo + ((long long)t * A.hq + (long long)h * G) * HD, A.scale_log2, A.part_ml + slot,
+                            A.part_acc + slot * HD, lds);
   }
 }
 
@@ -489,7 +690,7 @@ using namespace xenc;
 extern "C" size_t xenc_d18_workspace_bytes(int T, int hq, int n_docs, int hd, int nsplit) {
   if (T < 0 || hq <= 0 || n_docs <= 0 || hd <= 0 || nsplit <= 0) return 0;
   const size_t units = (size_t)T * hq * (n_docs + 1) * nsplit;
-  return d18_align256(units * sizeof(float4)) + d18_align256(units * hd * sizeof(float));
+  return d18_align256(units * sizeof(f32x4_t)) + d18_align256(units * hd * sizeof(float));
 }
 
 extern "C" int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_docs, const float* qd,
@@ -507,29 +708,57 @@ extern "C" int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_do
   // document keys (EPL 8) and the fp32 own rows (EPL 4) alike.
   if (hd != 32 && hd != 64 && hd != 128 && hd != 256) return XENC_EINVAL;
   const int epl = dtype == 2 ? 4 : 8;
-  if (s_dh % epl || s_dn % epl || s_oh % 4 || s_on % 4) return XENC_EALIGN;
+  if (s_dh % epl || s_dn % epl || s_oh % 4 || s_on % 4 || s_dn < hd || s_on < hd) return XENC_EALIGN;
   if (T == 0) return XENC_OK;
   if (!qd || !qo || !k_docs || !v_docs || !doc_ptr || !k_own || !v_own || !out || !w || !r || !rmax)
     return XENC_ENULL;
   if (!aligned16(qd) || !aligned16(qo) || !aligned16(k_docs) || !aligned16(v_docs) || !aligned16(k_own) ||
-      !aligned16(v_own))
+      !aligned16(v_own) || !aligned16(out))
     return XENC_EALIGN;
   if (!workspace) return XENC_ENULL;
+  if (!aligned16(workspace)) return XENC_EALIGN;
   if (workspace_bytes < xenc_d18_workspace_bytes(T, hq, n_docs, hd, nsplit)) return XENC_EWORKSPACE;
-  if ((long long)T * hq > 0x7fffffffLL) return XENC_EINVAL;
+  if ((long long)T * hkv > 0x7fffffffLL) return XENC_EINVAL;
+  // A 16-row tile's bytes fit the 32-bit buffer descriptor.
+  const long long esz = dtype == 2 ? 4 : 2;
+  if ((15 * s_dn + hd) * esz > 0x7fffffffLL || (15 * s_on + hd) * 4 > 0x7fffffffLL) return XENC_EINVAL;
   const size_t units = (size_t)T * hq * (n_docs + 1) * nsplit;
-  float4* part_ml = static_cast<float4*>(workspace);
-  float* part_acc = reinterpret_cast<float*>(static_cast<char*>(workspace) + d18_align256(units * sizeof(float4)));
+  char* ws = static_cast<char*>(workspace);
+  D18Args A;
+  A.T = T;
+  A.hq = hq;
+  A.hkv = hkv;
+  A.n_docs = n_docs;
+  A.S = nsplit;
+  A.P = P;
+  A.skip = skip;
+  A.top_k = top_k;
+  A.force = force;
+  A.scale_log2 = scale * kLog2e;
+  A.beta = beta;
+  A.qd = qd;
+  A.qo = qo;
+  A.kd = k_docs;
+  A.vd = v_docs;
+  A.s_dh = s_dh;
+  A.s_dn = s_dn;
+  A.ko = k_own;
+  A.vo = v_own;
+  A.s_oh = s_oh;
+  A.s_on = s_on;
+  A.wfix = wfix;
+  A.part_ml = reinterpret_cast<f32x4_t*>(ws);
+  A.part_acc = reinterpret_cast<float*>(ws + d18_align256(units * sizeof(f32x4_t)));
+  A.out = out;
+  A.w = w;
+  A.r = r;
+  A.rmax = rmax;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(T * hkv), (unsigned)((n_docs + 1) * nsplit));
-  const float sl2 = scale * kLog2e;
   // Query heads per kv head padded to 1, 2, 4 or 8 (padded heads have q = 0 and are not written).
   const int G = hq / hkv, GP = G <= 1 ? 1 : G <= 2 ? 2 : G <= 4 ? 4 : 8;
-#define XENC_D18_LAUNCH(TD, HDV, GPV)                                                              \
-  hipLaunchKernelGGL((d18_partials_kernel<TD, HDV, GPV>), grid, dim3(kD18PartThreads), 0, st, hq, hkv, \
-                     n_docs, nsplit, qd, qo, static_cast<const TD*>(k_docs),                         \
-                     static_cast<const TD*>(v_docs), s_dh, s_dn, doc_ptr, k_own, v_own, s_oh, s_on, P, \
-                     T, sl2, skip, part_ml, part_acc)
+#define XENC_D18_LAUNCH(TD, HDV, GPV) \
+  hipLaunchKernelGGL((d18_partials_kernel<TD, HDV, GPV>), grid, dim3(kD18Threads), 0, st, A, doc_ptr)
 #define XENC_D18_GP(TD, HDV)                            \
   switch (GP) {                                         \
     case 1: XENC_D18_LAUNCH(TD, HDV, 1); break;         \
@@ -553,7 +782,6 @@ extern "C" int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_do
 #undef XENC_D18_GP
 #undef XENC_D18_LAUNCH
   hipLaunchKernelGGL(d18_merge_kernel, dim3((unsigned)(T * hq), (unsigned)((hd + kD18MergeDims - 1) / kD18MergeDims)),
-                     dim3(kD18Threads), 0, st, T, hq, hkv, hd,
-                     n_docs, nsplit, part_ml, part_acc, beta, top_k, force, wfix, out, w, r, rmax);
+                     dim3(kD18Threads), 0, st, A, hd);
   return check_launch();
 }

@@ -5,8 +5,9 @@
         --kernel decode_read_kernel --copy-bytes 1073741824 [--json out.json]
 
 `traffic` averages FETCH_SIZE and WRITE_SIZE (KiB per dispatch) over the dispatches of the
-kernel, and scales each by what the same counter reads for the plain copy kernel of known size
-that `bench.py --calibration-copy-mib` launches (expected: copy_bytes read, copy_bytes written).
+kernel, and scales each by what the same counter reads for the device-to-device blit copy of
+known size that `bench.py --calibration-copy-mib` launches after the workload (expected:
+copy_bytes read, copy_bytes written).
 """
 
 from __future__ import annotations
@@ -39,12 +40,17 @@ def _counter(path: str, counter: str) -> list[tuple[str, float]]:
     return [(r["Kernel_Name"], float(r["Counter_Value"])) for r in rows if r["Counter_Name"] == counter]
 
 
-def _copy_kernel(vals: list[tuple[str, float]]) -> float:
-    """The calibration copy: the largest fp16 copy dispatches, which come last in the run."""
-    cands = [v for n, v in vals if "copy" in n.lower()]
-    if not cands:
-        raise SystemExit("no copy kernel dispatches found (run bench.py with --calibration-copy-mib)")
-    return statistics.median(sorted(cands)[-3:])
+def _copy_kernel(vals: list[tuple[str, float]], copy_bytes: int) -> float:
+    """The calibration copy: the three largest dispatches of the device-to-device blit kernel
+    (`__amd_rocclr_copyBuffer`) that `bench.py --calibration-copy-mib` launches after the workload.
+    Other kernels with "copy" in their names (dtype conversions while the synthetic inputs are
+    built) move other byte counts and are never taken.  A reading below 1/16 of the copy's size
+    means the calibration copy is not in the file."""
+    cands = sorted(v for n, v in vals if "copyBuffer" in n)
+    if len(cands) < 3 or cands[-1] * 1024.0 * 16 < copy_bytes:
+        raise SystemExit("no calibration copy dispatches of that size found "
+                         "(run bench.py with --calibration-copy-mib)")
+    return statistics.median(cands[-3:])
 
 
 def traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int) -> dict:
@@ -52,8 +58,8 @@ def traffic(fetch_csv: str, write_csv: str, kernel: str, copy_bytes: int) -> dic
     of each kernel (the kernels one step launches once each)."""
     f = _counter(fetch_csv, "FETCH_SIZE")
     w = _counter(write_csv, "WRITE_SIZE")
-    fetch_scale = copy_bytes / (_copy_kernel(f) * 1024.0)
-    write_scale = copy_bytes / (_copy_kernel(w) * 1024.0)
+    fetch_scale = copy_bytes / (_copy_kernel(f, copy_bytes) * 1024.0)
+    write_scale = copy_bytes / (_copy_kernel(w, copy_bytes) * 1024.0)
     per, fetch_b, write_b, disp = {}, 0.0, 0.0, 0
     for name in kernel.split(","):
         fk = [v for n, v in f if name in n]

@@ -84,6 +84,28 @@ def test_d18_key_splits_and_decode_shape(dev):
     _check(got, _oracle(qd, qo, docs, Kown, Vown, 300, 256 ** -0.5, skip=4, top_k=2), 2e-5)
 
 
+def test_d18_repeated_calls_and_shape_changes(dev):
+    """One call shape ten times in a row gives bit-identical results; a larger shape in between
+    and the return to the first shape still match the oracle and the first results."""
+    say("d18 repeated calls")
+
+    def run(case, **kw):
+        qd, qo, docs, Kown, Vown = case
+        return ops.d18_read(qd.to(dev), qo.to(dev), [(K.to(dev), V.to(dev)) for K, V in docs], Kown.to(dev),
+                            Vown.to(dev), 0.1, skip=1, **kw)
+
+    small = _case([40, 23], 1, 10, 2, 4, 128, torch.bfloat16, 21)
+    big = _case([300, 120, 77], 3, 50, 2, 4, 128, torch.bfloat16, 22)
+    first = run(small, nsplit=4)
+    for _ in range(10):
+        again = run(small, nsplit=4)
+        assert all(torch.equal(first[k], again[k]) for k in ("o", "w", "r", "rmax"))
+    _check(run(big, nsplit=5), _oracle(*big, 50, 0.1, skip=1), 2e-5)
+    back = run(small, nsplit=4)
+    assert all(torch.equal(first[k], back[k]) for k in ("o", "w", "r", "rmax"))
+    _check(back, _oracle(*small, 10, 0.1, skip=1), 2e-5)
+
+
 def test_d18_routing_modes_and_ties(dev):
     """Documents 0 and 2 identical (same keys, same rotation): their route logits tie exactly, and
     top_k = 1 keeps the lower index as the oracle's stable top-k does; force, wfix and a sharp beta
