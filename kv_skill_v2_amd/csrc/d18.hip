@@ -17,10 +17,10 @@
 // fp16 / fp32 keys against fp16 hi + lo); for 16-bit values P.V runs on the matrix cores too (the
 // weights split into parts the same way), for the fp32 own rows on the VALU; the running max
 // moves only by steps of more than 2^8, so most tiles skip the accumulator rescale; the 4 waves
-// merge through LDS in a fixed order.  d18_merge_kernel: one workgroup per (row, query head, 64 output dims)
-// merges the splits (each split's state and accumulator requested in one round of loads), joins
-// each document with the own rows (o_d), forms r, rmax and the routing weights, and sums
-// w_d o_d.  (Merging where the splits are produced, by the last workgroup of a unit and of a
+// merge through LDS in a fixed order.  d18_merge_kernel: one workgroup per (row, query head, 16
+// output dims), one unit per 16-lane row, merges the splits (each split's state and accumulator
+// requested in one round of loads), joins each document with the own rows (o_d), forms r, rmax
+// and the routing weights, and sums w_d o_d.  (Merging where the splits are produced, by the last workgroup of a unit and of a
 // row to arrive on a counter, measured slower: each level adds an L2 write-back, an atomic and
 // two rounds of loads to the critical path.)  Deterministic: every sum runs in a fixed order.
 #include <algorithm>
@@ -547,73 +547,61 @@ __device__ __forceinline__ float doc_weight(float r, bool has, int d, int D, flo
   return e / wave_sum(e);
 }
 
-// The S splits of unit u for query head g and the 64 dims of this lane's block: lane s < S holds
-// split s's state, lane e the S accumulator values of dim ec (all requested in one round).  The
-// unit's max M, the factors 2^(m_s - M) and the sums L, Lc come from wave reductions (a fixed
-// tree); the accumulator sums its splits in split order with the factors read back by readlane.
-struct D18UnitLoad {
-  f32x4_t st;
-  float v[kD18MaxSplits];
-};
-struct D18UnitSum {
-  f32x4_t st;   // (M, L, Mc, Lc), uniform over the wave
-  float acc;    // this lane's dim
-};
-
-__device__ __forceinline__ void load_unit(const D18Args& A, long long slot0, int G, int hd, int ec, int lane,
-                                          D18UnitLoad& L) {
-  const int S = A.S;   // split s at slot0 + s * G
-  L.st = lane < S ? A.part_ml[slot0 + (long long)lane * G] : f32x4_t{-INFINITY, 0.f, -INFINITY, 0.f};
-#pragma unroll
-  for (int s = 0; s < kD18MaxSplits; ++s)
-    L.v[s] = s < S ? A.part_acc[(slot0 + (long long)s * G) * hd + ec] : 0.f;
+// Max over each aligned group of 16 lanes (one row), every lane of the row ending with it (DPP).
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+  return fmaxf(v, dpp_f<0x140>(v));   // row_mirror
 }
 
-__device__ __forceinline__ D18UnitSum reduce_unit(const D18UnitLoad& L, int S) {
-  const float M = wave_max(L.st[0]), Mc = wave_max(L.st[2]);
-  const float f = rescale(L.st[0], M);
-  D18UnitSum r;
-  r.st = f32x4_t{M, wave_sum(L.st[1] * f), Mc, wave_sum(L.st[3] * rescale(L.st[2], Mc))};
-  float a = 0.f;
-#pragma unroll
-  for (int s = 0; s < kD18MaxSplits; ++s)
-    if (s < S) a = fmaf(L.v[s], readlane(f, s), a);
-  r.acc = a;
-  return r;
-}
-
-// One workgroup per (row t, kv head h, query head g) and block of 64 output dims:
-// blockIdx.x = (t * hkv + h) * G + g, blockIdx.y = dim block.  Wave v merges the splits of units
-// v, v + 4, ... (load_unit / reduce_unit) into LDS; wave 0 then forms r, rmax and the routing weights (one lane
-// per document; block 0 writes w, r, rmax) and sums o[e] = sum_d w_d o_d[e], o_d the join of
-// document d and the own rows: o_d = (a_d acc_d + b_d acc_own) / (a_d L_d + b_d L_own) with
+// One workgroup of 2 waves per (row t, kv head h, query head g) and block of 16 output dims:
+// blockIdx.x = (t * hkv + h) * G + g, blockIdx.y = dim block.  Each 16-lane row of the
+// workgroup merges one unit (row k of the 8 takes units k, k + 8, ...): lane j of the row holds
+// the states of splits j and j + 16 and the S accumulator values of dim 16 blk + j, all
+// requested in one round.  The unit's max M, the factors 2^(m_s - M) and the sums L, Lc come
+// from row reductions (a fixed tree); the accumulator sums its splits in split order with the
+// factors fetched from the row's lanes.  Wave 0 then forms r, rmax and the routing weights (one
+// lane per document; block 0 writes w, r, rmax) and sums o[e] = sum_d w_d o_d[e], o_d the join
+// of document d and the own rows: o_d = (a_d acc_d + b_d acc_own) / (a_d L_d + b_d L_own) with
 // a_d = 2^(M_d - M), b_d = 2^(M_own - M), M = max(M_d, M_own).
-constexpr int kD18MergeDims = kWave;
+constexpr int kD18MergeDims = 16;
+constexpr int kD18MergeThreads = 128;
+constexpr int kD18MergeRows = kD18MergeThreads / kD18MergeDims;   // units in flight
 
-__global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(const D18Args A, int hd) {
+__global__ __launch_bounds__(kD18MergeThreads) void d18_merge_kernel(const D18Args A, int hd) {
   __shared__ f32x4_t ust[kD18MaxDocs + 1];                 // per unit: (M, L, Mc, Lc)
   __shared__ float ua[kD18MaxDocs + 1][kD18MergeDims];     // per unit: the merged accumulator
   __shared__ float wl[kD18MaxDocs];
-  const int G = A.hq / A.hkv, U = A.n_docs + 1, D = A.n_docs;
+  const int G = A.hq / A.hkv, U = A.n_docs + 1, D = A.n_docs, S = A.S;
   const int g = blockIdx.x % G, th = blockIdx.x / G;
   const int t = th / A.hkv, h = th % A.hkv;
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
-  const int e = blockIdx.y * kD18MergeDims + lane;
+  const int row = threadIdx.x / kD18MergeDims, j = threadIdx.x % kD18MergeDims;
+  const int rbase = (lane / kD18MergeDims) * kD18MergeDims;   // this row's first lane in the wave
+  const int e = blockIdx.y * kD18MergeDims + j;
   const int ec = min(e, hd - 1);   // lanes past hd load a valid dim and store nothing
-  // Two units per wave in flight: units u0 and u0 + 4 of the wave's u0, u0 + 8, ...
-  for (int u0 = wv; u0 < U; u0 += 2 * kD18Waves) {
-    const int u1 = u0 + kD18Waves;
-    const bool two = u1 < U;   // wave-uniform
-    D18UnitLoad L0, L1;
-    load_unit(A, ((long long)th * U + u0) * A.S * G + g, G, hd, ec, lane, L0);
-    if (two) load_unit(A, ((long long)th * U + u1) * A.S * G + g, G, hd, ec, lane, L1);
-    const D18UnitSum m0 = reduce_unit(L0, A.S);
-    ua[u0][lane] = m0.acc;
-    if (lane == 0) ust[u0] = m0.st;
-    if (two) {
-      const D18UnitSum m1 = reduce_unit(L1, A.S);
-      ua[u1][lane] = m1.acc;
-      if (lane == 0) ust[u1] = m1.st;
+  const f32x4_t empty = {-INFINITY, 0.f, -INFINITY, 0.f};
+  for (int u0 = 0; u0 < U; u0 += kD18MergeRows) {
+    const int u = u0 + row;
+    const bool mine = u < U;
+    const long long slot0 = ((long long)th * U + min(u, U - 1)) * S * G + g;   // split s at slot0 + s * G
+    const f32x4_t s0 = j < S ? A.part_ml[slot0 + (long long)j * G] : empty;
+    const f32x4_t s1 = j + 16 < S ? A.part_ml[slot0 + (long long)(j + 16) * G] : empty;
+    float v[kD18MaxSplits];
+#pragma unroll
+    for (int s = 0; s < kD18MaxSplits; ++s) v[s] = s < S ? A.part_acc[(slot0 + (long long)s * G) * hd + ec] : 0.f;
+    const float M = row_max(fmaxf(s0[0], s1[0])), Mc = row_max(fmaxf(s0[2], s1[2]));
+    const float f0 = rescale(s0[0], M), f1 = rescale(s1[0], M);
+    const float L = group_sum<16>(s0[1] * f0 + s1[1] * f1);
+    const float Lc = group_sum<16>(s0[3] * rescale(s0[2], Mc) + s1[3] * rescale(s1[2], Mc));
+    float a = 0.f;
+#pragma unroll
+    for (int s = 0; s < kD18MaxSplits; ++s)
+      if (s < S) a = fmaf(v[s], __shfl(s < 16 ? f0 : f1, rbase + (s & 15)), a);
+    if (mine) {
+      ua[u][j] = a;
+      if (j == 0) ust[u] = f32x4_t{M, L, Mc, Lc};
     }
   }
   __syncthreads();
@@ -621,7 +609,7 @@ __global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(const D18Args A,
   {
     const int d = lane;
     const bool has = d < D;
-    const f32x4_t st = has ? ust[d] : f32x4_t{-INFINITY, 0.f, -INFINITY, 0.f};
+    const f32x4_t st = has ? ust[d] : empty;
     const float r = st[3] > 0.f ? st[2] * kLn2 + logf(st[3]) : -INFINITY;
     const float w = doc_weight(r, has, d, D, A.beta, A.top_k, A.force, A.wfix);
     if (has) {
@@ -637,15 +625,15 @@ __global__ __launch_bounds__(kD18Threads) void d18_merge_kernel(const D18Args A,
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-  if (e < hd) {
+  if (lane < kD18MergeDims && e < hd) {
     const f32x4_t so = ust[D];
-    const float ao = ua[D][lane];
+    const float ao = ua[D][j];
     float o = 0.f;
     for (int d = 0; d < D; ++d) {
       const f32x4_t sd = ust[d];
       const float M = fmaxf(sd[0], so[0]);
       const float a = rescale(sd[0], M), b = rescale(so[0], M);
-      o = fmaf(wl[d], (ua[d][lane] * a + ao * b) / (sd[1] * a + so[1] * b), o);
+      o = fmaf(wl[d], (ua[d][j] * a + ao * b) / (sd[1] * a + so[1] * b), o);
     }
     A.out[((long long)t * A.hq + (long long)h * G + g) * hd + e] = o;
   }
@@ -782,6 +770,6 @@ extern "C" int xenc_d18_read(int dtype, int T, int hq, int hkv, int hd, int n_do
 #undef XENC_D18_GP
 #undef XENC_D18_LAUNCH
   hipLaunchKernelGGL(d18_merge_kernel, dim3((unsigned)(T * hq), (unsigned)((hd + kD18MergeDims - 1) / kD18MergeDims)),
-                     dim3(kD18Threads), 0, st, A, hd);
+                     dim3(kD18MergeThreads), 0, st, A, hd);
   return check_launch();
 }
