@@ -8,10 +8,12 @@ written back:
     1. per token, in one launch (xenc_multi_depth_prepare): the selector's top-k of the logits
        z [B, L] with a softmax over the kept ones (ties go to the lower depth), the query row of
        each kept depth gathered from q_all [L, B, d], and gate * gain of each (token, depth) row;
-    2. routing over the chunks of that row's depth library (xenc_route_topk);
-    3. the paged split-K read of the routed pages (xenc_library_read_decode);
-    4. the depth's B streamed once with the row scale folded in (xenc_write_back);
-    5. the matched-norm rescale times the selector weight, summed over a token's kept depths
+    2. routing over the chunks of that row's depth library and the paged split-K read of the
+       routed pages in one call (xenc_route_read_decode: the q . S dots, the top-k of every row,
+       the ranking of the routed (row, page) entries by page, the read with the rows that routed
+       the same page side by side, the merge of the partials);
+    3. the depth's B streamed once with the row scale folded in (xenc_write_back);
+    4. the matched-norm rescale times the selector weight, summed over a token's kept depths
        (xenc_selector_apply).
 
 The depth libraries are one pool (`PagedLibrary` with one library per depth); the row's library
@@ -69,9 +71,9 @@ class MultiDepthDecode:
             _, top, wtop, qr, scale = ops.multi_depth_prepare(z, k, q_all, hn, self.gate_w, self.gate_b,
                                                               self.log_gain, self.gain_scale)
             depth = top.reshape(-1)
-            _, idx, wsel = ops.route_topk(qr, self.lib, depth, top_k=self.top_k, route_temp=self.route_temp)
-            r = ops.library_read_decode(qr, self.lib, idx, wsel, depth, read_temp=self.read_temp,
-                                        nsplit=self.nsplit)
+            _, idx, wsel, r = ops.route_read_decode(qr, self.lib, depth, top_k=self.top_k,
+                                                    route_temp=self.route_temp, read_temp=self.read_temp,
+                                                    nsplit=self.nsplit)
             upd = ops.write_back(r, self.B_w, depth, None, scale)
             out = ops.selector_apply(upd, h, wtop.reshape(-1), self.log_alpha, k=k)
         return out, idx, depth

@@ -382,6 +382,8 @@ FOLD_CASES = [
     ([5, 9, 3], [1, 1, 2], 256, 128, 7, 3),                        # top_k >= C for some libraries
     ([70, 20], [0, 1], 128, 64, 4, 1),                             # more than 64 chunks: two calls
     ([40, 33], [0, 1, 0, 1, 0, 1, 0, 1, 0, 1, 0, 1, 0, 1, 0, 1], 256, 64, 8, 1),  # shared libraries: page-grouped
+    ([64] * 8, [b % 8 for b in range(64)], 2560, 512, 8, 1),        # the multi-depth step's shape: grouped
+    ([64, 20, 50], [0, 1, 2] * 43, 128, 64, 5, 2),                   # 645 grouped entries, one thread per entry
 ]
 
 
