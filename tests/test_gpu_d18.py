@@ -106,6 +106,37 @@ def test_d18_repeated_calls_and_shape_changes(dev):
     _check(back, _oracle(*small, 10, 0.1, skip=1), 2e-5)
 
 
+@pytest.mark.parametrize("dtype,nsplit", [(torch.bfloat16, 2), (torch.float16, 1), (torch.float32, 3)])
+def test_d18_growing_scores_and_long_splits(dev, dtype, nsplit):
+    """Keys whose scores climb along the document: row j of every document and of the own rows
+    leans on the mean query direction with weight j / 4, so a query's score climbs by about 0.06 a
+    key in log2 units (the queries project ~2 on that direction, scale 1/sqrt(128)): across a
+    split of hundreds of keys the later tiles pass the running max by far more than 2^8, and the
+    accumulators are rescaled mid-split; splits of up to 1,000 keys also run the multi-tile loop
+    (several tiles per wave).  Against the fp64 oracle at the usual bar."""
+    say("d18 growing scores", dict(dtype=str(dtype), nsplit=nsplit))
+    g = torch.Generator().manual_seed(31)
+    D, T, P, Hkv, G, hd = 2, 2, 700, 2, 4, 128
+    Ns = [1000, 613]
+    qd = torch.randn(D, Hkv * G, T, hd, generator=g)
+    qo = torch.randn(Hkv * G, T, hd, generator=g)
+    qdir = torch.nn.functional.normalize(qd.mean(dim=(0, 1, 2)), dim=0)
+    odir = torch.nn.functional.normalize(qo.mean(dim=(0, 1)), dim=0)
+
+    def climb(n, direction):
+        base = torch.randn(Hkv, n, hd, generator=g) * 0.3
+        ramp = (torch.arange(n, dtype=torch.float32) / 4.0).view(1, n, 1)
+        return base + ramp * direction.view(1, 1, hd)
+
+    docs = [(climb(n, qdir).to(dtype), torch.randn(Hkv, n, hd, generator=g).to(dtype)) for n in Ns]
+    Kown, Vown = climb(P + T, odir), torch.randn(Hkv, P + T, hd, generator=g)
+    scale = hd ** -0.5
+    got = ops.d18_read(qd.to(dev), qo.to(dev), [(K.to(dev), V.to(dev)) for K, V in docs], Kown.to(dev),
+                       Vown.to(dev), scale, skip=5, nsplit=nsplit)
+    ref = _oracle(qd, qo, docs, Kown, Vown, P, scale, skip=5)
+    _check(got, ref, 2e-5)
+
+
 def test_d18_routing_modes_and_ties(dev):
     """Documents 0 and 2 identical (same keys, same rotation): their route logits tie exactly, and
     top_k = 1 keeps the lower index as the oracle's stable top-k does; force, wfix and a sharp beta
