@@ -168,6 +168,47 @@ def measured_stream_peak(dev, gib: int = 2) -> float:
     return best
 
 
+def timed_steps(step, steps: int, stream):
+    """Times `steps` back-to-back calls of `step` with nothing else queued between them, closed
+    by a device synchronisation on each side.  Returns (wall ms per step, GPU ms per step): the
+    second from ONE event pair around the whole region on `stream`, so it is the span the kernels
+    of the K steps occupy, gaps between them included.  A timing event between steps would add
+    GPU idle time of its own (about 10 us per pair on this stack), so none is recorded there."""
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record(stream)
+    for _ in range(steps):
+        step()
+    b.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return wall, a.elapsed_time(b) / steps
+
+
+def graph_of(step, same):
+    """`step` captured once in a HIP graph after a warm-up call on a side stream.  Returns (graph,
+    the captured call's output), or (None, None) when a replay does not reproduce the eager
+    result: three replays, each followed by a synchronisation, `same(captured output)`, an eager
+    call and another synchronisation."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        out = step()
+    for _ in range(3):
+        gph.replay()
+        torch.cuda.synchronize()
+        if not same(out):
+            return None, None
+        step()
+        torch.cuda.synchronize()
+    return gph, out
+
+
 def bench_prefill(args):
     """Prefill/registration read: 4 documents x 2048 query rows, each document a Library of 32 x 512
     slots (ragged tail), d_s = 2048, dense routing (every chunk read), fp16 MFMA with fp32
@@ -203,13 +244,17 @@ def bench_prefill(args):
         ops.route_backward(w, gamma, lib, plan, 10.0, dq)
         return dq
 
-    for _ in range(args.warmup):
-        w, r, p = fwd()
+    def step():
+        w, _, p = fwd()
         bwd(w, p)
-    torch.cuda.synchronize()
+
+    for _ in range(args.warmup):
+        step()
     stream = torch.cuda.current_stream(dev)
+    ms_step, _ = timed_steps(step, args.steps, stream)
+    # The split between the directions, from a second loop of K steps with events between the
+    # forward and the backward (outside the timed region above: the events add idle time).
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    t0 = time.perf_counter()
     for i in range(args.steps):
         evs[i][0].record(stream)
         w, r, p = fwd()
@@ -217,7 +262,6 @@ def bench_prefill(args):
         bwd(w, p)
         evs[i][2].record(stream)
     torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
     fwd_ms = statistics.mean(e[0].elapsed_time(e[1]) for e in evs)
     bwd_ms = statistics.mean(e[1].elapsed_time(e[2]) for e in evs)
     nvalid = sum(P.nvalid)
@@ -311,45 +355,24 @@ def bench_multi_depth(args):
                   + 2 * B * c["k_sel"] * (d + dr) * 4 + B * dr * 4 * 2)
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    ms_eager = (time.perf_counter() - t0) * 1e3 / args.steps
+    stream = torch.cuda.current_stream(dev)
+    ms_eager, span_eager = timed_steps(step, args.steps, stream)
 
-    # The step is ~20 small launches: capture it once in a HIP graph and replay it.  Every replay
-    # is checked against the eager result (bit for bit) with eager work and synchronisation in
-    # between; on any mismatch the eager time is reported.
-    ms_graph, graph_ok = None, False
+    # The step captured once in a HIP graph and replayed.  Every replay is checked against the
+    # eager result (bit for bit) with eager work and synchronisation in between; on
+    # any mismatch the eager time is reported.
+    ms_graph = span_graph = None
+    graph_ok = False
     if not args.no_graph:
         ref_out = step()[0].clone()
-        s = torch.cuda.Stream()
-        s.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s):
-            step()
-        torch.cuda.current_stream().wait_stream(s)
-        gph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gph):
-            g_out = step()[0]
-        graph_ok = True
-        for _ in range(3):
-            gph.replay()
-            torch.cuda.synchronize()
-            graph_ok &= bool(torch.equal(g_out, ref_out))
-            step()
-            torch.cuda.synchronize()
-        if graph_ok:
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                gph.replay()
-            torch.cuda.synchronize()
-            ms_graph = (time.perf_counter() - t0) * 1e3 / args.steps
-            graph_ok &= bool(torch.equal(g_out, ref_out))
+        gph, g_out = graph_of(lambda: step()[0], lambda o: torch.equal(o, ref_out))
+        if gph is not None:
+            ms_graph, span_graph = timed_steps(gph.replay, args.steps, stream)
+            graph_ok = bool(torch.equal(g_out, ref_out))
     # The step runs either way; report the faster of the two measured ways (named in config).
     timing = "hip_graph" if graph_ok and ms_graph < ms_eager else "eager"
-    ms_step = ms_graph if timing == "hip_graph" else ms_eager
-    achieved = bytes_step / (ms_step * 1e-3) / 1e9
+    ms_step, span = (ms_graph, span_graph) if timing == "hip_graph" else (ms_eager, span_eager)
+    achieved = bytes_step / (span * 1e-3) / 1e9
 
     cpu = None
     if args.cpu_sample > 0:
@@ -384,7 +407,7 @@ def bench_multi_depth(args):
         "roofline": {"bound": "hbm", "kernel": "whole step (route + read + write-back + epilogue)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-                     "algorithmic_bytes": bytes_step, "unique_routed_pages": len(pages),
+                     "algorithmic_bytes": bytes_step, "avg_launch_ms": span, "unique_routed_pages": len(pages),
                      "routed_page_reads": int((idx0 >= 0).sum()), "depths_used": used},
         "cpu_baseline": cpu,
     }
@@ -413,22 +436,13 @@ def bench_pool_build(args):
     del by_chunk, keep
     R = rows.shape[0]
     alg_bytes = R * d * 2 + C * N * d * 2 + C * d * 4 + C * 4 + (C + 1) * 8 + d * 4
+    def step():
+        ops.build_pages(rows, off, d, N, d, mu)
+
     for _ in range(args.warmup):
-        out = ops.build_pages(rows, off, d, N, d, mu)
-    del out
-    torch.cuda.synchronize()
+        step()
     stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        out = ops.build_pages(rows, off, d, N, d, mu)
-        ev[i][1].record(stream)
-        del out
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    k_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    ms_step, k_ms = timed_steps(step, args.steps, stream)
     achieved = alg_bytes / (k_ms * 1e-3) / 1e9
     # Read + write ceiling for reference: torch's device copy of the slot rows (same order of
     # bytes read and written as the build).
@@ -462,7 +476,7 @@ def bench_pool_build(args):
                           f"({cpu_s:.2f} s); CPU oracle on {cpu_model()}")}
     out = {
         "metric": "Library pool build from document caches: chunks/s and HBM GB/s (% peak)",
-        "value": C / (k_ms * 1e-3), "unit": "chunks/s", "n_gpus": 1, "steps": args.steps,
+        "value": C / (ms_step * 1e-3), "unit": "chunks/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32 (fp16 in/out)", "data": "synthetic",
         "config": {"workload": "pool_build", "documents": len(P.n_chunks), "chunks": C,
@@ -518,51 +532,20 @@ def bench_d18(args):
                  + T * hq * hd * 4 + 3 * hkv * G * T * D * 4)
     for _ in range(args.warmup):
         call()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for a, b in ev:
-        a.record(stream)
-        call()
-        b.record(stream)
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    k_ms_eager = statistics.mean(a.elapsed_time(b) for a, b in ev)
-    # A call is two short launches, so a host loop of calls leaves the GPU waiting on the host:
-    # the call is also captured in a HIP graph and K replays are timed between two events (every
-    # replay's output checked against the eager one).
-    k_ms_graph = None
+    ms_eager, k_ms_eager = timed_steps(call, args.steps, stream)
+    # The call (two launches) captured once in a HIP graph and replayed: every replay's output
+    # checked against the eager one.  The faster of the two ways is reported (named in config).
+    ms_graph = k_ms_graph = None
     if not args.no_graph:
         ref = (out.clone(), w.clone())
-        side = torch.cuda.Stream()
-        side.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(side):
-            call()
-        torch.cuda.current_stream().wait_stream(side)
-        gph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gph):
-            call()
-        ok = True
-        for _ in range(3):
-            gph.replay()
-            torch.cuda.synchronize()
-            ok &= bool(torch.equal(out, ref[0]) and torch.equal(w, ref[1]))
-            call()
-            torch.cuda.synchronize()
-        if ok:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            for _ in range(args.steps):
-                gph.replay()
-            b.record(stream)
-            torch.cuda.synchronize()
-            k_ms_graph = a.elapsed_time(b) / args.steps
-            ok &= bool(torch.equal(out, ref[0]))
-        if not ok:
-            k_ms_graph = None
-    timing = "hip_graph" if k_ms_graph is not None and k_ms_graph < k_ms_eager else "eager"
-    k_ms = k_ms_graph if timing == "hip_graph" else k_ms_eager
+        gph, _ = graph_of(call, lambda _: torch.equal(out, ref[0]) and torch.equal(w, ref[1]))
+        if gph is not None:
+            ms_graph, k_ms_graph = timed_steps(gph.replay, args.steps, stream)
+            if not torch.equal(out, ref[0]):
+                ms_graph = k_ms_graph = None
+    timing = "hip_graph" if ms_graph is not None and ms_graph < ms_eager else "eager"
+    ms_step, k_ms = (ms_graph, k_ms_graph) if timing == "hip_graph" else (ms_eager, k_ms_eager)
     achieved = alg_bytes / (k_ms * 1e-3) / 1e9
     cpu = None
     if args.cpu_sample > 0:
@@ -585,12 +568,12 @@ def bench_d18(args):
                           f"{cpu_model()}")}
     res = {
         "metric": "D18 multi-document read: reader rows/s and HBM GB/s (% peak)",
-        "value": T / (k_ms * 1e-3), "unit": "reader rows/s", "n_gpus": 1, "steps": args.steps,
+        "value": T / (ms_step * 1e-3), "unit": "reader rows/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32 (bf16 operators)", "data": "synthetic",
         "config": {"workload": "d18", "documents": D, "rows_per_document": N, "hkv": hkv, "hq": hq,
                    "head_dim": hd, "own_rows": P, "reader_rows": T, "skip": skip, "key_splits": S,
-                   "timing": timing, "ms_per_call_eager": k_ms_eager, "ms_per_call_graph": k_ms_graph},
+                   "timing": timing, "ms_per_call_eager": ms_eager, "ms_per_call_graph": ms_graph},
         "roofline": {"bound": "hbm", "kernel": "d18_partials_kernel + d18_merge_kernel", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "algorithmic_bytes": alg_bytes, "avg_launch_ms": k_ms},
@@ -636,17 +619,8 @@ def bench_op_b(args):
     alg_bytes = B * (op_len + own_len) * hkv * d * 2 * 2 + B * hq * d * (2 + 4)
     for _ in range(args.warmup):
         call()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for a, b in ev:
-        a.record(stream)
-        call()
-        b.record(stream)
-    torch.cuda.synchronize()
-    ms_step = (time.perf_counter() - t0) * 1e3 / args.steps
-    k_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
+    ms_step, k_ms = timed_steps(call, args.steps, stream)
     achieved = alg_bytes / (k_ms * 1e-3) / 1e9
     cpu = None
     if args.cpu_sample > 0:
@@ -678,7 +652,7 @@ def bench_op_b(args):
                           f"{max(1, args.cpu_reps)} reps after 1 warm-up; {cpu_model()}")}
     res = {
         "metric": "Op B decode read (DecodeReader): decode rows/s and HBM GB/s (% peak)",
-        "value": B / (k_ms * 1e-3), "unit": "decode rows/s", "n_gpus": 1, "steps": args.steps,
+        "value": B / (ms_step * 1e-3), "unit": "decode rows/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32 (bf16 pools)", "data": "synthetic",
         "config": {"workload": "op_b", "rows": B, "operator_rows": op_len, "own_rows": own_len, "hq": hq,
@@ -748,56 +722,27 @@ def bench_decode(args):
 
     for _ in range(args.warmup):
         step()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    # Eager steps with HIP events around the whole routed read on its stream (the q . S dots, the
-    # read kernel with the top-k in its prologue, and the merge): the roofline figure counts the
-    # step's algorithmic bytes (routed pages, S, q and r) over that span, and the eager step time.
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        ev[i][0].record(stream)
-        step()
-        ev[i][1].record(stream)
-    torch.cuda.synchronize()
-    ms_eager = (time.perf_counter() - t0) * 1e3 / args.steps
-    read_ms = statistics.mean(a.elapsed_time(b) for a, b in ev)
-    achieved = (read_bytes + route_bytes) / (read_ms * 1e-3) / 1e9
+    # Eager steps: the q . S dots, the read kernel with the top-k in its prologue and the merge,
+    # K steps back to back.  The roofline figure counts the step's algorithmic bytes (routed
+    # pages, S, q and r) over the GPU span per step of the timed region.
+    ms_eager, span_eager = timed_steps(step, args.steps, stream)
 
-    # The step (routing + read, 4 launches) captured once in a HIP graph and replayed: the host
-    # launch overhead between the kernels (measured ~11 us per eager step) goes away.  Every
-    # replay is checked bit for bit against the eager result, with eager work and a
-    # synchronisation in between; on any mismatch the eager time is reported.
-    ms_graph, graph_ok = None, False
+    # The step captured once in a HIP graph and replayed.  Every replay is checked bit for bit
+    # against the eager result, with eager work and a synchronisation in between; on any
+    # mismatch the eager time is reported.
+    ms_graph = span_graph = None
+    graph_ok = False
     if not args.no_graph:
         ref_out = step().clone()
-        s2 = torch.cuda.Stream()
-        s2.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(s2):
-            step()
-        torch.cuda.current_stream().wait_stream(s2)
-        gph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(gph):
-            g_out = step()
-        graph_ok = True
-        for _ in range(3):
-            gph.replay()
-            torch.cuda.synchronize()
-            graph_ok &= bool(torch.equal(g_out, ref_out))
-            step()
-            torch.cuda.synchronize()
-        if graph_ok:
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                gph.replay()
-            torch.cuda.synchronize()
-            ms_graph = (time.perf_counter() - t0) * 1e3 / args.steps
-            graph_ok &= bool(torch.equal(g_out, ref_out))
+        gph, g_out = graph_of(step, lambda o: torch.equal(o, ref_out))
+        if gph is not None:
+            ms_graph, span_graph = timed_steps(gph.replay, args.steps, stream)
+            graph_ok = bool(torch.equal(g_out, ref_out))
     # The step runs either way; report the faster of the two measured ways (named in config).
     timing = "hip_graph" if graph_ok and ms_graph < ms_eager else "eager"
-    ms_step = ms_graph if timing == "hip_graph" else ms_eager
+    ms_step, span = (ms_graph, span_graph) if timing == "hip_graph" else (ms_eager, span_eager)
+    achieved = (read_bytes + route_bytes) / (span * 1e-3) / 1e9
 
     traffic = traffic_from_profile(args.workload)
     stream_meas = measured_stream_peak(dev)
@@ -831,7 +776,7 @@ def bench_decode(args):
                      "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic["bytes_per_launch"] if traffic else None,
                      "traffic_source": traffic["source"] if traffic else None,
-                     "algorithmic_bytes": read_bytes + route_bytes, "avg_launch_ms": read_ms,
+                     "algorithmic_bytes": read_bytes + route_bytes, "avg_launch_ms": span,
                      "routed_slots": routed_slots, "read_bytes": read_bytes, "route_bytes": route_bytes,
                      "measured_peak": stream_meas, "frac_of_measured": achieved / stream_meas},
         "cpu_baseline": cpu,
