@@ -76,16 +76,30 @@ typedef __bf16 d18_bf8 __attribute__((ext_vector_type(8)));
 constexpr int kD18Tile = 16;   // keys per score tile (the MFMA's 16 rows)
 
 constexpr float kD18Lazy = 8.f;   // log2 headroom of the running max (weights <= 2^8)
-constexpr int kD18KPad = 4;    // words of padding per staged row (conflict-free MFMA-layout reads)
-constexpr int kD18KRow = kD18MaxHd + kD18KPad;   // words per staged key row (fp32 keys fill it)
+
+// Staged rows in LDS, in 4-byte words.  Every row starts 16-byte aligned, so the MFMA operand
+// reads and the row stores are single 16-byte LDS accesses.  The paddings make them free of bank
+// conflicts on gfx950 (measured: a row stride of 8 or 24 words mod 64 for the 16-byte reads
+// of row lane % 16 at word 4 (lane / 16); 4 or 12 mod 16 for the 4-byte V reads of row
+// 4 (lane / 16) + r at word lane % 16):
+//   16-bit keys: K rows of HD / 2 + 8 words, then the V rows of HD / 2 + 4 words;
+//   fp32 keys:   K rows of HD + 4 words (the V rows stay in registers);
+//   the query parts: rows of kD18MaxHd + 16 halves.
+template <typename TK, int HD> constexpr int kD18KStride = sizeof(TK) == 4 ? HD + 4 : HD / 2 + 8;
+template <int HD> constexpr int kD18VStride = HD / 2 + 4;
+template <int HD> constexpr int kD18VBase = kD18Tile * kD18KStride<__bf16, HD>;
+constexpr int kD18WaveWords = kD18Tile * (kD18MaxHd + 12);   // covers both layouts at HD 256
+constexpr int kD18QRow = kD18MaxHd + 16;
+static_assert(kD18VBase<kD18MaxHd> + kD18Tile * kD18VStride<kD18MaxHd> <= kD18WaveWords, "16-bit K and V rows");
+static_assert(kD18Tile * kD18KStride<float, kD18MaxHd> <= kD18WaveWords, "fp32 K rows");
 
 // LDS of a partials workgroup: the query fragments (the parts of the 16 padded heads' rows: bf16
 // keys three bf16 parts, other keys fp16 hi / lo), per wave the raw key (and 16-bit value) rows of
 // its current tile and the tile's probabilities [key][head] with the heads' rescale factors, then
 // per wave and query head the state (m, l, mc, lc) and the accumulator.
-struct D18Lds {
-  unsigned short q[3][16][kD18MaxHd + 8];
-  unsigned k[kD18Waves][kD18Tile][kD18KRow];
+struct alignas(16) D18Lds {
+  unsigned short q[3][16][kD18QRow];
+  unsigned kv[kD18Waves][kD18WaveWords];
   float p[kD18Waves][kD18Tile][16];
   float alpha[kD18Waves][16];
   float st[kD18Waves][kD18MaxG][4];
@@ -122,41 +136,60 @@ struct D18Args {
   float* rmax;
 };
 
-// The query rows of the 16 padded heads: thread x holds q[g][e] for i = j * 256 + x (g = i / HD,
-// e = i % HD); heads past G hold a copy of head G - 1 (store_q writes them as 0).
-template <int HD> constexpr int kQPer = 16 * HD / kD18Threads;
-
+// The query rows of the 16 padded heads in chunks of 8 dims: chunk c = thread + 256 j is head
+// c / (HD / 8), dims 8 (c % (HD / 8)) .. + 7.  Heads 8 .. 15 are padding (G <= 8), so only the
+// chunks c < HD carry values: a thread loads at most one chunk (HD <= 256), from head
+// min(g, G - 1) so the loads are unconditional; store_q writes heads past G as 0.
 template <int HD>
-__device__ __forceinline__ void load_q(const float* __restrict__ q, int G, float (&qv)[kQPer<HD>]) {
-#pragma unroll
-  for (int j = 0; j < kQPer<HD>; ++j) {
-    const int i = j * kD18Threads + threadIdx.x;
-    const int g = i / HD, e = i % HD;
-    qv[j] = q[min(g, G - 1) * HD + e];   // unconditional: the loads issue back to back
-  }
+__device__ __forceinline__ void load_q(const float* __restrict__ q, int G, f32x4_t (&qv)[2]) {
+  constexpr int CPR = HD / 8;
+  const int c = min((int)threadIdx.x, HD - 1);
+  const int g = c / CPR, e0 = (c % CPR) * 8;
+  const f32x4_t* src = reinterpret_cast<const f32x4_t*>(q + min(g, G - 1) * HD + e0);
+  qv[0] = src[0];
+  qv[1] = src[1];
 }
 
 // The query rows, scaled to the log2 domain, into LDS (heads past G: 0): the B operand of the
 // scores, read by every wave.  For bf16 keys three bf16 parts (q = p0 + p1 + p2 to 2^-24 |q|), so
-// the bf16 keys enter the matrix cores as stored; for fp16 / fp32 keys fp16 hi + lo.
+// the bf16 keys enter the matrix cores as stored; for fp16 / fp32 keys fp16 hi + lo.  One 16-byte
+// store per part and chunk.
 template <typename TK, int HD>
-__device__ __forceinline__ void store_q(const float (&qv)[kQPer<HD>], int G, float scale_log2, D18Lds& lds) {
+__device__ __forceinline__ void store_q(const f32x4_t (&qv)[2], int G, float scale_log2, D18Lds& lds) {
+  constexpr int CPR = HD / 8, NCH = 16 * CPR;
 #pragma unroll
-  for (int j = 0; j < kQPer<HD>; ++j) {
-    const int i = j * kD18Threads + threadIdx.x;
-    const int g = i / HD, e = i % HD;
-    const float x = g < G ? qv[j] * scale_log2 : 0.f;
-    if constexpr (__is_same(TK, __bf16)) {
-      const __bf16 p0 = (__bf16)x;
-      const float r1 = x - (float)p0;
-      const __bf16 p1 = (__bf16)r1;
-      lds.q[0][g][e] = __builtin_bit_cast(unsigned short, p0);
-      lds.q[1][g][e] = __builtin_bit_cast(unsigned short, p1);
-      lds.q[2][g][e] = __builtin_bit_cast(unsigned short, (__bf16)(r1 - (float)p1));
-    } else {
-      lds.q[0][g][e] = __builtin_bit_cast(unsigned short, f16_hi(x));
-      lds.q[1][g][e] = __builtin_bit_cast(unsigned short, f16_lo(x));
+  for (int j = 0; j * kD18Threads < NCH; ++j) {
+    const int c = j * kD18Threads + (int)threadIdx.x;
+    if (c >= NCH) break;
+    const int g = c / CPR, e0 = (c % CPR) * 8;
+    const bool live = c < HD && g < G;   // c < HD: this thread's loaded chunk (j = 0)
+    unsigned w[3][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      unsigned short h[3][2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const float x = live ? qv[(2 * i + s) / 4][(2 * i + s) % 4] * scale_log2 : 0.f;
+        if constexpr (__is_same(TK, __bf16)) {
+          const __bf16 p0 = (__bf16)x;
+          const float r1 = x - (float)p0;
+          const __bf16 p1 = (__bf16)r1;
+          h[0][s] = __builtin_bit_cast(unsigned short, p0);
+          h[1][s] = __builtin_bit_cast(unsigned short, p1);
+          h[2][s] = __builtin_bit_cast(unsigned short, (__bf16)(r1 - (float)p1));
+        } else {
+          h[0][s] = __builtin_bit_cast(unsigned short, f16_hi(x));
+          h[1][s] = __builtin_bit_cast(unsigned short, f16_lo(x));
+          h[2][s] = 0;
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < 3; ++p) w[p][i] = (unsigned)h[p][0] | ((unsigned)h[p][1] << 16);
     }
+    constexpr int NP = __is_same(TK, __bf16) ? 3 : 2;
+#pragma unroll
+    for (int p = 0; p < NP; ++p)
+      *reinterpret_cast<u32x4_t*>(&lds.q[p][g][e0]) = u32x4_t{w[p][0], w[p][1], w[p][2], w[p][3]};
   }
 }
 
@@ -204,8 +237,11 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int hs = lane % 16, k4 = lane / 16;              // score layout
+  const bool hi16 = (lane & 16) != 0, hi32 = (lane & 32) != 0;   // halves of the permlane swaps
   const int grp = lane / TPR, e0 = (lane % TPR) * EPL;   // load / value layout
   const int w0 = e0 * (int)sizeof(TK) / 4;               // this lane's first word of a row
+  constexpr int KS = kD18KStride<TK, HD>;               // staged K row stride (words)
+  unsigned* const kvw = lds.kv[wv];                      // this wave's staged rows
   float acc[GP][EPL];       // VALU P.V: heads x this lane's EPL dims
   f32x4_t accm[HD / 16];    // MFMA P.V: block b, heads 4 k4 .. + 3 at dim 32 (b / 2) + 2 hs + b % 2
 #pragma unroll
@@ -232,12 +268,13 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
   };
   // One 16-key tile (its K and V rows in kr, vr; keys t0 .. t0 + 15 of the split).
   auto tile = [&](const u32x4_t (&kr)[NI], const u32x4_t (&vr)[NI], int t0) {
-    // The tile's K rows to LDS (16-bit keys: the V rows beside them, words HD / 2 .. HD - 1).
+    // The tile's K rows to LDS (16-bit keys: then the V rows).
 #pragma unroll
-    for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4_t*>(&lds.k[wv][i * KPI + grp][w0]) = kr[i];
+    for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4_t*>(&kvw[(i * KPI + grp) * KS + w0]) = kr[i];
     if constexpr (kPvMfma) {
 #pragma unroll
-      for (int i = 0; i < NI; ++i) *reinterpret_cast<u32x4_t*>(&lds.k[wv][i * KPI + grp][HD / 2 + w0]) = vr[i];
+      for (int i = 0; i < NI; ++i)
+        *reinterpret_cast<u32x4_t*>(&kvw[kD18VBase<HD> + (i * KPI + grp) * kD18VStride<HD> + w0]) = vr[i];
     }
     wave_sync_lds();
     // One accumulator per product, so the MFMA chains are independent; summed at the end.
@@ -246,7 +283,7 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
     for (int kb = 0; kb < KB; ++kb) {
       const int qo = 32 * kb + 8 * k4;
       if constexpr (__is_same(TK, __bf16)) {
-        const d18_bf8 kv = *reinterpret_cast<const d18_bf8*>(&lds.k[wv][hs][qo / 2]);
+        const d18_bf8 kv = *reinterpret_cast<const d18_bf8*>(&kvw[hs * KS + qo / 2]);
         s0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, *reinterpret_cast<const d18_bf8*>(&lds.q[0][hs][qo]), s0, 0, 0, 0);
         s1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, *reinterpret_cast<const d18_bf8*>(&lds.q[1][hs][qo]), s1, 0, 0, 0);
         s2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, *reinterpret_cast<const d18_bf8*>(&lds.q[2][hs][qo]), s2, 0, 0, 0);
@@ -254,8 +291,8 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
         const d18_half8 qh = *reinterpret_cast<const d18_half8*>(&lds.q[0][hs][qo]);
         const d18_half8 ql = *reinterpret_cast<const d18_half8*>(&lds.q[1][hs][qo]);
         if constexpr (kF32) {
-          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][qo]);
-          const f32x4_t b = *reinterpret_cast<const f32x4_t*>(&lds.k[wv][hs][qo + 4]);
+          const f32x4_t a = *reinterpret_cast<const f32x4_t*>(&kvw[hs * KS + qo]);
+          const f32x4_t b = *reinterpret_cast<const f32x4_t*>(&kvw[hs * KS + qo + 4]);
           d18_half8 ka, kl;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
@@ -268,7 +305,7 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
           s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, s1, 0, 0, 0);
           s2 = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh, s2, 0, 0, 0);
         } else {
-          const d18_half8 ka = *reinterpret_cast<const d18_half8*>(&lds.k[wv][hs][qo / 2]);
+          const d18_half8 ka = *reinterpret_cast<const d18_half8*>(&kvw[hs * KS + qo / 2]);
           s0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qh, s0, 0, 0, 0);
           s1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql, s1, 0, 0, 0);
         }
@@ -283,8 +320,8 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
       ok[r] = t0 + 4 * k4 + r < n;
       if (ok[r]) mx = fmaxf(mx, sc[r]);
     }
-    mx = fmaxf(mx, shfl_xor(mx, 16));
-    mx = fmaxf(mx, shfl_xor(mx, 32));
+    mx = fmaxf(mx, swap_partner<16>(mx, hi16));
+    mx = fmaxf(mx, swap_partner<32>(mx, hi32));
     // The running max moves only when the tile's max passes it by more than 2^8: the weights stay
     // <= 256 and most tiles need no rescale of the accumulators (the state (m, l, acc) stays exact:
     // a rescale is a power of two).
@@ -298,8 +335,8 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
       pr[r] = ok[r] ? __builtin_amdgcn_exp2f(sc[r] - mn) : 0.f;
       ps += pr[r];
     }
-    ps += shfl_xor(ps, 16);
-    ps += shfl_xor(ps, 32);
+    ps += swap_partner<16>(ps, hi16);
+    ps += swap_partner<32>(ps, hi32);
     l = l * a + ps;
     m = mn;
     if (cmode == 2) {
@@ -307,15 +344,15 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) mcx = fmaxf(mcx, sc[r]);
-      mcx = fmaxf(mcx, shfl_xor(mcx, 16));
-      mcx = fmaxf(mcx, shfl_xor(mcx, 32));
+      mcx = fmaxf(mcx, swap_partner<16>(mcx, hi16));
+      mcx = fmaxf(mcx, swap_partner<32>(mcx, hi32));
       const float mcn = fmaxf(mc, mcx);
       float cs = 0.f;
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         if (ok[r] && j_base + t0 + 4 * k4 + r >= skip_c) cs += __builtin_amdgcn_exp2f(sc[r] - mcn);
-      cs += shfl_xor(cs, 16);
-      cs += shfl_xor(cs, 32);
+      cs += swap_partner<16>(cs, hi16);
+      cs += swap_partner<32>(cs, hi32);
       lc = lc * rescale(mc, mcn) + cs;
       mc = mcn;
     }
@@ -365,7 +402,7 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
       for (int c = 0; c < HD / 32; ++c) {
         unsigned w[4];   // keys 4 k4 + r, dims 32 c + 2 hs (low half) and + 1 (high half)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) w[r] = lds.k[wv][4 * k4 + r][HD / 2 + 16 * c + hs];
+        for (int r = 0; r < 4; ++r) w[r] = kvw[kD18VBase<HD> + (4 * k4 + r) * kD18VStride<HD> + 16 * c + hs];
         const unsigned ev01 = (w[0] & 0xffffu) | (w[1] << 16), ev23 = (w[2] & 0xffffu) | (w[3] << 16);
         const unsigned od01 = (w[0] >> 16) | (w[1] & 0xffff0000u), od23 = (w[2] >> 16) | (w[3] & 0xffff0000u);
         const u32x4_t be = {ev01, ev23, ev01, ev23}, bo = {od01, od23, od01, od23};
@@ -414,7 +451,7 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
   };
   constexpr int kStep = kD18Waves * kD18Tile;   // a wave's next tile
   const int t_first = wv * kD18Tile;
-  float qv[kQPer<HD>];
+  f32x4_t qv[2];
   if constexpr (!kF32) {
     // 16-bit rows: two tiles in registers, the next one loading while this one computes (loads
     // past the split return 0 and touch no memory, so every load is unconditional).  The query
