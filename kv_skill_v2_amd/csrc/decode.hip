@@ -511,8 +511,9 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
 // Page-grouped runs: entry i = (row i / kk, routed chunk i % kk) of the n = M * kk entries gets
 // its rank among the entries ordered by (page, i); unrouted entries sort last.  Workgroup b
 // ranks entries [64b, 64b + 64): every workgroup builds all n keys in LDS, then 8 threads per
-// entry each count the keys before it in one eighth of the list, and an xor-shuffle over the 8
-// adds the counts (integers: the order of the adds does not matter).
+// entry each count the keys before it, thread t of the 8 over keys t, t + 8, ... (the 8 read
+// consecutive words: no bank conflict), and a reduction over the 8 adds the counts (integers:
+// the order of the adds does not matter).
 constexpr int kOrderMax = 1024;
 constexpr int kOrderPerWg = 64;
 __global__ __launch_bounds__(512) void page_order_kernel(
@@ -531,16 +532,12 @@ __global__ __launch_bounds__(512) void page_order_kernel(
   int cnt = 0;
   if (i < n) {
     const int ki = key[i];
-    const int per = (n + 7) / 8;
-    const int j1 = min(n, (part + 1) * per);
-    for (int j = part * per; j < j1; ++j) {
+    for (int j = part; j < n; j += 8) {
       const int kj = key[j];
       cnt += (kj < ki || (kj == ki && j < i)) ? 1 : 0;
     }
   }
-  cnt += __shfl_xor(cnt, 1, kWave);
-  cnt += __shfl_xor(cnt, 2, kWave);
-  cnt += __shfl_xor(cnt, 4, kWave);
+  cnt = (int)group_sum<8>((float)cnt);   // counts <= 1024: exact in fp32, summed by DPP
   if (i < n && part == 0) order[cnt] = i;
 }
 

@@ -163,6 +163,51 @@ def test_page_grouped_runs(dev, M, top_k, nsplit):
         _check_close(r[m], ref.view(-1), f"row {m} (library {g})")
 
 
+@pytest.mark.parametrize("softmax", [True, False])
+def test_page_grouped_shared_pages_and_unrouted(dev, softmax):
+    """Page-grouped runs (one split per page, merge in the second kernel): every row routes its
+    library's shared chunk (48 readers of one page), every 7th row routes 5 of its 8 slots
+    (unrouted entries), and chunk 3 of library 1 sits on the page of chunk 5 of library 0 with 9
+    fewer valid slots (one page read with two lengths).  Bit-identical to one call per row (never
+    grouped) and within the bar of the oracle."""
+    say("page-grouped shared pages", dict(softmax=softmax))
+    d, N, M, kk = 512, 128, 96, 8
+    P = synth.pool([24, 16], N, d, device="cpu", tail_lo=1)
+    a0, a1 = int(P.chunk_ptr[0]), int(P.chunk_ptr[1])
+    cp, nv = P.chunk_page.clone(), P.chunk_nvalid.clone()
+    cp[a1 + 3] = cp[a0 + 5]
+    nv[a1 + 3] = max(1, int(nv[a0 + 5]) - 9)
+    lib = ops.PagedLibrary(P.pages.to(dev), cp.to(dev), nv.to(dev), P.chunk_ptr.to(dev), P.S.to(dev),
+                           n_chunks=P.n_chunks, nvalid=nv.tolist())
+    groups = [m % 2 for m in range(M)]
+    gen = torch.Generator().manual_seed(31)
+    idx = torch.full((M, kk), -1, dtype=torch.int32)
+    for m, g in enumerate(groups):
+        shared = 5 if g == 0 else 3
+        k = kk if m % 7 else kk - 3
+        rest = [c for c in torch.randperm(P.n_chunks[g], generator=gen).tolist() if c != shared]
+        idx[m, :k] = torch.tensor([shared] + rest[:k - 1], dtype=torch.int32)
+    wsel = torch.softmax(torch.randn(M, kk, generator=gen), -1) * (idx >= 0)
+    q = synth.queries(M, d, device="cpu", seed=33)
+    qg = torch.tensor(groups, dtype=torch.int32, device=dev)
+    r = ops.library_read_decode(q.to(dev), lib, idx.to(dev), wsel.to(dev), qg, softmax=softmax, nsplit=1)
+    single = torch.stack([ops.library_read_decode(q[m:m + 1].to(dev), lib, idx[m:m + 1].to(dev),
+                                                  wsel[m:m + 1].to(dev), qg[m:m + 1], softmax=softmax,
+                                                  nsplit=1)[0] for m in range(M)])
+    assert torch.equal(r, single)
+    pages = P.pages.double()
+    for m, g in enumerate(groups):
+        a, b = int(P.chunk_ptr[g]), int(P.chunk_ptr[g + 1])
+        K = pages[cp[a:b].long()]
+        Mk = torch.arange(N).view(1, N) < nv[a:b].long().view(-1, 1)
+        w = torch.zeros(1, 1, b - a, dtype=torch.float64)
+        for j in range(kk):
+            if int(idx[m, j]) >= 0:
+                w[0, 0, int(idx[m, j])] = float(wsel[m, j])
+        ref, _ = O.read(q[m].view(1, 1, -1).double(), K, Mk, w, 12.0, read_softmax=softmax)
+        _check_close(r[m], ref.view(-1), f"row {m} (library {g})")
+
+
 def test_read_is_linear_in_route_weights(dev):
     say("linearity in w", dict(d=256))
     P = synth.pool([5, 5], 64, 256, device="cpu")
