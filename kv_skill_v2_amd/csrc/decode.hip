@@ -66,12 +66,18 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 // Buffer descriptor word 3 for CDNA (raw buffer, 32-bit format fields unused by b128 loads).
 constexpr int kBufferWord3 = 0x00020000;
 // Cache policy of the page loads: nt (nontemporal).  Streamed reads measured 7.1 TB/s with it
-// against 6.2 TB/s without on MI355X.
+// against 6.2 TB/s without on MI355X.  Pages that more than one entry of a page-grouped run reads
+// load with the default policy instead, so that the page stays in L2 for its other readers.
 constexpr int kLoadNT = 2;
+constexpr int kLoadShared = 0;
+// A position of the page order: the entry in the low bits, bit 30 set when other entries read
+// the same page.
+constexpr int kOrderShared = 1 << 30;
 
 struct DecodeWorkspace {
   int* counters;    // [max_rows] arrivals per query (0 between calls; in-kernel merge only)
-  int* order;       // [M * kk]   (row, routed chunk) entries ranked by page (page-grouped runs)
+  int* order;       // [M * kk]   (row, routed chunk) entries ranked by page (page-grouped runs),
+                    //            kOrderShared set when more than one entry reads the page
   float2* part_ml;  // [units]    (max in log2 units, sum) per partial; sum 0 = empty
   float* part_acc;  // [units, d] un-normalised value sums
 };
@@ -220,14 +226,14 @@ struct TileCtx {
 // Issue the SPT*CB 16-byte loads of the slot rows t0 .. t0+SPT-1.  Rows past s1 re-read row
 // s1-1 (excluded from the softmax through nval) and columns past d re-read the last 8 columns
 // (their q is 0 and their acc is never stored).  Nontemporal: pages are streamed once.
-template <int SPT, int CB>
+template <int SPT, int CB, int AUX = kLoadNT>
 __device__ __forceinline__ void load_tile(u32x4 (&kv)[SPT][CB], const TileCtx<CB>& c, int t0) {
 #pragma unroll
   for (int j = 0; j < SPT; ++j) {
     const int soff = min(t0 + j, c.s1 - 1) * c.row_bytes;
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
-      kv[j][cb] = __builtin_amdgcn_raw_buffer_load_b128(c.rsrc, c.voff[cb], soff, kLoadNT);
+      kv[j][cb] = __builtin_amdgcn_raw_buffer_load_b128(c.rsrc, c.voff[cb], soff, AUX);
   }
   __builtin_amdgcn_sched_barrier(0);
 }
@@ -318,7 +324,9 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
   // page-ranked entries; otherwise the unit is the block index.
   const int pos = grouped ? xcd_remap(blockIdx.x, gridDim.x) : blockIdx.x;
   const int s = pos % nsplit;
-  const int mj = grouped ? ws.order[pos / nsplit] : pos / nsplit;
+  const int word = grouped ? __builtin_amdgcn_readfirstlane(ws.order[pos / nsplit]) : 0;
+  const int mj = grouped ? (word & (kOrderShared - 1)) : pos / nsplit;
+  const bool shared_page = (word & kOrderShared) != 0;   // workgroup-uniform
   const int unit = mj * nsplit + s;
   const int m = mj / kk;
   const int lane = threadIdx.x & (kWave - 1);
@@ -407,10 +415,18 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
     const int step = NW * SPT;
     const int first = s0 + wv * SPT;
     const int ntile = first < s1 ? (s1 - first + step - 1) / step : 0;
-    for (int i = 0; i < ntile; ++i) {
-      u32x4 ka[SPT][CB];
-      load_tile<SPT, CB>(ka, ctx, first + i * step);
-      consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, acc, mrun, lrun);
+    if (shared_page) {
+      for (int i = 0; i < ntile; ++i) {
+        u32x4 ka[SPT][CB];
+        load_tile<SPT, CB, kLoadShared>(ka, ctx, first + i * step);
+        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, acc, mrun, lrun);
+      }
+    } else {
+      for (int i = 0; i < ntile; ++i) {
+        u32x4 ka[SPT][CB];
+        load_tile<SPT, CB>(ka, ctx, first + i * step);
+        consume_tile<SPT, CB>(ka, ctx, first + i * step, qv, acc, mrun, lrun);
+      }
     }
 
     // Merge the NW waves of this workgroup: rescale each wave to the common max, then a tree
@@ -513,7 +529,8 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
 // ranks entries [64b, 64b + 64): every workgroup builds all n keys in LDS, then 8 threads per
 // entry each count the keys before it, thread t of the 8 over keys t, t + 8, ... (the 8 read
 // consecutive words: no bank conflict), and a reduction over the 8 adds the counts (integers:
-// the order of the adds does not matter).
+// the order of the adds does not matter).  The same pass counts the entries on the entry's page,
+// and entries of a page read more than once are marked (kOrderShared).
 constexpr int kOrderMax = 1024;
 constexpr int kOrderPerWg = 64;
 __global__ __launch_bounds__(512) void page_order_kernel(
@@ -529,16 +546,18 @@ __global__ __launch_bounds__(512) void page_order_kernel(
   __syncthreads();
   const int i = blockIdx.x * kOrderPerWg + threadIdx.x / 8;   // the entry this thread helps rank
   const int part = threadIdx.x & 7;
-  int cnt = 0;
+  int cnt = 0, same = 0;
   if (i < n) {
     const int ki = key[i];
     for (int j = part; j < n; j += 8) {
       const int kj = key[j];
       cnt += (kj < ki || (kj == ki && j < i)) ? 1 : 0;
+      same += kj == ki ? 1 : 0;
     }
   }
   cnt = (int)group_sum<8>((float)cnt);   // counts <= 1024: exact in fp32, summed by DPP
-  if (i < n && part == 0) order[cnt] = i;
+  same = (int)group_sum<8>((float)same);
+  if (i < n && part == 0) order[cnt] = i | (same > 1 && key[i] != 0x7fffffff ? kOrderShared : 0);
 }
 
 // Second pass of a large launch: one workgroup per query row merges its partials (the same
