@@ -411,7 +411,9 @@ __global__ __launch_bounds__(8 * kWave) void route_dots_kernel(
   for (int cb = 0; cb < CB4; ++cb) {
     const int i = (cb * kWave + lane) * 4;
     qv[cb] = i < d ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-    sv[cb] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(srow + min(i, d - 4)));
+    // Default cache policy: the nontemporal hint measured slower here (5.97 against 5.27 us on
+    // 64 rows x 2177 chunks, 9.62 against 7.03 us on 64 rows over 8 libraries of 64 chunks).
+    sv[cb] = *reinterpret_cast<const f32x4*>(srow + min(i, d - 4));
   }
   float a = 0.f;
 #pragma unroll
