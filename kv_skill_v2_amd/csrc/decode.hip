@@ -549,6 +549,7 @@ __global__ __launch_bounds__(512) void page_order_kernel(
   int cnt = 0, same = 0;
   if (i < n) {
     const int ki = key[i];
+#pragma unroll 8
     for (int j = part; j < n; j += 8) {
       const int kj = key[j];
       cnt += (kj < ki || (kj == ki && j < i)) ? 1 : 0;
