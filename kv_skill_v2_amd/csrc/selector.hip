@@ -7,7 +7,9 @@
 //   selector_apply_kernel    out[b] = sum_{j<k} w[b,j] * alpha * delta[b*k+j] / (rel + 1e-6),
 //                            rel = |delta[b*k+j]| / (|h[b]| + 1e-6), alpha = exp(*log_alpha): the
 //                            matched-norm rescale and weighting of LayerSelector.apply, summed
-//                            over the k selected layers of a token (k = 1: apply itself)
+//                            over the k selected layers of a token (k = 1: apply itself);
+//                            selector_apply_regs_kernel, the same for k <= 2 with the rows held
+//                            in registers (one pass of loads, one workgroup sum for all norms)
 //   gate_scale_kernel        scale[m] = gain_scale * exp(log_gain[p]) *
 //                            sigmoid(<hn[t], gate_w> + gate_b[p]), t = row_token[m],
 //                            p = row_pos[m]: the per-row factor of delta = scale * B(r)
@@ -131,6 +133,76 @@ __device__ __forceinline__ float row_dot(const float* a, const float* b, int d, 
 struct Fma {
   __device__ float operator()(float x, float y, float acc) const { return fmaf(x, y, acc); }
 };
+
+// selector_apply_kernel for 16-byte rows of d <= 4 * kRowThreads * kApplyPer and K <= 2 kept
+// layers: the thread's pieces of h and of the K update rows load together and stay in registers,
+// the K + 1 norms are summed in one fixed-order workgroup pass, and the output comes from the
+// registers.  Every sum runs in the order of row_dot / block_sum and of the general kernel's
+// output loop, so the result is bit-identical to it.
+constexpr int kApplyPer = 8;
+template <int K>
+__global__ __launch_bounds__(kRowThreads) void selector_apply_regs_kernel(
+    int d, const float* __restrict__ delta, long long ldd, const float* __restrict__ h, long long ldh,
+    const float* __restrict__ w_row, const float* __restrict__ log_alpha, float* __restrict__ out,
+    long long ldo) {
+  __shared__ float red[K + 1][kRowThreads / kWave];
+  const int b = blockIdx.x;
+  const int d4 = d / 4;
+  const f32x4* rows[K + 1];
+  rows[0] = reinterpret_cast<const f32x4*>(h + (long long)b * ldh);
+#pragma unroll
+  for (int j = 0; j < K; ++j) rows[j + 1] = reinterpret_cast<const f32x4*>(delta + ((long long)b * K + j) * ldd);
+  f32x4 x[K + 1][kApplyPer];
+#pragma unroll
+  for (int u = 0; u < kApplyPer; ++u) {
+    const int i = min((int)threadIdx.x + u * kRowThreads, d4 - 1);   // clamped: unconditional loads
+#pragma unroll
+    for (int j = 0; j <= K; ++j) x[j][u] = rows[j][i];
+  }
+  float ss[K + 1];
+#pragma unroll
+  for (int j = 0; j <= K; ++j) {
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < kApplyPer; ++u)
+      if ((int)threadIdx.x + u * kRowThreads < d4) {
+        acc = fmaf(x[j][u][0], x[j][u][0], acc);
+        acc = fmaf(x[j][u][1], x[j][u][1], acc);
+        acc = fmaf(x[j][u][2], x[j][u][2], acc);
+        acc = fmaf(x[j][u][3], x[j][u][3], acc);
+      }
+    ss[j] = wave_sum(acc);
+  }
+  const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j <= K; ++j) red[j][wv] = ss[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j <= K; ++j) ss[j] = (red[j][0] + red[j][1]) + (red[j][2] + red[j][3]);
+  const float hnorm = sqrtf(ss[0]);
+  const float alpha = __expf(*log_alpha);
+  float coef[K];
+#pragma unroll
+  for (int j = 0; j < K; ++j) {
+    const float rel = sqrtf(ss[j + 1]) / (hnorm + 1e-6f);
+    coef[j] = w_row[(long long)b * K + j] * alpha / (rel + 1e-6f);
+  }
+  f32x4* o = reinterpret_cast<f32x4*>(out + (long long)b * ldo);
+#pragma unroll
+  for (int u = 0; u < kApplyPer; ++u) {
+    const int i = (int)threadIdx.x + u * kRowThreads;
+    if (i < d4) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < K; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[e] = fmaf(coef[j], x[j + 1][u][e], acc[e]);
+      o[i] = acc;
+    }
+  }
+}
 
 // One workgroup per output row b.
 __global__ __launch_bounds__(kRowThreads) void selector_apply_kernel(
@@ -256,9 +328,18 @@ extern "C" int xenc_selector_apply(int B, int k, int d, const float* delta, long
   if (!delta || !h || !w_row || !log_alpha || !out) return XENC_ENULL;
   const int vec4 = (d % 4 == 0 && ldd % 4 == 0 && ldh % 4 == 0 && ldo % 4 == 0 && aligned16(delta) &&
                     aligned16(h) && aligned16(out)) ? 1 : 0;
-  hipLaunchKernelGGL(selector_apply_kernel, dim3(B), dim3(kRowThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), k, d, delta, ldd, h, ldh, w_row, log_alpha,
-                     out, ldo, vec4);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (vec4 && k <= 2 && d / 4 <= kRowThreads * kApplyPer) {
+    if (k == 1)
+      hipLaunchKernelGGL(selector_apply_regs_kernel<1>, dim3(B), dim3(kRowThreads), 0, st, d, delta, ldd, h, ldh,
+                         w_row, log_alpha, out, ldo);
+    else
+      hipLaunchKernelGGL(selector_apply_regs_kernel<2>, dim3(B), dim3(kRowThreads), 0, st, d, delta, ldd, h, ldh,
+                         w_row, log_alpha, out, ldo);
+    return check_launch();
+  }
+  hipLaunchKernelGGL(selector_apply_kernel, dim3(B), dim3(kRowThreads), 0, st, k, d, delta, ldd, h, ldh, w_row,
+                     log_alpha, out, ldo, vec4);
   return check_launch();
 }
 
