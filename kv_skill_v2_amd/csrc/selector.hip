@@ -43,7 +43,30 @@ __device__ __forceinline__ void select_weights_row(const float* __restrict__ zr,
   }
   float kept_v = -INFINITY;   // lane j < k ends with the j-th kept value and index
   int kept_i = 0;
-  for (int r = 0; r < k; ++r) {
+  if (n <= kWave) {
+    // One candidate per lane: its rank is the number of larger keys (the keys are distinct),
+    // counted over the n lanes by readlane; the candidate of rank r then goes to lane r.  The
+    // same selection as the rounds below, without their cross-lane shuffles.
+    const unsigned klo = (unsigned)key[0], khi = (unsigned)(key[0] >> 32);
+    int rank = 0;
+    for (int c = 0; c < n; ++c) {
+      const unsigned long long kc =
+          ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)khi, c) << 32) |
+          (unsigned)__builtin_amdgcn_readlane((int)klo, c);
+      rank += kc > key[0] ? 1 : 0;
+    }
+    for (int r = 0; r < k; ++r) {
+      const unsigned long long hit = __ballot(lane < n && rank == r);
+      // Exactly one lane has rank r < k <= n.
+      const int c = __builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit));
+      const float vc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v[0]), c));
+      if (lane == r) {
+        kept_v = vc;
+        kept_i = c;
+      }
+    }
+  }
+  for (int r = 0; n > kWave && r < k; ++r) {
     unsigned long long best = key[0];
 #pragma unroll
     for (int u = 1; u < 4; ++u) best = key[u] > best ? key[u] : best;
@@ -277,28 +300,78 @@ __global__ __launch_bounds__(kRowThreads) void multi_depth_prepare_kernel(
   __shared__ int kept[64];
   const int b = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
+  const float* hrow = hn + (long long)b * ldh;
+  // 16-byte rows of d_r <= 4 * kRowThreads * kApplyPer: this thread's pieces of the gate dot load
+  // before the selection, so that their latency overlaps it, and are summed afterwards in
+  // row_dot's order (bit-identical to gate_scale_kernel's sum).
+  const int d4 = d_r / 4;
+  const bool pre = vec4_h && d4 <= kRowThreads * kApplyPer;
+  f32x4 hx[kApplyPer], gx[kApplyPer];
+  if (pre) {
+#pragma unroll
+    for (int u = 0; u < kApplyPer; ++u) {
+      const int i = min((int)threadIdx.x + u * kRowThreads, d4 - 1);   // clamped: unconditional loads
+      hx[u] = reinterpret_cast<const f32x4*>(hrow)[i];
+      gx[u] = reinterpret_cast<const f32x4*>(gate_w)[i];
+    }
+  }
   if (threadIdx.x < kWave) {
     select_weights_row(z + (long long)b * ldz, n, k, lane, w + (long long)b * ldw, idx + (long long)b * lds,
                        w_sel + (long long)b * lds);
     if (lane < k) kept[lane] = idx[(long long)b * lds + lane];
   }
-  // The gate dot does not depend on the selection: it runs while wave 0 selects (row_dot's
-  // barriers also publish kept[]).
-  const float s = row_dot(hn + (long long)b * ldh, gate_w, d_r, vec4_h, red, Fma());
-  for (int j = 0; j < k; ++j) {
-    const int p = kept[j];
-    const float* src = q_all + (long long)p * q_depth_stride + (long long)b * q_token_stride;
-    float* dst = q_rows + ((long long)b * k + j) * ldr;
+  // The gate dot does not depend on the selection; block_sum's barriers also publish kept[].
+  float s;
+  if (pre) {
+    float acc = 0.f;
+#pragma unroll
+    for (int u = 0; u < kApplyPer; ++u)
+      if ((int)threadIdx.x + u * kRowThreads < d4) {
+        acc = fmaf(hx[u][0], gx[u][0], acc);
+        acc = fmaf(hx[u][1], gx[u][1], acc);
+        acc = fmaf(hx[u][2], gx[u][2], acc);
+        acc = fmaf(hx[u][3], gx[u][3], acc);
+      }
+    s = block_sum(acc, red);
+  } else {
+    s = row_dot(hrow, gate_w, d_r, vec4_h, red, Fma());
+  }
+  // The kept depths' query rows, up to four rows' loads in flight before their stores.
+  for (int j0 = 0; j0 < k; j0 += 4) {
+    const float* src[4];
+    float* dst[4];
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int j = min(j0 + jj, k - 1);
+      src[jj] = q_all + (long long)kept[j] * q_depth_stride + (long long)b * q_token_stride;
+      dst[jj] = q_rows + ((long long)b * k + j) * ldr;
+    }
+    const int nj = min(4, k - j0);
     if (vec4_q) {
-      for (int i = threadIdx.x; i < d / 4; i += kRowThreads)
-        reinterpret_cast<f32x4*>(dst)[i] = reinterpret_cast<const f32x4*>(src)[i];
+#pragma unroll 2
+      for (int i = threadIdx.x; i < d / 4; i += kRowThreads) {
+        f32x4 t[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) t[jj] = reinterpret_cast<const f32x4*>(src[jj])[i];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          if (jj < nj) reinterpret_cast<f32x4*>(dst[jj])[i] = t[jj];
+      }
     } else {
-      for (int e = threadIdx.x; e < d; e += kRowThreads) dst[e] = src[e];
+      for (int e = threadIdx.x; e < d; e += kRowThreads) {
+        float t[4];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) t[jj] = src[jj][e];
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          if (jj < nj) dst[jj][e] = t[jj];
+      }
     }
-    if (threadIdx.x == 0) {
-      const float g = 1.f / (1.f + __expf(-(s + gate_b[p])));
-      scale[(long long)b * k + j] = gain_scale * __expf(log_gain[p]) * g;
-    }
+  }
+  if (threadIdx.x < k) {
+    const int p = kept[threadIdx.x];
+    const float g = 1.f / (1.f + __expf(-(s + gate_b[p])));
+    scale[(long long)b * k + threadIdx.x] = gain_scale * __expf(log_gain[p]) * g;
   }
 }
 
