@@ -559,6 +559,41 @@ __device__ __forceinline__ void d18_unit(int G, const TK* __restrict__ K, const 
   }
 }
 
+// Max over each aligned group of 16 lanes (one row), every lane of the row ending with it (DPP).
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
+  return fmaxf(v, dpp_f<0x140>(v));   // row_mirror
+}
+
+// Max over the wave: the rows by DPP, then across rows by the permlane swaps (VALU only).
+__device__ __forceinline__ float wave_max64(float v) {
+  v = row_max(v);
+  unsigned u = __float_as_uint(v);
+  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  u = __float_as_uint(v);
+  r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// The value of lane N of this lane's 16-lane row (DPP row_newbcast).
+template <int N>
+__device__ __forceinline__ float row_bcast(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x150 + N, 0xF, 0xF, false));
+}
+
+// a += sum over the splits s < S (in split order) of v[s] times the factor of split s, which lane
+// s % 16 of the row holds (f0 for s < 16, f1 for s >= 16).
+template <int S0>
+__device__ __forceinline__ void sum_splits(const float (&v)[kD18MaxSplits], float f0, float f1, int S, float& a) {
+  if constexpr (S0 < kD18MaxSplits) {
+    if (S0 < S) a = fmaf(v[S0], row_bcast<S0 % 16>(S0 < 16 ? f0 : f1), a);
+    sum_splits<S0 + 1>(v, f0, f1, S, a);
+  }
+}
+
 // Routing weight of document d (lane d; has = d < D) from r: one-hot at force, wfix, or the
 // softmax of beta * r over the top_k largest (ties to the lower index, ranked over 64-bit order
 // keys as the routing top-k does).  Called by whole waves.
@@ -579,17 +614,9 @@ __device__ __forceinline__ float doc_weight(float r, bool has, int d, int D, flo
     }
     keep = has && rank < top_k;
   }
-  const float mx = wave_max(keep ? logit : -INFINITY);
+  const float mx = wave_max64(keep ? logit : -INFINITY);
   const float e = keep ? expf(logit - mx) : 0.f;
-  return e / wave_sum(e);
-}
-
-// Max over each aligned group of 16 lanes (one row), every lane of the row ending with it (DPP).
-__device__ __forceinline__ float row_max(float v) {
-  v = fmaxf(v, dpp_f<0xB1>(v));    // quad_perm [1,0,3,2]
-  v = fmaxf(v, dpp_f<0x4E>(v));    // quad_perm [2,3,0,1]
-  v = fmaxf(v, dpp_f<0x141>(v));   // row_half_mirror
-  return fmaxf(v, dpp_f<0x140>(v));   // row_mirror
+  return e / group_sum<kWave>(e);
 }
 
 // One workgroup of 2 waves per (row t, kv head h, query head g) and block of 16 output dims:
@@ -615,7 +642,6 @@ __global__ __launch_bounds__(kD18MergeThreads) void d18_merge_kernel(const D18Ar
   const int t = th / A.hkv, h = th % A.hkv;
   const int lane = threadIdx.x & (kWave - 1), wv = threadIdx.x / kWave;
   const int row = threadIdx.x / kD18MergeDims, j = threadIdx.x % kD18MergeDims;
-  const int rbase = (lane / kD18MergeDims) * kD18MergeDims;   // this row's first lane in the wave
   const int e = blockIdx.y * kD18MergeDims + j;
   const int ec = min(e, hd - 1);   // lanes past hd load a valid dim and store nothing
   const f32x4_t empty = {-INFINITY, 0.f, -INFINITY, 0.f};
@@ -633,9 +659,7 @@ __global__ __launch_bounds__(kD18MergeThreads) void d18_merge_kernel(const D18Ar
     const float L = group_sum<16>(s0[1] * f0 + s1[1] * f1);
     const float Lc = group_sum<16>(s0[3] * rescale(s0[2], Mc) + s1[3] * rescale(s1[2], Mc));
     float a = 0.f;
-#pragma unroll
-    for (int s = 0; s < kD18MaxSplits; ++s)
-      if (s < S) a = fmaf(v[s], __shfl(s < 16 ? f0 : f1, rbase + (s & 15)), a);
+    sum_splits<0>(v, f0, f1, S, a);
     if (mine) {
       ua[u][j] = a;
       if (j == 0) ust[u] = f32x4_t{M, L, Mc, Lc};
