@@ -567,17 +567,6 @@ __device__ __forceinline__ float row_max(float v) {
   return fmaxf(v, dpp_f<0x140>(v));   // row_mirror
 }
 
-// Max over the wave: the rows by DPP, then across rows by the permlane swaps (VALU only).
-__device__ __forceinline__ float wave_max64(float v) {
-  v = row_max(v);
-  unsigned u = __float_as_uint(v);
-  auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  u = __float_as_uint(v);
-  r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
 // The value of lane N of this lane's 16-lane row (DPP row_newbcast).
 template <int N>
 __device__ __forceinline__ float row_bcast(float x) {
@@ -614,9 +603,9 @@ __device__ __forceinline__ float doc_weight(float r, bool has, int d, int D, flo
     }
     keep = has && rank < top_k;
   }
-  const float mx = wave_max64(keep ? logit : -INFINITY);
+  const float mx = wave_max(keep ? logit : -INFINITY);
   const float e = keep ? expf(logit - mx) : 0.f;
-  return e / group_sum<kWave>(e);
+  return e / wave_sum(e);
 }
 
 // One workgroup of 2 waves per (row t, kv head h, query head g) and block of 16 output dims:

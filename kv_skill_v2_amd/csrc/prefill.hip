@@ -284,7 +284,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
           acc[mt][nt][r] = v;
           m = fmaxf(m, v);
         }
-      rmax[nt] = fmaxf(m, shfl_xor(m, 32));
+      rmax[nt] = fmaxf(m, swap_partner<32>(m, hl != 0));
     }
     if (hl == 0)
 #pragma unroll
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
           acc[mt][nt][r] = e;
           s += e;
         }
-      rsum[nt] = s + shfl_xor(s, 32);
+      rsum[nt] = s + swap_partner<32>(s, hl != 0);
     }
     if (hl == 0)
 #pragma unroll
@@ -363,7 +363,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
           for (int e = 0; e < 4; ++e) s += (float)pv[mt][nt][q4][e] * acc[mt][nt][q4 * 4 + e];
         }
-      gpart[nt] = s + shfl_xor(s, 32);
+      gpart[nt] = s + swap_partner<32>(s, hl != 0);
     }
     if (hl == 0)
 #pragma unroll
