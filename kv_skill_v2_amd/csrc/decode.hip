@@ -35,8 +35,9 @@
 // Waves per workgroup and slots per wave step (for d <= 2048 / above).  Chosen by measurement:
 // large two-pass launches take NW_STREAM waves (the kernel holds 179 VGPRs, two waves per SIMD,
 // so two 4-wave workgroups share a CU and one's prologue / tail overlaps the other's streaming:
-// B = 64 batched decode 0.197 -> 0.188 ms per step); small launches (the in-kernel merge) and
-// page-grouped runs keep NW_WIDE (one row x 4 pages: 36.5 against 38.4 us).
+// B = 64 batched decode 0.197 -> 0.188 ms per step; 64 rows over 8 shared libraries, page-grouped:
+// 0.258 -> 0.252 ms per step); small launches (the in-kernel merge) keep NW_WIDE (one row x 4
+// pages: 36.5 against 38.4 us).
 #ifndef XENC_DECODE_NW_STREAM
 #define XENC_DECODE_NW_STREAM 4
 #endif
@@ -671,7 +672,7 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
   // Page-grouped runs when rows share libraries and there are enough entries to matter.
   const long long entries = (long long)M * kk;
   const int grouped = (!rf.dots && M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
-  const int nw = (fused || grouped) ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
+  const int nw = fused ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
   // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
   const size_t lds = std::max((size_t)std::max(nw / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
   if (lds > 64 * 1024) return XENC_EINVAL;

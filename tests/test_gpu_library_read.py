@@ -132,8 +132,10 @@ def test_nsplit_invariance_and_page_relabel(dev):
 @pytest.mark.parametrize("M,top_k,nsplit", [(40, 6, 2), (100, 8, 1), (24, 8, 3)])
 def test_page_grouped_runs(dev, M, top_k, nsplit):
     """Rows sharing libraries with >= 128 (row, chunk) entries run page-grouped (entries ranked
-    by page, XCD-major).  The result must match the oracle and be bit-identical to the same rows
-    read one call per row (never grouped) and to a relabelled page pool (a different order)."""
+    by page, XCD-major).  The result must match the oracle and the same rows read one call per row
+    (never grouped; the in-kernel merge splits the slots over 8 waves instead of 4, so the sums
+    round differently: within PRECISE), and be bit-identical under a relabelled page pool (a
+    different order, the same kernels)."""
     say("page-grouped", dict(M=M, top_k=top_k, nsplit=nsplit))
     d = 512
     P = synth.pool([24, 16], 128, d, device="cpu", tail_lo=1)
@@ -145,7 +147,7 @@ def test_page_grouped_runs(dev, M, top_k, nsplit):
     r = ops.library_read_decode(q.to(dev), lib, idx, wsel, qg, nsplit=nsplit)
     single = torch.stack([ops.library_read_decode(q[m:m + 1].to(dev), lib, idx[m:m + 1], wsel[m:m + 1],
                                                   qg[m:m + 1], nsplit=nsplit)[0] for m in range(M)])
-    assert torch.equal(r, single)
+    assert (r - single).abs().max().item() <= PRECISE
     perm = torch.randperm(P.pages.shape[0], generator=torch.Generator().manual_seed(2))
     inv = torch.empty_like(perm)
     inv[perm] = torch.arange(perm.numel())
@@ -168,8 +170,9 @@ def test_page_grouped_shared_pages_and_unrouted(dev, softmax):
     """Page-grouped runs (one split per page, merge in the second kernel): every row routes its
     library's shared chunk (48 readers of one page), every 7th row routes 5 of its 8 slots
     (unrouted entries), and chunk 3 of library 1 sits on the page of chunk 5 of library 0 with 9
-    fewer valid slots (one page read with two lengths).  Bit-identical to one call per row (never
-    grouped) and within the bar of the oracle."""
+    fewer valid slots (one page read with two lengths).  Equal to one call per row (never grouped;
+    within PRECISE: the in-kernel merge splits the slots over more waves) and within the bar of the
+    oracle."""
     say("page-grouped shared pages", dict(softmax=softmax))
     d, N, M, kk = 512, 128, 96, 8
     P = synth.pool([24, 16], N, d, device="cpu", tail_lo=1)
@@ -194,7 +197,7 @@ def test_page_grouped_shared_pages_and_unrouted(dev, softmax):
     single = torch.stack([ops.library_read_decode(q[m:m + 1].to(dev), lib, idx[m:m + 1].to(dev),
                                                   wsel[m:m + 1].to(dev), qg[m:m + 1], softmax=softmax,
                                                   nsplit=1)[0] for m in range(M)])
-    assert torch.equal(r, single)
+    assert (r - single).abs().max().item() <= PRECISE
     pages = P.pages.double()
     for m, g in enumerate(groups):
         a, b = int(P.chunk_ptr[g]), int(P.chunk_ptr[g + 1])
