@@ -310,6 +310,29 @@ int xenc_multi_depth_prepare(const float* z, long long ldz, int B, int n, int k,
                              void* stream);
 
 /*
+ * xenc_multi_depth_prepare_route: xenc_multi_depth_prepare followed by the routing of the B*k rows
+ *   (xenc_route_topk with q = q_rows, q_group = idx, the depth of each row as its library), with
+ *   the routing dots computed in the same launch as the per-token work, so the step needs one
+ *   launch fewer.  n <= 64 depths and ld_sel == k (idx is then the [B*k] library of each row);
+ *   d % 8 == 0, d <= 4096, q_all and S 16-byte aligned with strides that keep every row aligned.
+ *   The routing outputs are w_dense [B*k, ldwd] (the dots are formed there, then replaced by the
+ *   dense weights), ridx / rw_sel [B*k, kk].  Every output equals xenc_multi_depth_prepare then
+ *   xenc_route_topk bit for bit (B*k below 256 rows, where xenc_route_topk takes the same dots
+ *   and selection kernels).  Composes xenc/selector.py:59-67 and LibraryInjector.route
+ *   (xenc/injector.py:220-229) at each kept layer.
+ */
+int xenc_multi_depth_prepare_route(const float* z, long long ldz, int B, int n, int k,
+                                   const float* q_all, long long q_depth_stride,
+                                   long long q_token_stride, int d, const float* hn, long long ldh,
+                                   int d_r, const float* gate_w, const float* gate_b,
+                                   const float* log_gain, float gain_scale, float* w, long long ldw,
+                                   int* idx, float* w_sel, long long ld_sel, float* q_rows,
+                                   long long ldr, float* scale, const float* S,
+                                   const int* chunk_ptr, int G, int top_k, float route_temp,
+                                   float* w_dense, long long ldwd, int* ridx, float* rw_sel, int kk,
+                                   void* stream);
+
+/*
  * ---- Slot top-k selection read (D8)
  * xenc_select_scores: scores[b, i] = pool over query heads h of <q[b, h], keys[i, h / G]>
  *   (G = n_q / n_kv; pool_mean = 0: max, 1: mean), -inf where valid[i] == 0 (valid may be NULL).

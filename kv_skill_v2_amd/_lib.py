@@ -113,6 +113,16 @@ SIGNATURES = {
         c_void_p, c_void_p, c_void_p, c_float,       # gate_w, gate_b, log_gain, gain_scale
         c_void_p, c_longlong, c_void_p, c_void_p, c_longlong,  # w, ldw, idx, w_sel, ld_sel
         c_void_p, c_longlong, c_void_p, c_void_p]),  # q_rows, ldr, scale, stream
+    "xenc_multi_depth_prepare_route": (c_int, [
+        c_void_p, c_longlong, c_int, c_int, c_int,   # z, ldz, B, n, k
+        c_void_p, c_longlong, c_longlong, c_int,     # q_all, q_depth_stride, q_token_stride, d
+        c_void_p, c_longlong, c_int,                 # hn, ldh, d_r
+        c_void_p, c_void_p, c_void_p, c_float,       # gate_w, gate_b, log_gain, gain_scale
+        c_void_p, c_longlong, c_void_p, c_void_p, c_longlong,  # w, ldw, idx, w_sel, ld_sel
+        c_void_p, c_longlong, c_void_p,              # q_rows, ldr, scale
+        c_void_p, c_void_p, c_int, c_int, c_float,   # S, chunk_ptr, G, top_k, route_temp
+        c_void_p, c_longlong, c_void_p, c_void_p, c_int,  # w_dense, ldwd, ridx, rw_sel, kk
+        c_void_p]),                                  # stream
     "xenc_select_scores": (c_int, [
         c_void_p, c_int, c_int, c_int, c_int,        # q, B, n_q, n_kv, hd
         c_void_p, c_int, c_void_p, c_int,            # keys, S, valid, pool_mean

@@ -402,29 +402,19 @@ __global__ __launch_bounds__(8 * kWave) void route_dots_kernel(
   const int c0 = chunk_ptr[g];
   const int C = min(chunk_ptr[g + 1] - c0, ldw);
   if (c >= C) return;
-  const float* qrow = q + (long long)m * ldq;
-  const float* srow = S + (long long)(c0 + c) * d;
-  typedef float f32x4 __attribute__((ext_vector_type(4)));
-  float4 qv[CB4];
-  f32x4 sv[CB4];
-#pragma unroll
-  for (int cb = 0; cb < CB4; ++cb) {
-    const int i = (cb * kWave + lane) * 4;
-    qv[cb] = i < d ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-    // Default cache policy: the nontemporal hint measured slower here (5.97 against 5.27 us on
-    // 64 rows x 2177 chunks, 9.62 against 7.03 us on 64 rows over 8 libraries of 64 chunks).
-    sv[cb] = *reinterpret_cast<const f32x4*>(srow + min(i, d - 4));
-  }
-  float a = 0.f;
-#pragma unroll
-  for (int cb = 0; cb < CB4; ++cb) {
-    a = fmaf(qv[cb].x, sv[cb].x, a);
-    a = fmaf(qv[cb].y, sv[cb].y, a);
-    a = fmaf(qv[cb].z, sv[cb].z, a);
-    a = fmaf(qv[cb].w, sv[cb].w, a);
-  }
-  a = wave_sum(a);
+  const float a = route_dot_wave<CB4>(q + (long long)m * ldq, S + (long long)(c0 + c) * d, d, lane);
   if (lane == 0) w_dense[(long long)m * ldw + c] = a;
+}
+
+int launch_route_select(int M, const int* chunk_ptr, const int* q_group, int G, int top_k,
+                        float route_temp, float* w_dense, int ldw, int* idx, float* w_sel, int kk,
+                        hipStream_t st) {
+  const size_t sel_lds = (size_t)kSelectWaves * 3 * select_lds_stride(ldw) * sizeof(float);
+  if (sel_lds > 64 * 1024) return XENC_EINVAL;
+  hipLaunchKernelGGL(route_rows_select_kernel, dim3((M + kSelectWaves - 1) / kSelectWaves),
+                     dim3(kSelectWaves * kWave), sel_lds, st, M, chunk_ptr, nullptr, q_group, G, top_k,
+                     route_temp, w_dense, ldw, idx, w_sel, kk);
+  return check_launch();
 }
 
 int launch_route_dots(const float* q, long long ldq, int M, int d, const float* S, const int* chunk_ptr,

@@ -17,6 +17,9 @@
 //                            in one launch: per token the selector top-k, the kept depths' query
 //                            rows gathered and their row scales
 // Every sum runs in a fixed order (deterministic).
+#include <climits>
+
+#include "route_select.h"
 #include "xenc_common.h"
 
 namespace xenc {
@@ -289,16 +292,35 @@ __global__ __launch_bounds__(kRowThreads) void gate_scale_kernel(
 // top-k of z[b] (select_weights_row, wave 0), then the query row of each kept depth copied from
 // q_all into q_rows[b*k + j], and the row scale of each kept depth from the token's gate dot
 // (row_dot, the gate_scale_kernel sum).  Each output is bit-identical to the separate kernel's.
-__global__ __launch_bounds__(kRowThreads) void multi_depth_prepare_kernel(
-    const float* __restrict__ z, long long ldz, int n, int k, const float* __restrict__ q_all,
-    long long q_depth_stride, long long q_token_stride, int d, const float* __restrict__ hn,
-    long long ldh, int d_r, const float* __restrict__ gate_w, const float* __restrict__ gate_b,
-    const float* __restrict__ log_gain, float gain_scale, float* __restrict__ w, long long ldw,
-    int* __restrict__ idx, float* __restrict__ w_sel, long long lds, float* __restrict__ q_rows,
-    long long ldr, float* __restrict__ scale, int vec4_q, int vec4_h) {
-  __shared__ float red[kRowThreads / kWave];
-  __shared__ int kept[64];
-  const int b = blockIdx.x;
+struct PrepareArgs {
+  const float* z; long long ldz; int n, k;
+  const float* q_all; long long q_depth_stride, q_token_stride; int d;
+  const float* hn; long long ldh; int d_r;
+  const float *gate_w, *gate_b, *log_gain; float gain_scale;
+  float* w; long long ldw; int* idx; float* w_sel; long long lds;
+  float* q_rows; long long ldr; float* scale; int vec4_q, vec4_h;
+};
+
+// Token b's work by the first kRowThreads threads of a workgroup (red: kRowThreads / kWave
+// floats, kept: 64 ints of LDS).
+__device__ __forceinline__ void prepare_token(int b, const PrepareArgs& a, float* red, int* kept) {
+  const float* __restrict__ z = a.z;
+  const long long ldz = a.ldz;
+  const int n = a.n, k = a.k, d = a.d, d_r = a.d_r, vec4_q = a.vec4_q, vec4_h = a.vec4_h;
+  const float* __restrict__ q_all = a.q_all;
+  const long long q_depth_stride = a.q_depth_stride, q_token_stride = a.q_token_stride;
+  const float* __restrict__ hn = a.hn;
+  const long long ldh = a.ldh;
+  const float* __restrict__ gate_w = a.gate_w;
+  const float* __restrict__ gate_b = a.gate_b;
+  const float* __restrict__ log_gain = a.log_gain;
+  const float gain_scale = a.gain_scale;
+  float* __restrict__ w = a.w;
+  const long long ldw = a.ldw, lds = a.lds, ldr = a.ldr;
+  int* __restrict__ idx = a.idx;
+  float* __restrict__ w_sel = a.w_sel;
+  float* __restrict__ q_rows = a.q_rows;
+  float* __restrict__ scale = a.scale;
   const int lane = threadIdx.x & (kWave - 1);
   const float* hrow = hn + (long long)b * ldh;
   // 16-byte rows of d_r <= 4 * kRowThreads * kApplyPer: this thread's pieces of the gate dot load
@@ -375,6 +397,54 @@ __global__ __launch_bounds__(kRowThreads) void multi_depth_prepare_kernel(
   }
 }
 
+__global__ __launch_bounds__(kRowThreads) void multi_depth_prepare_kernel(PrepareArgs a) {
+  __shared__ float red[kRowThreads / kWave];
+  __shared__ int kept[64];
+  prepare_token(blockIdx.x, a, red, kept);
+}
+
+// The per-token work above and the routing dots of the step's rows in one launch.  Workgroup
+// (b, 0) runs prepare_token(b); workgroup (b, 1 + j * ncb + cb) takes chunks 4cb .. 4cb + 3 of
+// row b*k + j, one wave per chunk, with route_dot_wave (the dots of route_dots_kernel, bit for
+// bit).  Its depth, the candidate of rank j in z[b], is ranked here from the same 64-bit keys
+// as select_weights_row (n <= 64), so the dots do not wait for the selection's launch; the query
+// row is read from q_all, of which q_rows[b*k + j] is a copy.
+template <int CB4>
+__global__ __launch_bounds__(kRowThreads) void multi_depth_prepare_dots_kernel(
+    PrepareArgs a, int ncb, const float* __restrict__ S, const int* __restrict__ chunk_ptr, int G,
+    float* __restrict__ dots, int ldd) {
+  __shared__ float red[kRowThreads / kWave];
+  __shared__ int kept[64];
+  const int b = blockIdx.x;
+  if (blockIdx.y == 0) {
+    prepare_token(b, a, red, kept);
+    return;
+  }
+  const int lane = threadIdx.x & (kWave - 1);
+  const int j = (blockIdx.y - 1) / ncb;
+  const int c = ((blockIdx.y - 1) % ncb) * (kRowThreads / kWave) + (int)(threadIdx.x / kWave);
+  const float v = lane < a.n ? a.z[(long long)b * a.ldz + lane] : -INFINITY;
+  const unsigned long long key =
+      lane < a.n ? ((unsigned long long)order_key(v) << 32) | (unsigned)~lane : 0ull;
+  const unsigned klo = (unsigned)key, khi = (unsigned)(key >> 32);
+  int rank = 0;
+  for (int i = 0; i < a.n; ++i) {
+    const unsigned long long ki =
+        ((unsigned long long)(unsigned)__builtin_amdgcn_readlane((int)khi, i) << 32) |
+        (unsigned)__builtin_amdgcn_readlane((int)klo, i);
+    rank += ki > key ? 1 : 0;
+  }
+  const unsigned long long hit = __ballot(lane < a.n && rank == j);   // one lane: j < k <= n
+  const int depth = min(__builtin_amdgcn_readfirstlane((int)__builtin_ctzll(hit | (1ull << 63))), a.n - 1);
+  const int g = min(max(depth, 0), G - 1);
+  const int c0 = chunk_ptr[g];
+  const int C = min(chunk_ptr[g + 1] - c0, ldd);
+  if (c >= C) return;
+  const float* qrow = a.q_all + (long long)depth * a.q_depth_stride + (long long)b * a.q_token_stride;
+  const float x = route_dot_wave<CB4>(qrow, S + (long long)(c0 + c) * a.d, a.d, lane);
+  if (lane == 0) dots[((long long)b * a.k + j) * ldd + c] = x;
+}
+
 }  // namespace
 }  // namespace xenc
 
@@ -446,9 +516,52 @@ extern "C" int xenc_multi_depth_prepare(const float* z, long long ldz, int B, in
   const int vec4_q = (d % 4 == 0 && q_depth_stride % 4 == 0 && q_token_stride % 4 == 0 && ldr % 4 == 0 &&
                       aligned16(q_all) && aligned16(q_rows)) ? 1 : 0;
   const int vec4_h = (d_r % 4 == 0 && ldh % 4 == 0 && aligned16(hn) && aligned16(gate_w)) ? 1 : 0;
+  const PrepareArgs a{z, ldz, n, k, q_all, q_depth_stride, q_token_stride, d, hn, ldh, d_r, gate_w, gate_b,
+                      log_gain, gain_scale, w, ldw, idx, w_sel, ld_sel, q_rows, ldr, scale, vec4_q, vec4_h};
   hipLaunchKernelGGL(multi_depth_prepare_kernel, dim3(B), dim3(kRowThreads), 0,
-                     reinterpret_cast<hipStream_t>(stream), z, ldz, n, k, q_all, q_depth_stride,
-                     q_token_stride, d, hn, ldh, d_r, gate_w, gate_b, log_gain, gain_scale, w, ldw, idx,
-                     w_sel, ld_sel, q_rows, ldr, scale, vec4_q, vec4_h);
+                     reinterpret_cast<hipStream_t>(stream), a);
   return check_launch();
+}
+
+extern "C" int xenc_multi_depth_prepare_route(
+    const float* z, long long ldz, int B, int n, int k, const float* q_all, long long q_depth_stride,
+    long long q_token_stride, int d, const float* hn, long long ldh, int d_r, const float* gate_w,
+    const float* gate_b, const float* log_gain, float gain_scale, float* w, long long ldw, int* idx,
+    float* w_sel, long long ld_sel, float* q_rows, long long ldr, float* scale, const float* S,
+    const int* chunk_ptr, int G, int top_k, float route_temp, float* w_dense, long long ldwd,
+    int* ridx, float* rw_sel, int kk, void* stream) {
+  if (B < 0 || n <= 0 || n > kWave || k <= 0 || k > n || ldz < n || ldw < n || ld_sel < k || d <= 0 ||
+      d_r <= 0 || ldh < d_r || ldr < d || G <= 0 || kk <= 0 || ldwd <= 0)
+    return XENC_EINVAL;
+  if (q_depth_stride < 0 || q_token_stride < 0) return XENC_EINVAL;
+  if (d % 8 != 0 || d > 4096 || q_depth_stride % 4 != 0 || q_token_stride % 4 != 0) return XENC_EINVAL;
+  if (ld_sel != k || (long long)B * k > INT_MAX / 2) return XENC_EINVAL;   // idx doubles as [B*k] libraries
+  if (B == 0) return XENC_OK;
+  if (!z || !q_all || !hn || !gate_w || !gate_b || !log_gain || !w || !idx || !w_sel || !q_rows || !scale ||
+      !S || !chunk_ptr || !w_dense || !ridx || !rw_sel)
+    return XENC_ENULL;
+  if (!aligned16(q_all) || !aligned16(S)) return XENC_EALIGN;
+  const int vec4_q = (ldr % 4 == 0 && aligned16(q_rows)) ? 1 : 0;
+  const int vec4_h = (d_r % 4 == 0 && ldh % 4 == 0 && aligned16(hn) && aligned16(gate_w)) ? 1 : 0;
+  const PrepareArgs a{z, ldz, n, k, q_all, q_depth_stride, q_token_stride, d, hn, ldh, d_r, gate_w, gate_b,
+                      log_gain, gain_scale, w, ldw, idx, w_sel, ld_sel, q_rows, ldr, scale, vec4_q, vec4_h};
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  constexpr int kChunksPerBlock = kRowThreads / kWave;
+  const int ncb = (int)((ldwd + kChunksPerBlock - 1) / kChunksPerBlock);
+  const dim3 grid(B, 1 + k * ncb);
+  switch ((d + 255) / 256) {
+#define XENC_PD(N)                                                                               \
+  case N:                                                                                        \
+    hipLaunchKernelGGL(multi_depth_prepare_dots_kernel<N>, grid, dim3(kRowThreads), 0, st, a, ncb, \
+                       S, chunk_ptr, G, w_dense, (int)ldwd);                                     \
+    break;
+    XENC_PD(1) XENC_PD(2) XENC_PD(3) XENC_PD(4) XENC_PD(5) XENC_PD(6) XENC_PD(7) XENC_PD(8)
+    XENC_PD(9) XENC_PD(10) XENC_PD(11) XENC_PD(12) XENC_PD(13) XENC_PD(14) XENC_PD(15) XENC_PD(16)
+#undef XENC_PD
+    default:
+      return XENC_EINVAL;
+  }
+  // The rows' libraries are their depths, written by the workgroups (b, 0) above.
+  return launch_route_select(B * k, chunk_ptr, idx, G, top_k, route_temp, w_dense, (int)ldwd, ridx, rw_sel,
+                             kk, st);
 }

@@ -5,13 +5,14 @@ every candidate layer and multiplies the update of every unselected layer by zer
 selector's top-k runs first, and only the (token, selected depth) rows are routed, read and
 written back:
 
-    1. per token, in one launch (xenc_multi_depth_prepare): the selector's top-k of the logits
-       z [B, L] with a softmax over the kept ones (ties go to the lower depth), the query row of
-       each kept depth gathered from q_all [L, B, d], and gate * gain of each (token, depth) row;
-    2. routing over the chunks of that row's depth library and the paged split-K read of the
-       routed pages in one call (xenc_route_read_decode: the q . S dots, the top-k of every row,
-       the ranking of the routed (row, page) entries by page, the read with the rows that routed
-       the same page side by side, the merge of the partials);
+    1. per token, in one launch (xenc_multi_depth_prepare_route): the selector's top-k of the
+       logits z [B, L] with a softmax over the kept ones (ties go to the lower depth), the query
+       row of each kept depth gathered from q_all [L, B, d], gate * gain of each (token, depth)
+       row, and beside them, in the same launch, the q . S dots of every row over the chunks of
+       its depth library; then the top-k of every row;
+    2. the paged split-K read of the routed pages (xenc_library_read_decode: the ranking of the
+       routed (row, page) entries by page, the read with the rows that routed the same page side
+       by side, the merge of the partials);
     3. the depth's B streamed once with the row scale folded in (xenc_write_back);
     4. the matched-norm rescale times the selector weight, summed over a token's kept depths
        (xenc_selector_apply).
@@ -68,12 +69,20 @@ class MultiDepthDecode:
         routed chunks, depth [B*k_sel] int32): row b*k_sel + j is token b's j-th kept depth."""
         k = self.k_sel
         with torch.no_grad():
-            _, top, wtop, qr, scale = ops.multi_depth_prepare(z, k, q_all, hn, self.gate_w, self.gate_b,
-                                                              self.log_gain, self.gain_scale)
-            depth = top.reshape(-1)
-            _, idx, wsel, r = ops.route_read_decode(qr, self.lib, depth, top_k=self.top_k,
-                                                    route_temp=self.route_temp, read_temp=self.read_temp,
-                                                    nsplit=self.nsplit)
+            if self.lib.n_libraries <= 64:
+                _, top, wtop, qr, scale, _, idx, wsel = ops.multi_depth_prepare_route(
+                    z, k, q_all, hn, self.gate_w, self.gate_b, self.log_gain, self.lib, top_k=self.top_k,
+                    route_temp=self.route_temp, gain_scale=self.gain_scale)
+                depth = top.reshape(-1)
+                r = ops.library_read_decode(qr, self.lib, idx, wsel, q_group=depth, read_temp=self.read_temp,
+                                            nsplit=self.nsplit)
+            else:
+                _, top, wtop, qr, scale = ops.multi_depth_prepare(z, k, q_all, hn, self.gate_w, self.gate_b,
+                                                                  self.log_gain, self.gain_scale)
+                depth = top.reshape(-1)
+                _, idx, wsel, r = ops.route_read_decode(qr, self.lib, depth, top_k=self.top_k,
+                                                        route_temp=self.route_temp, read_temp=self.read_temp,
+                                                        nsplit=self.nsplit)
             upd = ops.write_back(r, self.B_w, depth, None, scale)
             out = ops.selector_apply(upd, h, wtop.reshape(-1), self.log_alpha, k=k)
         return out, idx, depth

@@ -572,6 +572,54 @@ def multi_depth_prepare(z: torch.Tensor, k: int, q_all: torch.Tensor, hn: torch.
     return w, top, wtop, q_rows, scale
 
 
+def multi_depth_prepare_route(z: torch.Tensor, k: int, q_all: torch.Tensor, hn: torch.Tensor,
+                              gate_w: torch.Tensor, gate_b: torch.Tensor, log_gain: torch.Tensor,
+                              lib_: PagedLibrary, top_k: int = 0, route_temp: float = 10.0,
+                              gain_scale: float = 1.0):
+    """multi_depth_prepare, then route_topk of its q_rows with each row's depth as its library,
+    with the routing dots in the same launch as the per-token work (xenc_multi_depth_prepare_route;
+    at most 64 depths).  Returns (w, top, wtop, q_rows, scale, w_route [B*k, cmax], idx [B*k, kk],
+    w_sel [B*k, kk]), equal bit for bit to the two calls (LayerSelector._weights_from_logits and
+    LibraryInjector.route at each kept layer: xenc/selector.py:59-67, xenc/injector.py:220-229)."""
+    for t, n in ((z, "z"), (q_all, "q_all"), (hn, "hn"), (gate_w, "gate_w"), (gate_b, "gate_b"),
+                 (log_gain, "log_gain")):
+        _require_device(t, n)
+    if z.dtype != torch.float32 or z.dim() != 2 or z.stride(1) != 1:
+        raise ValueError("z must be fp32 [B, L] with unit column stride")
+    B, L = z.shape
+    if L != lib_.n_libraries:
+        raise ValueError(f"the pool must hold one library per depth ({L}), it holds {lib_.n_libraries}")
+    if L > 64:
+        raise ValueError("at most 64 depths")
+    if q_all.dtype != torch.float32 or q_all.dim() != 3 or q_all.shape[:2] != (L, B) or q_all.shape[2] != lib_.d:
+        raise ValueError(f"q_all must be fp32 [{L}, {B}, {lib_.d}]")
+    if q_all.stride(2) != 1 or q_all.stride(0) % 4 or q_all.stride(1) % 4 or q_all.data_ptr() % 16:
+        q_all = q_all.contiguous()
+    if hn.dtype != torch.float32 or hn.dim() != 2 or hn.shape[0] != B or hn.stride(1) != 1:
+        raise ValueError(f"hn must be fp32 [{B}, d_r] with unit column stride")
+    d, d_r = lib_.d, hn.shape[1]
+    gw, gb, lg = (t.detach().float().reshape(-1).contiguous() for t in (gate_w, gate_b, log_gain))
+    if gw.numel() != d_r or gb.numel() != L or lg.numel() != L:
+        raise ValueError(f"gate_w must have {d_r} entries and gate_b / log_gain one per depth ({L})")
+    dev = z.device
+    kk = lib_.kept(int(top_k))
+    w = torch.empty(B, L, dtype=torch.float32, device=dev)
+    top = torch.empty(B, k, dtype=torch.int32, device=dev)
+    wtop = torch.empty(B, k, dtype=torch.float32, device=dev)
+    q_rows = torch.empty(B * k, d, dtype=torch.float32, device=dev)
+    scale = torch.empty(B * k, dtype=torch.float32, device=dev)
+    w_route = torch.empty(B * k, lib_.cmax, dtype=torch.float32, device=dev)
+    idx = torch.empty(B * k, kk, dtype=torch.int32, device=dev)
+    w_sel = torch.empty(B * k, kk, dtype=torch.float32, device=dev)
+    check(lib().xenc_multi_depth_prepare_route(
+        ptr(z), z.stride(0), B, L, int(k), ptr(q_all), q_all.stride(0), q_all.stride(1), d, ptr(hn),
+        hn.stride(0), d_r, ptr(gw), ptr(gb), ptr(lg), float(gain_scale), ptr(w), w.stride(0), ptr(top),
+        ptr(wtop), k, ptr(q_rows), q_rows.stride(0), ptr(scale), ptr(lib_.S), ptr(lib_.chunk_ptr), L,
+        int(top_k), float(route_temp), ptr(w_route), w_route.stride(0), ptr(idx), ptr(w_sel), kk,
+        stream_handle(dev)), "xenc_multi_depth_prepare_route")
+    return w, top, wtop, q_rows, scale, w_route, idx, w_sel
+
+
 def select_scores(q: torch.Tensor, keys: torch.Tensor, valid: torch.Tensor | None = None,
                   pool: str = "max") -> torch.Tensor:
     """Pooled selection scores [B, S] on xenc_select_scores: q fp32 [B, n_q, hd] (one position),

@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle as O
-from kv_skill_v2_amd import ops
+from kv_skill_v2_amd import ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -140,6 +140,40 @@ def test_multi_depth_prepare_equals_separate_calls(dev, B, L, k, d, d_r, ties, v
     assert torch.equal(scale, scale2)
     with pytest.raises(ValueError):
         ops.multi_depth_prepare(z, k, q_all, hn, gate_w, gate_b[:-1], log_gain, 0.7)
+
+
+@pytest.mark.parametrize("B,chunks,k,top_k,d,ties", [(32, [64] * 8, 2, 8, 2560, False),
+                                                     (7, [5, 33, 64, 1, 12], 3, 4, 264, True),
+                                                     (3, [9, 17, 2, 40], 1, 0, 64, False),
+                                                     (12, [64, 30, 7], 2, 64, 520, True)])
+def test_multi_depth_prepare_route_equals_separate_calls(dev, B, chunks, k, top_k, d, ties):
+    """xenc_multi_depth_prepare_route: every output equals xenc_multi_depth_prepare followed by
+    xenc_route_topk of its q_rows (the depth of each row as its library) bit for bit: the dots
+    of the fused launch take each row's depth from their own rank count of the logits, so tied
+    logits, unequal libraries, dense routing (top_k 0 or >= the chunks) and d not a multiple of
+    256 are the cases where that could part from the selection kernel."""
+    L = len(chunks)
+    say("multi-depth prepare + route", dict(B=B, chunks=chunks, k=k, top_k=top_k, d=d, ties=ties))
+    P = synth.pool(chunks, 64, d, device=dev)
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    g = torch.Generator().manual_seed(B * L + d + k)
+    z = (torch.randint(-1, 2, (B, L), generator=g).float() if ties else torch.randn(B, L, generator=g)).to(dev)
+    q_all = torch.randn(L, B, d, generator=g).to(dev)
+    d_r = 48
+    hn = torch.randn(B, d_r, generator=g).to(dev)
+    gate_w = (torch.randn(d_r, generator=g) / d_r ** 0.5).to(dev)
+    gate_b = torch.randn(L, generator=g).to(dev)
+    log_gain = (0.1 * torch.randn(L, generator=g)).to(dev)
+    got = ops.multi_depth_prepare_route(z, k, q_all, hn, gate_w, gate_b, log_gain, lib, top_k=top_k,
+                                        route_temp=10.0, gain_scale=0.7)
+    w, top, wtop, q_rows, scale = ops.multi_depth_prepare(z, k, q_all, hn, gate_w, gate_b, log_gain, 0.7)
+    wr, idx, wsel = ops.route_topk(q_rows, lib, top.reshape(-1), top_k=top_k, route_temp=10.0)
+    for a, b, name in zip(got, (w, top, wtop, q_rows, scale, wr, idx, wsel),
+                          ("w", "top", "wtop", "q_rows", "scale", "w_route", "idx", "w_sel")):
+        assert a.shape == b.shape and torch.equal(a, b), name
+    with pytest.raises(ValueError):
+        ops.multi_depth_prepare_route(z, k, q_all[:, :, :-8], hn, gate_w, gate_b, log_gain, lib)
 
 
 def test_selector_guards(dev):
