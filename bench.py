@@ -657,7 +657,7 @@ def bench_op_b(args):
         "vs_baseline": None, "dtype": "fp32 (bf16 pools)", "data": "synthetic",
         "config": {"workload": "op_b", "rows": B, "operator_rows": op_len, "own_rows": own_len, "hq": hq,
                    "hkv": hkv, "head_dim": d, "block_size": bs, "key_splits": dec.S, "chunk": chunk},
-        "roofline": {"bound": "hbm", "kernel": "joint_read_kernel", "achieved": achieved,
+        "roofline": {"bound": "hbm", "kernel": "joint_read_mfma_kernel + joint_merge_kernel", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "algorithmic_bytes": alg_bytes, "avg_launch_ms": k_ms},
         "cpu_baseline": cpu,
