@@ -4,7 +4,9 @@ Multi-depth selector decode (8 depth Libraries of 64 x 512 slots, d_s 2560, 32 t
 top-2, routing top-8, write-back to d_r 5120): the step `bench.py --workload multi_depth` times
 (kv_skill_v2_amd.multi_depth.MultiDepthDecode) against the fp64 oracle computed the reference's
 way: the branch at EVERY candidate depth, each over all 64 chunks (xenc/injector.py:231-273),
-then the selector weighting of every depth's update (xenc/selector.py:95-110), summed per token.
+then the selector weighting of every depth's update (xenc/selector.py:95-110), summed per token;
+the same step at reduced sizes with one to three kept depths, unequal depth libraries and dense
+routing.
 
 Prefill (4 documents x 2048 rows x 32 chunks of 512 slots, d_s 2048, dense routing): the
 forward r and the dQ backward of the composition `bench.py --workload prefill` times, over the
@@ -86,6 +88,52 @@ def test_multi_depth_step_full_shape(dev):
     assert err <= 2e-3 and rel <= 1e-2
     row_rel = ((out - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
     assert row_rel <= 1e-2, row_rel
+
+
+@pytest.mark.parametrize("chunks,B,ks,k", [([5, 12, 64, 3, 20], 24, 3, 4),
+                                            ([16, 9, 30, 1], 40, 1, 8),
+                                            ([64] * 6, 20, 2, 0)])
+def test_multi_depth_step_reduced_shapes(dev, chunks, B, ks, k):
+    """The multi-depth step (MultiDepthDecode) at reduced sizes against the fp64 oracle computed
+    the reference's way (every depth read over all its chunks, then the selector weighting): one,
+    two or three kept depths, depth libraries of unequal chunk counts (one of a single chunk),
+    routing top-k below, at and above a library's chunk count and dense (k = 0), runs that the
+    read groups by page and runs it does not (k_sel 1 with few rows per depth)."""
+    L, N, d, dr = len(chunks), 64, 256, 96
+    say("multi-depth step, reduced", dict(chunks=chunks, B=B, ks=ks, k=k))
+    P = synth.pool(chunks, N, d, device=dev)
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    gen = torch.Generator().manual_seed(B + L + ks)
+    z = torch.randn(B, L, generator=gen)
+    q_all = torch.nn.functional.normalize(torch.randn(L, B, d, generator=gen), dim=-1)
+    h = torch.randn(B, dr, generator=gen)
+    Bw = torch.randn(L, dr, d, generator=gen) / d ** 0.5
+    gate_w = torch.randn(dr, generator=gen) * 0.05
+    gate_b = torch.linspace(-1.0, 1.0, L)
+    log_gain = torch.linspace(-0.3, 0.3, L)
+    log_alpha = math.log(0.02)
+    hn = rms_norm(h)
+    md = MultiDepthDecode(lib, Bw.to(dev), gate_w.to(dev), gate_b.to(dev), log_gain.to(dev),
+                          torch.tensor(log_alpha, device=dev), k_sel=ks, top_k=k)
+    out, idx, depth = md(z.to(dev), q_all.to(dev), h.to(dev), hn.to(dev))
+    torch.cuda.synchronize()
+    out, depth = out.double().cpu(), depth.cpu()
+    zc, hc, hnc = z.double(), h.double(), hn.double()
+    wsel = O.selector_weights(zc, ks)
+    ref = torch.zeros(B, dr, dtype=torch.float64)
+    for l in range(L):
+        K, M, S = P.library(l)
+        K, M, S = K.double().cpu(), M.cpu(), S.double().cpu()
+        r_l, _ = O.branch_read(q_all[l].double().view(B, 1, d), K, M, S, top_k=k)
+        d_l = O.epilogue(hnc.view(B, 1, dr), r_l, Bw[l].double(), None, gate_w.double(), gate_b[l].double(),
+                         log_gain[l].double())
+        ref += O.selector_apply(d_l.view(B, dr), hc, wsel[:, l], log_alpha)
+    assert torch.equal(depth.view(B, ks).long(), O.topk_order(zc, ks))
+    err = (out - ref).abs().max().item()
+    row_rel = ((out - ref).norm(dim=-1) / ref.norm(dim=-1)).max().item()
+    say("max-abs", err, "row-rel", row_rel)
+    assert err <= 2e-3 and row_rel <= 1e-2
 
 
 def test_prefill_full_shape_row_sample(dev):
