@@ -110,9 +110,10 @@ int xenc_library_read_decode(const float* q, long long ldq, int M, int d,
  * xenc_library_read_decode's r, same arguments as the two calls together, same results bit for
  * bit.  When every library has at most 64 chunks (ldw <= 64) and the rows do not share libraries
  * (the page-grouped order needs the routed chunks first), the top-k + softmax runs in the read
- * kernel's prologue instead of a kernel of its own: the q . S dots go to the workspace first, each
- * read workgroup ranks its row's dots itself, and the workgroup of the row's first routed slot
- * writes the dense weights.  Otherwise it makes the two calls.  Workspace as for
+ * kernel's prologue instead of a kernel of its own: the q . S dots go to the workspace first (for
+ * libraries of at most 16 chunks, ldw <= 16, the read workgroups form them too, with no launch of
+ * their own), each read workgroup ranks its row's dots itself, and the workgroup of the row's
+ * first routed slot writes the dense weights.  Otherwise it makes the two calls.  Workspace as for
  * xenc_library_read_decode.
  * Replaces LibraryInjector.route and the read of _branch (xenc/injector.py:220-265) for decode rows.
  */

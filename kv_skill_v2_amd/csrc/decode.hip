@@ -88,13 +88,18 @@ struct DecodeWorkspace {
 // chunks itself (select_topk_softmax_rank, the routing kernels' own selection) to find the chunk of
 // its routed slot; split 0 of each slot publishes idx / w_sel, and the workgroup of (row, slot 0,
 // split 0) writes the row's dense weights into w_dense.
+// With S set instead of dots (libraries of at most kDotsInRead chunks), each workgroup also forms
+// its row's dots itself, wave w taking chunks w, w + NW, ... with route_dot_wave (the dots of
+// route_dots_kernel, bit for bit), so the routing needs no launch of its own.
 struct RouteFuse {
   const float* dots;
   float* w_dense;
   int ldw;
   int top_k;
   float route_temp;
+  const float* S;
 };
+constexpr int kDotsInRead = 16;
 
 // LDS of the fused selection: the row's dots (reused for the exponentials), the 64-bit keys,
 // the dense weights and the kept (index, weight) list by rank.
@@ -106,10 +111,12 @@ struct SelectLds {
   float sel[kWave];
 };
 
-// Wave-level: the top-k + softmax of row m (library g) into sl (dense weights zeroed first).
-__device__ __forceinline__ void select_row(const RouteFuse& rf, int m, int C, int kk, SelectLds& sl, int lane) {
+// Wave-level: the top-k + softmax of a row from its C dots drow (global or LDS) into sl (dense
+// weights zeroed first).
+__device__ __forceinline__ void select_row(const RouteFuse& rf, const float* drow, int C, int kk, SelectLds& sl,
+                                           int lane) {
   sl.w[lane] = 0.f;
-  if (lane < C) sl.x[lane] = rf.dots[(long long)m * rf.ldw + lane];
+  if (lane < C) sl.x[lane] = drow[lane];
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -339,7 +346,7 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
   const int C_g = chunk_ptr[g + 1] - cbeg;
   int nv = 0;
   long long pbase = 0;
-  if (rf.dots) {  // uniform: routing folded into the read
+  if (rf.dots || rf.S) {  // uniform: routing folded into the read
     // Every wave ranks the row's chunks itself (its own LDS, no workgroup barrier) while the
     // valid counts and pages of all the row's chunks load, one per lane; the routed chunk's are
     // then taken from its lane.
@@ -347,7 +354,17 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
     const int C = min(C_g, rf.ldw);
     const int lnv = lane < C ? chunk_nvalid[cbeg + lane] : 0;
     const int lpg = lane < C ? chunk_page[cbeg + lane] : 0;
-    select_row(rf, m, C, kk, sl[wv], lane);
+    const float* drow = rf.dots + (long long)m * rf.ldw;
+    if (rf.S) {
+      __shared__ float row_dots[kDotsInRead];
+      for (int c = wv; c < C; c += NW) {
+        const float x = route_dot_wave<2 * CB>(q + (long long)m * ldq, rf.S + (long long)(cbeg + c) * d, d, lane);
+        if (lane == 0) row_dots[c] = x;
+      }
+      __syncthreads();
+      drow = row_dots;
+    }
+    select_row(rf, drow, C, kk, sl[wv], lane);
     const int cl = __builtin_amdgcn_readfirstlane(sl[wv].idx[j]);
     if (cl >= 0 && cl < C) {
       nv = min(__builtin_amdgcn_readlane(lnv, cl), slots_per_page);
@@ -671,7 +688,7 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
   const int fused = units < kTwoPassUnits ? 1 : 0;
   // Page-grouped runs when rows share libraries and there are enough entries to matter.
   const long long entries = (long long)M * kk;
-  const int grouped = (!rf.dots && M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
+  const int grouped = (!rf.dots && !rf.S && M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
   const int nw = fused ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
   // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
   const size_t lds = std::max((size_t)std::max(nw / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
@@ -817,10 +834,16 @@ extern "C" int xenc_route_read_decode(const float* q, long long ldq, int M, int 
   if (!workspace) return XENC_ENULL;
   if (!aligned16(workspace)) return XENC_EALIGN;
   if (workspace_bytes < workspace_need(max_rows, M, kk, (long long)M * kk * nsplit, d)) return XENC_EWORKSPACE;
+  if (ldw <= kDotsInRead) {   // the read's workgroups form the dots too
+    const RouteFuse rf{nullptr, w_dense, (int)ldw, top_k, route_temp, S};
+    return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid, chunk_ptr,
+                       q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr, workspace,
+                       workspace_bytes, max_rows, XENC_EWORKSPACE, st, rf);
+  }
   float* dots = reinterpret_cast<float*>(carve(workspace, max_rows, M, kk, nsplit).order);
   const int rc = launch_route_dots(q, ldq, M, d, S, chunk_ptr, q_group, G, dots, (int)ldw, st);
   if (rc != XENC_OK) return rc;
-  const RouteFuse rf{dots, w_dense, (int)ldw, top_k, route_temp};
+  const RouteFuse rf{dots, w_dense, (int)ldw, top_k, route_temp, nullptr};
   return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid, chunk_ptr,
                      q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr, workspace,
                      workspace_bytes, max_rows, XENC_EWORKSPACE, st, rf);
