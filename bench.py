@@ -39,6 +39,10 @@ def parse():
     ap.add_argument("--cpu-sample", type=int, default=16, help="sequences in the CPU baseline sample (0 = skip)")
     ap.add_argument("--cpu-reps", type=int, default=3)
     ap.add_argument("--no-graph", action="store_true", help="time the eager step only (no HIP graph replay)")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="batched_paged_decode: leave out the prefill block of the JSON line")
+    ap.add_argument("--prefill-steps", type=int, default=10,
+                    help="batched_paged_decode: timed steps of the prefill block (3 warm-up steps)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the timed loop, copy a buffer of this size 3 times (a plain copy "
                          "kernel of known bytes, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -209,12 +213,13 @@ def graph_of(step, same):
     return gph, out
 
 
-def bench_prefill(args):
+def measure_prefill(steps: int, warmup: int, cpu_sample: int) -> dict:
     """Prefill/registration read: 4 documents x 2048 query rows, each document a Library of 32 x 512
     slots (ragged tail), d_s = 2048, dense routing (every chunk read), fp16 MFMA with fp32
     accumulation; forward (route + read) and the dQ backward (read + route) against a seeded
     upstream gradient ~N(0,1).  Algorithmic FLOPs per document and direction: 4 * T * sum(n_valid) * d
-    (two GEMMs of 2 FLOPs per multiply-add; recomputation is not counted)."""
+    (two GEMMs of 2 FLOPs per multiply-add; recomputation is not counted).  Returns the timings,
+    TFLOP/s and fractions of the fp16 MFMA peak (vendor and measured) plus the CPU baseline."""
     from kv_skill_v2_amd import ops, synth
 
     dev = torch.device("cuda:0")
@@ -227,7 +232,6 @@ def bench_prefill(args):
     gen = torch.Generator(device=dev)
     gen.manual_seed(7)
     g_up = torch.randn(G * T, d, generator=gen, device=dev)
-    qg = ops._plan_groups(plan).to(dev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     lib.fragment_pages(0), lib.fragment_pages(1)  # one-time fragment-ordered copies of the pages
@@ -248,14 +252,14 @@ def bench_prefill(args):
         w, _, p = fwd()
         bwd(w, p)
 
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     stream = torch.cuda.current_stream(dev)
-    ms_step, _ = timed_steps(step, args.steps, stream)
+    ms_step, _ = timed_steps(step, steps, stream)
     # The split between the directions, from a second loop of K steps with events between the
     # forward and the backward (outside the timed region above: the events add idle time).
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
-    for i in range(args.steps):
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
         evs[i][0].record(stream)
         w, r, p = fwd()
         evs[i][1].record(stream)
@@ -271,7 +275,7 @@ def bench_prefill(args):
     mfma_meas = measured_mfma_peak(dev)
 
     cpu = None
-    if args.cpu_sample > 0:
+    if cpu_sample > 0:
         import oracle as O
         torch.set_num_threads(max(1, int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))))
         K, M, S = P.library(0)
@@ -287,22 +291,38 @@ def bench_prefill(args):
                "sample": (f"1 of {G} documents ({T} rows x {C} chunks), fp32 route+read forward and torch "
                           f"autograd backward in the reference's operation order, 1 rep ({cpu_s:.2f} s); "
                           f"CPU oracle on {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
+    del lib, P, q, g_up
+    torch.cuda.empty_cache()
+    return {"steps": steps, "warmup": warmup, "ms_per_step": ms_step,
+            "tflops_fwd_bwd": 2 * flops / (ms_step * 1e-3) / 1e12, "algorithmic_flops_per_direction": flops,
+            "config": {"documents": G, "rows_per_document": T, "chunks": C, "slots_per_page": N, "d_s": d,
+                       "routing": "dense (top_k=0)", "accumulate": "fp32", "fragment_pages_ms_once": frag_ms},
+            "fwd": {"ms": fwd_ms, "tflops": fwd_tf, "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS,
+                    "frac_of_measured": fwd_tf / mfma_meas if mfma_meas else None},
+            "bwd": {"ms": bwd_ms, "tflops": bwd_tf, "frac": bwd_tf / MFMA_FP16_PEAK_TFLOPS,
+                    "frac_of_measured": bwd_tf / mfma_meas if mfma_meas else None},
+            "peak_tflops": MFMA_FP16_PEAK_TFLOPS, "measured_peak_tflops": mfma_meas,
+            "cpu_baseline": cpu}
+
+
+def bench_prefill(args):
+    """The prefill/registration read (measure_prefill) as its own JSON line."""
+    pf = measure_prefill(args.steps, args.warmup, args.cpu_sample)
+    fwd_tf = pf["fwd"]["tflops"]
     out = {
         "metric": "Prefill/registration read TFLOP/s (fwd and dQ bwd), 4 docs x 2048 rows x 32x512 slots",
-        "value": 2 * flops / (ms_step * 1e-3) / 1e12, "unit": "TFLOP/s (fwd+bwd)", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True,
+        "value": pf["tflops_fwd_bwd"], "unit": "TFLOP/s (fwd+bwd)", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": pf["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
-        "config": {"workload": "prefill", "documents": G, "rows_per_document": T, "chunks": C,
-                   "slots_per_page": N, "d_s": d, "routing": "dense (top_k=0)", "accumulate": "fp32",
-                   "fragment_pages_ms_once": frag_ms},
-        "fwd": {"ms": fwd_ms, "tflops": fwd_tf, "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS},
-        "bwd": {"ms": bwd_ms, "tflops": bwd_tf, "frac": bwd_tf / MFMA_FP16_PEAK_TFLOPS},
+        "config": {"workload": "prefill", **pf["config"]},
+        "fwd": pf["fwd"], "bwd": pf["bwd"],
         "roofline": {"bound": "mfma", "kernel": "scores_kernel + readout_kernel (fwd)",
                      "achieved": fwd_tf, "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS, "traffic": None,
-                     "algorithmic_flops": flops, "measured_peak": mfma_meas,
-                     "frac_of_measured": fwd_tf / mfma_meas if mfma_meas else None},
-        "cpu_baseline": cpu,
+                     "algorithmic_flops": pf["algorithmic_flops_per_direction"],
+                     "measured_peak": pf["measured_peak_tflops"],
+                     "frac_of_measured": pf["fwd"]["frac_of_measured"]},
+        "cpu_baseline": pf["cpu_baseline"],
     }
     print(json.dumps(out), flush=True)
 
@@ -781,6 +801,11 @@ def bench_decode(args):
                      "measured_peak": stream_meas, "frac_of_measured": achieved / stream_meas},
         "cpu_baseline": cpu,
     }
+    if args.workload == "batched_paged_decode" and not args.no_prefill:
+        # The north star's second target, measured in the same run: the prefill/registration read
+        # (4 documents x 2048 rows x 32 x 512 slots, forward and dQ backward) against the fp16
+        # MFMA peak.  `metric` and `value` stay the batched decode's.
+        out["prefill"] = measure_prefill(args.prefill_steps, 3, min(args.cpu_sample, 1))
     print(json.dumps(out), flush=True)
 
 

@@ -52,9 +52,12 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const u32x4* __restric
 #pragma unroll
     for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(src + i + u * 256);
 #pragma unroll
-    for (int u = 0; u < U; ++u) acc ^= v[u][u & 3];
+    for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];   // all 16 bytes live
   }
-  for (; i < end; i += 256) acc ^= __builtin_nontemporal_load(src + i)[0];
+  for (; i < end; i += 256) {
+    const u32x4 t = __builtin_nontemporal_load(src + i);
+    acc ^= t[0] ^ t[1] ^ t[2] ^ t[3];
+  }
   out[blockIdx.x * blockDim.x + threadIdx.x] = (float)acc;
 }
 

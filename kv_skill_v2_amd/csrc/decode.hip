@@ -111,6 +111,15 @@ struct SelectLds {
   float sel[kWave];
 };
 
+// Dynamic LDS of the read kernel, in floats: the wave-merge tree [NW/2][d], reused by the
+// merge's per-partial lists [4 * kk * nsplit], rounded up to 16 bytes.  Launches with the
+// routing folded in add one SelectLds per wave after it; other launches allocate none.
+__host__ __device__ inline size_t read_red_floats(int nw, int d, int kk, int nsplit) {
+  const size_t tree = (size_t)(nw / 2 > 1 ? nw / 2 : 1) * d;
+  const size_t lists = (size_t)4 * kk * nsplit;
+  return ((tree > lists ? tree : lists) + 3) & ~size_t(3);
+}
+
 // Wave-level: the top-k + softmax of a row from its C dots drow (global or LDS) into sl (dense
 // weights zeroed first).
 __device__ __forceinline__ void select_row(const RouteFuse& rf, const float* drow, int C, int kk, SelectLds& sl,
@@ -323,10 +332,11 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
     DecodeWorkspace ws, int fused_merge, int grouped, RouteFuse rf) {
   // idx / w_sel: read (routed in advance) or written by split 0 of each slot (routing folded in),
   // so neither is declared read-only.
-  extern __shared__ float red[];  // [NW/2][d] wave-merge tree; reused by the merge
+  extern __shared__ __align__(16) float red[];  // [NW/2][d] wave-merge tree; reused by the merge
   __shared__ float wml[NW][2];
   __shared__ int is_last;
-  __shared__ SelectLds sl[NW];   // one per wave (routing folded into the read)
+  // One SelectLds per wave after the tree, allocated only when the routing is folded in.
+  SelectLds* const sl = reinterpret_cast<SelectLds*>(red + read_red_floats(NW, d, kk, nsplit));
 
   // Launch position -> logical unit: in page-grouped runs the XCD-major position indexes the
   // page-ranked entries; otherwise the unit is the block index.
@@ -661,14 +671,26 @@ extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_byte
   return check_launch();
 }
 
-// Validation and launches of the decode read over a workspace of workspace_bytes at `workspace`
-// whose counter region is sized for max_rows (shared by the two entry points below).
-static int read_decode(const float* q, long long ldq, int M, int d, const void* pages,
-                       int slots_per_page, long long page_stride, const int* chunk_page,
-                       const int* chunk_nvalid, const int* chunk_ptr, const int* q_group, int G,
-                       const int* idx, const float* w_sel, int kk, float read_temp, int softmax,
-                       int nsplit, float* r, long long ldr, void* workspace, size_t workspace_bytes,
-                       int max_rows, int short_code, hipStream_t st, const RouteFuse& rf = RouteFuse{}) {
+// Workgroup size and LDS bytes (dynamic, then the whole workgroup's) of a read launch.
+static int read_waves(long long units) {
+  return units < kTwoPassUnits ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
+}
+static size_t read_dynamic_lds(int nw, int d, int kk, int nsplit, bool fold) {
+  return read_red_floats(nw, d, kk, nsplit) * sizeof(float) + (fold ? (size_t)nw * sizeof(SelectLds) : 0);
+}
+static size_t read_total_lds(int nw, int d, int kk, int nsplit, bool fold) {
+  // static part: wml[NW][2], is_last and row_dots[kDotsInRead]
+  return read_dynamic_lds(nw, d, kk, nsplit, fold) + (size_t)nw * 2 * sizeof(float) + sizeof(int) +
+         kDotsInRead * sizeof(float);
+}
+
+// Every argument check of the decode read, done before anything is launched (the routing
+// launches of xenc_route_read_decode included), so a rejected call leaves its outputs untouched.
+static int validate_read(const float* q, long long ldq, int M, int d, const void* pages, int slots_per_page,
+                         long long page_stride, const int* chunk_page, const int* chunk_nvalid,
+                         const int* chunk_ptr, const int* q_group, int G, const int* idx, const float* w_sel,
+                         int kk, int nsplit, const float* r, long long ldr, const void* workspace,
+                         size_t workspace_bytes, int max_rows, int short_code, bool fold) {
   if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || slots_per_page <= 0) return XENC_EINVAL;
   if (M > max_rows) return short_code;
   if (d % 8 != 0 || d > 8 * 512) return XENC_EINVAL;
@@ -685,14 +707,30 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
   const long long units = (long long)M * kk * nsplit;
   if (units > 0x7fffffffLL) return XENC_EINVAL;
   if (workspace_bytes < workspace_need(max_rows, M, kk, units, d)) return short_code;
+  if (read_total_lds(read_waves(units), d, kk, nsplit, fold) > device_lds_limit()) return XENC_EINVAL;
+  return XENC_OK;
+}
+
+// Validation and launches of the decode read over a workspace of workspace_bytes at `workspace`
+// whose counter region is sized for max_rows (shared by the entry points below).
+static int read_decode(const float* q, long long ldq, int M, int d, const void* pages,
+                       int slots_per_page, long long page_stride, const int* chunk_page,
+                       const int* chunk_nvalid, const int* chunk_ptr, const int* q_group, int G,
+                       const int* idx, const float* w_sel, int kk, float read_temp, int softmax,
+                       int nsplit, float* r, long long ldr, void* workspace, size_t workspace_bytes,
+                       int max_rows, int short_code, hipStream_t st, const RouteFuse& rf = RouteFuse{}) {
+  const bool fold = rf.dots || rf.S;
+  const int vrc = validate_read(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid,
+                                chunk_ptr, q_group, G, idx, w_sel, kk, nsplit, r, ldr, workspace,
+                                workspace_bytes, max_rows, short_code, fold);
+  if (vrc != XENC_OK || M == 0) return vrc;
+  const long long units = (long long)M * kk * nsplit;
   const int fused = units < kTwoPassUnits ? 1 : 0;
   // Page-grouped runs when rows share libraries and there are enough entries to matter.
   const long long entries = (long long)M * kk;
-  const int grouped = (!rf.dots && !rf.S && M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
-  const int nw = fused ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
-  // LDS: the wave-merge tree [NW/2][d], or the merge's per-partial lists [4 * kk * nsplit].
-  const size_t lds = std::max((size_t)std::max(nw / 2, 1) * d, (size_t)4 * kk * nsplit) * sizeof(float);
-  if (lds > 64 * 1024) return XENC_EINVAL;
+  const int grouped = (!fold && M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
+  const int nw = read_waves(units);
+  const size_t lds = read_dynamic_lds(nw, d, kk, nsplit, fold);
 
   const DecodeWorkspace ws = carve(workspace, max_rows, M, kk, nsplit);
   const int split_slots = (slots_per_page + nsplit - 1) / nsplit;
@@ -813,11 +851,20 @@ extern "C" int xenc_route_read_decode(const float* q, long long ldq, int M, int 
   if (M < 0 || d <= 0 || G <= 0 || kk <= 0 || ldw <= 0) return XENC_EINVAL;
   if (M == 0) return XENC_OK;
   if (!S || !w_dense || !idx || !w_sel) return XENC_ENULL;
+  if (!aligned16(S)) return XENC_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   const long long entries = (long long)M * kk;
   // The read ranks a row's chunks itself when a library has at most 64 and the rows do not share
-  // libraries enough for the page-grouped order (which needs the routed chunks before the read).
-  const bool fold = ldw <= kWave && kk <= kWave && !(M > G && entries >= 128 && entries <= kOrderMax);
+  // libraries enough for the page-grouped order (which needs the routed chunks before the read),
+  // and when the workgroup's LDS then fits the device.
+  const bool fold = ldw <= kWave && kk <= kWave && !(M > G && entries >= 128 && entries <= kOrderMax) &&
+                    read_total_lds(read_waves(entries * std::max(nsplit, 1)), d, kk, std::max(nsplit, 1), true) <=
+                        device_lds_limit();
+  // All of the read's checks come first: nothing is launched for a call the read would reject.
+  const int vrc = validate_read(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid,
+                                chunk_ptr, q_group, G, idx, w_sel, kk, nsplit, r, ldr, workspace,
+                                workspace_bytes, max_rows, XENC_EWORKSPACE, fold);
+  if (vrc != XENC_OK) return vrc;
   if (!fold) {
     const int rc = xenc_route_topk(q, ldq, M, d, S, chunk_ptr, q_group, G, top_k, route_temp, w_dense, ldw,
                                    idx, w_sel, kk, stream);
@@ -826,14 +873,6 @@ extern "C" int xenc_route_read_decode(const float* q, long long ldq, int M, int 
                        chunk_ptr, q_group, G, idx, w_sel, kk, read_temp, softmax, nsplit, r, ldr,
                        workspace, workspace_bytes, max_rows, XENC_EWORKSPACE, st);
   }
-  if (d % 8 != 0 || d > 4096 || ldq < d || ldq % 4 != 0) return XENC_EINVAL;
-  if (!q || !chunk_ptr || !q_group) return XENC_ENULL;
-  if (!aligned16(q) || !aligned16(S)) return XENC_EALIGN;
-  if (M > max_rows) return XENC_EWORKSPACE;
-  if (nsplit < 1 || nsplit > 64) return XENC_EINVAL;
-  if (!workspace) return XENC_ENULL;
-  if (!aligned16(workspace)) return XENC_EALIGN;
-  if (workspace_bytes < workspace_need(max_rows, M, kk, (long long)M * kk * nsplit, d)) return XENC_EWORKSPACE;
   if (ldw <= kDotsInRead) {   // the read's workgroups form the dots too
     const RouteFuse rf{nullptr, w_dense, (int)ldw, top_k, route_temp, S};
     return read_decode(q, ldq, M, d, pages, slots_per_page, page_stride, chunk_page, chunk_nvalid, chunk_ptr,

@@ -24,6 +24,22 @@ inline int check_launch() {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// The most LDS (static + dynamic) one workgroup may use on the current device, queried once per
+// device (64 KiB if the query fails).
+inline size_t device_lds_limit() {
+  constexpr int kDevices = 64;
+  static int cached[kDevices];  // 0 = not yet queried
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kDevices) return 64 * 1024;
+  int v = __atomic_load_n(&cached[dev], __ATOMIC_RELAXED);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+      v = 64 * 1024;
+    __atomic_store_n(&cached[dev], v, __ATOMIC_RELAXED);
+  }
+  return (size_t)v;
+}
+
 // ---------------------------------------------------------------- wave-level primitives
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 __device__ __forceinline__ int shfl_xor(int v, int mask) { return __shfl_xor(v, mask, kWave); }
@@ -34,8 +50,22 @@ __device__ __forceinline__ float readlane(float v, int lane) {
 
 // DPP move of x with the given control (row_mask / bank_mask all, bound_ctrl on): a VALU
 // operand, no LDS-pipe permute.
+//
+// Precondition of every reduction built on it (dpp_f, swap_partner, group_sum, wave_sum,
+// wave_max, wave_reduce_scatter): ALL 64 lanes of the wave are active.  With bound_ctrl on, an
+// inactive source lane reads as 0, and the permlane swaps move whatever the inactive lanes hold,
+// so a partial wave would add zeros to a sum or raise a max of negative values to 0.  Callers
+// reach these helpers only with wave-uniform control flow (whole waves exit early or not at
+// all).  Debug builds (XENC_CHECK_FULL_WAVE) trap when the precondition is broken.
+__device__ __forceinline__ void assert_full_wave() {
+#ifdef XENC_CHECK_FULL_WAVE
+  if (__builtin_amdgcn_read_exec() != ~0ull) __builtin_trap();
+#endif
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float x) {
+  assert_full_wave();
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, true));
 }
 
@@ -46,6 +76,7 @@ __device__ __forceinline__ float dpp_f(float x) {
 template <int MASK>
 __device__ __forceinline__ float swap_partner(float x, bool hi) {
   static_assert(MASK == 32 || MASK == 16, "permlane swaps pair lanes at distance 32 or 16");
+  assert_full_wave();
   const unsigned u = __float_as_uint(x);
   if constexpr (MASK == 32) {
     const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);

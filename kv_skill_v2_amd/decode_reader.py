@@ -32,21 +32,33 @@ from ._lib import check, lib, ptr, stream_handle
 _DTYPES = {torch.float16: 0, torch.bfloat16: 1}
 
 
+class DecodeReaderError(ValueError, AssertionError):
+    """A DecodeReader argument that does not fit the reader: a bad pool, table, shape or dtype.
+    The reference checks its call preconditions with `assert` (xenc/d23_read_kernels.py:146-150),
+    so callers written against it catch AssertionError; callers of this build catch ValueError.
+    Both work."""
+
+
+class DecodeReaderDeviceError(RuntimeError, AssertionError):
+    """A DecodeReader tensor that is not on the reader's GPU (there is no CPU path).  The
+    reference asserts `q.is_cuda` (xenc/d23_read_kernels.py:146), hence AssertionError too."""
+
+
 class DecodeReader:
     def __init__(self, max_n: int, hq: int, hkv: int, d: int, max_keys: int, device, chunk: int | None = 1024,
                  block_n: int = 64):
         if hq % hkv:
-            raise ValueError(f"hq={hq} must be a multiple of hkv={hkv}")
+            raise DecodeReaderError(f"hq={hq} must be a multiple of hkv={hkv}")
         self.G, self.hq, self.hkv, self.d = hq // hkv, int(hq), int(hkv), int(d)
         if not 1 <= self.G <= 8 or d % 8 or d > 512 or self.G * d > 4096:
-            raise ValueError(f"unsupported head layout: G={self.G} (1..8), d={d} (multiple of 8, <= 512)")
+            raise DecodeReaderError(f"unsupported head layout: G={self.G} (1..8), d={d} (multiple of 8, <= 512)")
         if chunk is None:
             chunk = self.auto_chunk(max_n, hkv, max_keys)
         self.max_n, self.chunk, self.block_n = int(max_n), int(chunk), int(block_n)
         self.S = max(1, math.ceil(max_keys / self.chunk))
         device = torch.device(device)
         if device.type != "cuda":
-            raise RuntimeError("DecodeReader runs only on a ROCm GPU (there is no CPU path)")
+            raise DecodeReaderDeviceError("DecodeReader runs only on a ROCm GPU (there is no CPU path)")
         L = lib()
         nbytes = L.xenc_joint_workspace_bytes(self.max_n, self.hkv, self.S, self.G, self.d)
         self.workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
@@ -68,31 +80,31 @@ class DecodeReader:
     @staticmethod
     def _pool(k: torch.Tensor, v: torch.Tensor, name: str):
         if k.dim() != 4 or k.shape != v.shape or k.stride() != v.stride() or k.dtype != v.dtype:
-            raise ValueError(f"{name} K and V pools must be [num_blocks, block_size, hkv, d] with equal "
+            raise DecodeReaderError(f"{name} K and V pools must be [num_blocks, block_size, hkv, d] with equal "
                              "shapes, strides and dtypes")
         if k.stride(-1) != 1:
-            raise ValueError(f"{name} pools need a contiguous last dim")
+            raise DecodeReaderError(f"{name} pools need a contiguous last dim")
         return k.stride(0), k.stride(1), k.stride(2), k.shape[1]
 
     @staticmethod
     def _table(bt: torch.Tensor, ln: torch.Tensor, N: int, name: str):
         if bt.dtype != torch.int32 or bt.dim() != 2 or bt.shape[0] < N or bt.stride(1) != 1:
-            raise ValueError(f"{name}_bt must be int32 [>= N, max_blocks] with contiguous rows")
+            raise DecodeReaderError(f"{name}_bt must be int32 [>= N, max_blocks] with contiguous rows")
         if ln.dtype != torch.int32 or ln.dim() != 1 or ln.shape[0] < N or ln.stride(0) != 1:
-            raise ValueError(f"{name}_len must be a contiguous int32 [>= N] tensor")
+            raise DecodeReaderError(f"{name}_len must be a contiguous int32 [>= N] tensor")
         return bt.stride(0)
 
     def __call__(self, q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale):
         N = q.shape[0]
         if N > self.max_n or q.shape[1:] != (self.hq, self.d):
-            raise ValueError(f"q must be [N <= {self.max_n}, {self.hq}, {self.d}], got {tuple(q.shape)}")
+            raise DecodeReaderError(f"q must be [N <= {self.max_n}, {self.hq}, {self.d}], got {tuple(q.shape)}")
         for t, nm in ((q, "q"), (op_k, "op_k"), (own_k, "own_k"), (op_bt, "op_bt"), (own_bt, "own_bt")):
             if not t.is_cuda or t.device != self.device:
-                raise RuntimeError(f"{nm} must be on {self.device} (there is no CPU path)")
+                raise DecodeReaderDeviceError(f"{nm} must be on {self.device} (there is no CPU path)")
         if op_k.dtype not in _DTYPES or own_k.dtype != op_k.dtype:
-            raise ValueError("pools must both be fp16 or both bf16")
+            raise DecodeReaderError("pools must both be fp16 or both bf16")
         if op_k.shape[2:] != (self.hkv, self.d) or own_k.shape[2:] != (self.hkv, self.d):
-            raise ValueError(f"pools must be [num_blocks, block_size, {self.hkv}, {self.d}]")
+            raise DecodeReaderError(f"pools must be [num_blocks, block_size, {self.hkv}, {self.d}]")
         self._pool(op_k, op_v, "operator")
         self._pool(own_k, own_v, "own")
         self._table(op_bt, op_len, N, "op")
@@ -132,7 +144,7 @@ class DecodeState:
                  dummy_block: int, device):
         device = torch.device(device)
         if device.type != "cuda":
-            raise RuntimeError("DecodeState lives on a ROCm GPU (there is no CPU path)")
+            raise DecodeReaderDeviceError("DecodeState lives on a ROCm GPU (there is no CPU path)")
         if min(max_n, n_slots, own_blocks, block_size, max_op_blocks) < 1 or dummy_block < 0:
             raise ValueError("sizes must be >= 1 and dummy_block >= 0")
         self.max_n, self.n_slots, self.own_blocks = int(max_n), int(n_slots), int(own_blocks)

@@ -70,7 +70,9 @@ class LibraryPool:
                 else:
                     self.free[i] = (s + n, ln - n)
                 return s
-        raise MemoryError(f"no free range of {n} pages in the pool (free ranges: {self.free})")
+        # The reference's static pool reports a full pool as torch.cuda.OutOfMemoryError
+        # (xenc/d23_vllm_plugin.py:181-183), the error its serving retry path keys on.
+        raise torch.cuda.OutOfMemoryError(f"no free range of {n} pages in the pool (free ranges: {self.free})")
 
     def _release(self, start: int, n: int) -> None:
         self.free.append((start, n))

@@ -10,6 +10,8 @@ Pins (each function is checked by tests/test_oracle.py against something other t
                                invariants (:241-261), subset == rebuild (:186-199)
   route                        brute-force rank counting in pure Python, sum/sparsity invariants
                                (tests/test_library.py:126-145)
+  boundary_gap                 closed forms: a planted exact tie at the k-th place gives 0, a
+                               planted gap gives that gap, k = 0 or k >= C gives +inf
   read                         pure-Python loops on tiny inputs; one-chunk closed form
                                (tests/test_library.py:91-123); linear-read closed form
                                (tests/test_integration.py:139-173); one-hot force_attn

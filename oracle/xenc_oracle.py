@@ -247,28 +247,6 @@ def lse_merge(o1, l1, o2, l2):
     return o1.float() * torch.exp(l1 - lse).t().unsqueeze(-1) + o2.float() * torch.exp(l2 - lse).t().unsqueeze(-1)
 
 
-# ----------------------------------------------------------------------------- batched decode (C2/C3)
-def batched_decode(q: torch.Tensor, libs, route_temp=10.0, read_temp=12.0, top_k=0, routed_only=False):
-    """One query row per sequence b, each reading its own Library (K_b, M_b, S_b): the reference has
-    one Library per call, so this is a loop of calls (xenc/injector.py:236-265 per sequence).
-    routed_only=True reads just the routed chunks (same value, fewer bytes).
-    Returns (r [B, d], list of w_b [C_b])."""
-    rs, ws = [], []
-    for b, (K, M, S) in enumerate(libs):
-        qb = q[b].view(1, 1, -1)
-        w = route(qb, S, route_temp, top_k)
-        if routed_only:
-            C = S.shape[0]
-            k = C if (not top_k or top_k >= C) else top_k
-            order = topk_order(w.view(1, -1), k)
-            r = read_routed(q[b:b + 1], K, M, order, w.view(1, -1).gather(-1, order), read_temp)
-        else:
-            r, _ = read(qb, K, M, w, read_temp)
-        rs.append(r.reshape(-1))
-        ws.append(w.reshape(-1))
-    return torch.stack(rs), ws
-
-
 # ----------------------------------------------------------------------------- D8 slot top-k read ((f)4)
 def select_scores(q: torch.Tensor, keys: torch.Tensor, valid: torch.Tensor | None = None,
                   pool: str = "max") -> torch.Tensor:

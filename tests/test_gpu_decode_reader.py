@@ -156,24 +156,39 @@ def test_decode_reader_is_deterministic(dev):
 
 
 def test_decode_reader_rejects_bad_inputs(dev):
+    """Bad shapes, tables, dtypes and devices raise errors that are both this build's types
+    (ValueError / RuntimeError) and the reference's (AssertionError: its __call__ asserts its
+    preconditions, xenc/d23_read_kernels.py:146-150)."""
     say("op B guards")
     with pytest.raises(ValueError):
         DecodeReader(4, 36, 4, 64, 128, dev)          # G = 9
-    with pytest.raises(ValueError):
+    with pytest.raises(AssertionError):
         DecodeReader(4, 16, 4, 60, 128, dev)          # d % 8
     dec = DecodeReader(2, 8, 2, 64, 128, dev)
     args = [a.to(dev) for a in _case(3, 8, 2, 64, 16, 10, 10, 0, torch.bfloat16, op_blocks=4, own_blocks=4)]
-    with pytest.raises(ValueError):
-        dec(*args, 0.1)                                # N above max_n
+    for exc in (ValueError, AssertionError):
+        with pytest.raises(exc):
+            dec(*args, 0.1)                            # N above max_n
     args = [a.to(dev) for a in _case(2, 8, 2, 64, 16, 10, 10, 0, torch.bfloat16, op_blocks=4, own_blocks=4)]
     bad = list(args)
     bad[4] = bad[4].long()
-    with pytest.raises(ValueError):
-        dec(*bad, 0.1)
+    for exc in (ValueError, AssertionError):
+        with pytest.raises(exc):
+            dec(*bad, 0.1)
     bad = list(args)
     bad[2] = bad[2].half()
-    with pytest.raises(ValueError):
+    for exc in (ValueError, AssertionError):
+        with pytest.raises(exc):
+            dec(*bad, 0.1)
+    bad = list(args)
+    bad[5] = bad[5][:, :8]                             # own K and V pools of different shapes
+    with pytest.raises(AssertionError):
         dec(*bad, 0.1)
+    bad = list(args)
+    bad[0] = bad[0].cpu()                              # q on the host
+    for exc in (RuntimeError, AssertionError):
+        with pytest.raises(exc):
+            dec(*bad, 0.1)
 
 
 def test_decode_reader_zero_rows(dev):

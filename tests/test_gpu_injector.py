@@ -167,7 +167,8 @@ def test_training_gradients_match_oracle(dev, top_k):
     (ref_out * g_up.double()).sum().backward()
     ours, theirs = dict(itf.named_parameters()), dict(it.named_parameters())
     for name in ("A.weight", "B.weight", "gate_w", "gate_b", "log_gain"):
-        ok, err, rn = close(ours[name].grad, theirs[name].grad, rel=2e-2, atol=5e-3)
+        ok, err, rn = close(ours[name].grad, theirs[name].grad)      # rel 1e-2, max-abs 2e-3
+        print(f"[grad] top_k={top_k} {name}: max-abs {err:.3g} rel {rn:.3g}", flush=True)
         assert ok, (top_k, name, err, rn)
 
 

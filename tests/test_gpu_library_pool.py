@@ -71,7 +71,7 @@ def test_pool_reads_like_fresh_build_and_reuses_ranges(dev):
     fresh2 = ops.PagedLibrary.from_doc_caches([DOCS["d"], DOCS["a"]], RHO, dev, center=center)
     assert torch.equal(_read(lib2, q, qg), _read(fresh2, q, qg))
     free_before = list(pool.free)
-    with pytest.raises(MemoryError):
+    with pytest.raises(torch.cuda.OutOfMemoryError):   # the reference's full-pool error
         pool.load("e", _cache([5] * 5, 7), RHO)  # 5 chunks; all 16 pages are taken (a, d, c)
     assert "e" not in pool.docs and pool.free == free_before
 

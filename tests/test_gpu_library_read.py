@@ -262,6 +262,32 @@ def test_full_size_decode_workloads(dev, name):
         _check_close(r[b], ref.view(-1), f"{name} row {b}")
 
 
+@pytest.mark.parametrize("name", ["single_decode", "batched_paged_decode"])
+def test_full_size_fused_step(dev, name):
+    """The benchmark's timed step itself, ops.route_read_decode (routing folded into the read's
+    launches), on the benchmark's own inputs: routed indices bit-exact against the fp64 oracle
+    for every row, read parity on a sample of rows, and equal bit for bit to the separate
+    route_topk + library_read_decode."""
+    say("full-size fused step", name)
+    P, q, qg, top_k = synth.decode_workload(name, device=dev)
+    lib = ops.PagedLibrary(P.pages, P.chunk_page, P.chunk_nvalid, P.chunk_ptr, P.S,
+                           n_chunks=P.n_chunks, nvalid=P.nvalid)
+    w, idx, wsel, r = ops.route_read_decode(q, lib, qg, top_k=top_k, route_temp=10.0, read_temp=12.0)
+    w1, i1, s1 = ops.route_topk(q, lib, qg, top_k=top_k, route_temp=10.0)
+    r1 = ops.library_read_decode(q, lib, i1, s1, qg, read_temp=12.0)
+    torch.cuda.synchronize()
+    assert torch.equal(idx, i1) and torch.equal(wsel, s1) and torch.equal(w, w1)
+    assert torch.equal(r, r1), float((r - r1).abs().max())
+    B = q.shape[0]
+    qc = q.cpu()
+    assert _check_route(P, qc, list(range(B)), w, idx, wsel, top_k) == 0
+    for b in sorted(set([0, min(1, B - 1), B - 1, B // 2, B // 3, (2 * B) // 3])):
+        K, M, S = P.library(b)
+        ref, _ = O.branch_read(qc[b].view(1, 1, -1).double(), K.cpu().double(), M.cpu(), S.cpu().double(),
+                               top_k=top_k)
+        _check_close(r[b], ref.view(-1), f"{name} fused row {b}")
+
+
 def test_repeated_calls_are_bit_identical(dev):
     """The per-query arrival counters re-arm themselves: many calls in a row (different nsplit,
     hence different workspace layouts) give bit-identical results."""

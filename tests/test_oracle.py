@@ -114,6 +114,24 @@ def test_route_tie_goes_to_lower_index():
     assert O.topk_order(torch.tensor([0.5, 0.9, 0.9, 0.1]), 3).tolist() == [1, 2, 0]
 
 
+def test_boundary_gap_closed_forms():
+    """boundary_gap = (k-th largest dot) - ((k+1)-th largest dot), in fp64.  With S = I the dots
+    are the query's own entries, so every gap is known in closed form: a planted tie at the k-th
+    place gives exactly 0, planted gaps give themselves (entries out of order, so a missing sort
+    or an off-by-one rank fails), and dense routing (k = 0 or k >= C) gives +inf."""
+    S = torch.eye(4, dtype=torch.float64)
+    q = torch.tensor([[[0.125, 0.625, 0.875, 0.5]], [[0.125, 0.625, 0.875, 0.625]]], dtype=torch.float64)
+    assert O.boundary_gap(q, S, 1).tolist() == [[0.25], [0.25]]
+    assert O.boundary_gap(q, S, 2).tolist() == [[0.125], [0.0]]        # row 1: a tie at the boundary
+    assert O.boundary_gap(q, S, 3).tolist() == [[0.375], [0.5]]
+    for k in (0, 4, 9):
+        g = O.boundary_gap(q, S, k)
+        assert g.shape == (2, 1) and bool(torch.isinf(g).all()) and g.dtype == torch.float64
+    # fp32 inputs are compared in fp64: a gap below fp32's resolution near 1 is still seen
+    q32 = torch.tensor([[1.0, 1.0 - 2.0 ** -23, 0.0]], dtype=torch.float32)
+    assert O.boundary_gap(q32, torch.eye(3), 1).item() == 2.0 ** -23
+
+
 # ---------------------------------------------------------------- R5: read
 def _read_brute(q, K, M, w, temp, softmax=True):
     C, N, d = len(K), len(K[0]), len(K[0][0])
