@@ -51,6 +51,28 @@ __device__ __forceinline__ f32x16 mfma32(const half8_t& a, const half8_t& b, con
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
+// Instruction classes of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
+
+// One 16-byte chunk per lane from global memory straight into LDS (gfx950
+// global_load_lds_dwordx4): lane i of the wave writes lds_wave_base + 16 i.  lds_wave_base must
+// be wave-uniform.  Issued as inline assembly so that the compiler does not treat the LDS
+// write as pending at every barrier and LDS read (it would wait for every outstanding global
+// load there); the caller waits for these loads itself (wait_vmem) before publishing the LDS.
+__device__ __forceinline__ void stage_to_lds(_Float16* lds_wave_base, const _Float16* src) {
+  const unsigned lds = __builtin_amdgcn_readfirstlane(
+      (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_wave_base);
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding (they complete in
+// issue order for the counter).
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 constexpr int kChunkGroup = 4;  // scores tiles: chunks per group, all row tiles of a group adjacent
 
 // Library g of tile b: tile_ptr[g] <= b < tile_ptr[g+1] (binary search; G is small).
@@ -161,25 +183,22 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
     abase[mt] = Ka + (long long)min(wv * 2 + mt, N / 32 - 1) * (d / 16) * 512 + lane * 8;
-  // B staging: 128 rows x 8 chunks, 2 per thread (rows past the library are not stored).
-  int brow[2], bch[2];
-  const _Float16* xrow[2];
+  // B staging, straight from global memory into LDS (gfx950 global_load_lds_dwordx4): a stage is
+  // 128 rows x 8 chunks of 16 bytes, LDS chunk id = tid + 512 i (two per thread), and a wave's 64
+  // lanes fill 1 KiB of LDS in lane order.  The swizzle is applied on the global side: the lane
+  // that fills LDS position p of row r loads the row's chunk p ^ swizzle(r).  Rows past the
+  // library re-read its last row (their scores are never stored).
+  const _Float16* xdir[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int id = tid + 512 * i;
-    brow[i] = id >> 3;
-    bch[i] = id & 7;
-    xrow[i] = X + (long long)min(row0 + brow[i], rend - 1) * d + bch[i] * 8;
+    const int r = id >> 3;
+    xdir[i] = X + (long long)min(row0 + r, rend - 1) * d + (((id & 7) ^ ((r ^ (r >> 3)) & 7)) << 3);
   }
   half8_t fa[2][4];  // [mt][k16 step]: refilled for the next k-step as soon as it is consumed
-  u32x4 rb[2];
-  auto load_b = [&](int k0) {
+  auto stage_b = [&](int st, int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) rb[i] = *reinterpret_cast<const u32x4*>(xrow[i] + k0);
-  };
-  auto store_b = [&](int st) {
-#pragma unroll
-    for (int i = 0; i < 2; ++i) *reinterpret_cast<u32x4*>(&lB[st][swz(brow[i], bch[i])]) = rb[i];
+    for (int i = 0; i < 2; ++i) stage_to_lds(&lB[st][(512 * i + 64 * wv) * 8], xdir[i] + k0);
   };
 
   f32x16 acc[2][4];
@@ -198,13 +217,22 @@ __global__ __launch_bounds__(512) void scores_kernel(
     for (int nt = 0; nt < 4; ++nt)
       fb0[nt] = *reinterpret_cast<const half8_t*>(&lB[st][swz(nt * 32 + l32, hl)]);
   };
+  // One k-step: four k16 steps of 8 MFMAs.  The B fragments of k16 step ks + 1 are read from
+  // LDS while the MFMAs of step ks issue (MFMA and ds_read alternating), and the two A fragment
+  // refills go out between the last MFMAs, so no MFMA waits on a read issued just before it.
+  // The group barriers fix that order; left alone, the compiler sinks every read to just before
+  // its first use.
   auto compute = [&](int st, int knext) {
+    half8_t fbn[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       half8_t fb[4];
 #pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-        fb[nt] = ks == 0 ? fb0[nt] : *reinterpret_cast<const half8_t*>(&lB[st][swz(nt * 32 + l32, ks * 2 + hl)]);
+      for (int nt = 0; nt < 4; ++nt) fb[nt] = ks == 0 ? fb0[nt] : fbn[nt];
+      if (ks < 3)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+          fbn[nt] = *reinterpret_cast<const half8_t*>(&lB[st][swz(nt * 32 + l32, (ks + 1) * 2 + hl)]);
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
@@ -212,35 +240,53 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
         fa[mt][ks] = *reinterpret_cast<const half8_t*>(abase[mt] + (knext / 16 + ks) * 512);
+      if (ks < 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        }
+      } else {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // The prefetch past the last k-step re-reads it (no branch around a load).
+  // The prefetch past the last k-step re-reads it (no branch around a load).  The first A
+  // fragments load in the loop's own order (k16 step major), so the wait counts the compiler
+  // derives for the loop hold on entry too.
   const int nk = d / BK;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) fa[mt][ks] = *reinterpret_cast<const half8_t*>(abase[mt] + ks * 512);
-  // Three LDS stages: k-step k reads stage k % 3 while the rows of step k + 2 are stored into
-  // stage (k + 2) % 3 (last read in step k - 1, before the barrier that ended it) and the first
-  // fragments of step k + 1 are read from stage (k + 1) % 3 (stored in step k - 1, before that
-  // same barrier).  One barrier per k-step.
-  load_b(0);
-  store_b(0);
-  load_b(min(1, nk - 1) * BK);
-  store_b(1);
+    for (int mt = 0; mt < 2; ++mt) fa[mt][ks] = *reinterpret_cast<const half8_t*>(abase[mt] + ks * 512);
+  // Three LDS stages: k-step k reads stage k % 3; at its start it stages the rows of step k + 2
+  // into stage (k + 2) % 3 (last read in step k - 1, before the barrier that ended it), waits for
+  // them at its end, and reads the first fragments of step k + 1 from stage (k + 1) % 3 (staged in
+  // step k - 1 and published by that barrier).  One barrier per k-step.  The staging loads are
+  // invisible to the compiler's wait counts, so their waits are explicit: at the end of a
+  // k-step only its 8 A fragment refills (issued after the staging) may still be in flight.
+  stage_b(0, 0);
+  stage_b(1, min(1, nk - 1) * BK);
+  wait_vmem<0>();
   __syncthreads();
   read_fb0(0);
   for (int k = 0; k < nk; ++k) {
     const int k1 = min(k + 1, nk - 1) * BK;
-    load_b(min(k + 2, nk - 1) * BK);
+    stage_b((k + 2) % 3, min(k + 2, nk - 1) * BK);
     __builtin_amdgcn_sched_barrier(0);
     compute(k % 3, k1);
-    store_b((k + 2) % 3);
+    wait_vmem<8>();
     read_fb0((k + 1) % 3);
     __syncthreads();
   }
+  wait_vmem<0>();
 
   // acc[mt][nt][r] = S^T[slot][row]: slot = 64w + 32mt + 8(r/4) + 4hl + r%4, row = 32nt + l32.
   auto slot_of = [&](int mt, int r) { return wv * 64 + mt * 32 + (r >> 2) * 8 + hl * 4 + (r & 3); };
@@ -486,31 +532,53 @@ __global__ __launch_bounds__(256) void readout_kernel(
     for (int mt = 0; mt < NA; ++mt)
       fa0[mt] = *reinterpret_cast<const half8_t*>(&lA[st][swz(mt * 32 + l32, hl)]);
   };
+  // As in the scores kernel: the A fragments of k16 step ks + 1 are read while the MFMAs of
+  // step ks issue, and the B refills go out between the last MFMAs.
   auto compute = [&](int st, const _Float16* kbn, int nbn) {
+    half8_t fan[NA];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
+      half8_t fa[NA];
 #pragma unroll
-      for (int mt = 0; mt < NA; ++mt) {
-        const half8_t fa =
-            ks == 0 ? fa0[mt] : *reinterpret_cast<const half8_t*>(&lA[st][swz(mt * 32 + l32, ks * 2 + hl)]);
+      for (int mt = 0; mt < NA; ++mt) fa[mt] = ks == 0 ? fa0[mt] : fan[mt];
+      if (ks < 3)
 #pragma unroll
-        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(fa, fb[nt][ks], acc[mt][nt]);
-      }
+        for (int mt = 0; mt < NA; ++mt)
+          fan[mt] = *reinterpret_cast<const half8_t*>(&lA[st][swz(mt * 32 + l32, (ks + 1) * 2 + hl)]);
+#pragma unroll
+      for (int mt = 0; mt < NA; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = mfma32(fa[mt], fb[nt][ks], acc[mt][nt]);
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt)
         fb[nt][ks] = *reinterpret_cast<const half8_t*>(kbn + ((long long)dbk[nt] * (N / 16) + nbn + ks) * 512);
-      __builtin_amdgcn_sched_barrier(0);  // keep the refill here (see the scores kernel)
+      static_assert(NA == 4, "the schedule below is written for 8 MFMAs per k16 step");
+      if (ks < 3) {
+#pragma unroll
+        for (int i = 0; i < NA; ++i) {
+          __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 1, 0);
+        }
+      } else {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedVmemRead, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 2, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
   };
 
   const int kpc = N / BK;  // k-steps per chunk
   const int total = C * kpc;
-  {
+  {  // in the loop's own order (k16 step major), as in the scores kernel
     const _Float16* kb0 = kb_base(0);
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt)
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+      for (int nt = 0; nt < 2; ++nt)
         fb[nt][ks] = *reinterpret_cast<const half8_t*>(kb0 + ((long long)dbk[nt] * (N / 16) + ks) * 512);
   }
   // Three LDS stages, as in the scores kernel: step it reads stage it % 3, stores the rows of
