@@ -172,21 +172,26 @@ def measured_stream_peak(dev, gib: int = 2) -> float:
     return best
 
 
-def timed_steps(step, steps: int, stream):
+def timed_steps(step, steps: int, stream, host: list | None = None):
     """Times `steps` back-to-back calls of `step` with nothing else queued between them, closed
     by a device synchronisation on each side.  Returns (wall ms per step, GPU ms per step): the
     second from ONE event pair around the whole region on `stream`, so it is the span the kernels
     of the K steps occupy, gaps between them included.  A timing event between steps would add
-    GPU idle time of its own (about 10 us per pair on this stack), so none is recorded there."""
+    GPU idle time of its own (about 10 us per pair on this stack), so none is recorded there.
+    `host`, when given, receives the host time per step spent issuing the calls (the loop before
+    the closing synchronisation): the step's host cost while the launch queue does not block."""
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     a.record(stream)
     for _ in range(steps):
         step()
+    t_issue = time.perf_counter()
     b.record(stream)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
+    if host is not None:
+        host.append((t_issue - t0) * 1e3 / steps)
     return wall, a.elapsed_time(b) / steps
 
 
@@ -376,7 +381,8 @@ def bench_multi_depth(args):
     for _ in range(args.warmup):
         step()
     stream = torch.cuda.current_stream(dev)
-    ms_eager, span_eager = timed_steps(step, args.steps, stream)
+    host = []
+    ms_eager, span_eager = timed_steps(step, args.steps, stream, host)
 
     # The step captured once in a HIP graph and replayed.  Every replay is checked against the
     # eager result (bit for bit) with eager work and synchronisation in between; on
@@ -423,7 +429,8 @@ def bench_multi_depth(args):
         "config": {"workload": "multi_depth", "depths": L, "chunks_per_depth": c["chunks"],
                    "slots_per_page": c["N"], "d_s": d, "d_reader": dr, "batch": B,
                    "selector_top_k": c["k_sel"], "top_k": k, "B_dtype": "fp32", "accumulate": "fp32",
-                   "timing": timing, "ms_per_step_eager": ms_eager, "ms_per_step_graph": ms_graph},
+                   "timing": timing, "ms_per_step_eager": ms_eager, "ms_per_step_graph": ms_graph,
+                   "host_issue_us_per_step": host[0] * 1e3},
         "roofline": {"bound": "hbm", "kernel": "whole step (route + read + write-back + epilogue)",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None,
@@ -746,7 +753,8 @@ def bench_decode(args):
     # Eager steps: the q . S dots, the read kernel with the top-k in its prologue and the merge,
     # K steps back to back.  The roofline figure counts the step's algorithmic bytes (routed
     # pages, S, q and r) over the GPU span per step of the timed region.
-    ms_eager, span_eager = timed_steps(step, args.steps, stream)
+    host = []
+    ms_eager, span_eager = timed_steps(step, args.steps, stream, host)
 
     # The step captured once in a HIP graph and replayed.  Every replay is checked bit for bit
     # against the eager result, with eager work and a synchronisation in between; on any
@@ -789,7 +797,8 @@ def bench_decode(args):
                    "slots_per_page": P.pages.shape[1], "top_k": top_k, "read_temp": read_temp,
                    "route_temp": route_temp, "accumulate": "fp32", "page_table": "seeded shuffle",
                    "nsplit": args.nsplit or ops.default_nsplit(B * idx_h.shape[1], P.pages.shape[1]),
-                   "timing": timing, "ms_per_step_eager": ms_eager, "ms_per_step_graph": ms_graph},
+                   "timing": timing, "ms_per_step_eager": ms_eager, "ms_per_step_graph": ms_graph,
+                   "host_issue_us_per_step": host[0] * 1e3},
         "roofline": {"bound": "hbm",
                      "kernel": "route_dots_kernel + decode_read_kernel (top-k in its prologue) + merge_kernel",
                      "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",

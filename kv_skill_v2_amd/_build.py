@@ -18,6 +18,8 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIBDIR = PKG / "_lib"
 LIB = LIBDIR / "libxenc_hip.so"
+TORCH_LIB = LIBDIR / "libxenc_torch.so"
+TORCH_OPS_SRC = CSRC / "torch_ops.cpp"
 ARCH = "gfx950"
 
 # Packed fp32 VALU ops are disabled: the kernels here are written for scalar/float4 math.
@@ -64,7 +66,31 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             list(ex.map(lambda c: _run(c, verbose), cmds))
         _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)], verbose)
     os.replace(tmp, LIB)
+    build_torch_ops(verbose)
     return LIB
+
+
+def build_torch_ops(verbose: bool = False) -> Path:
+    """The per-token operators registered in torch's dispatcher from C++ (csrc/torch_ops.cpp):
+    host code only, compiled by the system C++ compiler against torch's headers and linked to
+    libxenc_hip.so (found next to it at load time)."""
+    import torch
+
+    tdir = Path(torch.__file__).resolve().parent
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "c++"
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    tmp = TORCH_LIB.with_suffix(".so.tmp")
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-w",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           "-I", str(tdir / "include"), "-I", str(tdir / "include" / "torch" / "csrc" / "api" / "include"),
+           "-I", str(Path(rocm) / "include"), "-I", str(PKG.parent / "include"),
+           str(TORCH_OPS_SRC), "-o", str(tmp),
+           "-L", str(tdir / "lib"), "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           "-L", str(LIBDIR), "-lxenc_hip", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{tdir / 'lib'}"]
+    _run(cmd, verbose)
+    os.replace(tmp, TORCH_LIB)
+    return TORCH_LIB
 
 
 if __name__ == "__main__":

@@ -199,7 +199,17 @@ def check(rc: int, what: str) -> None:
 
 
 def stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw hipStream_t of torch's current stream on `device` (0 = the null stream)."""
+    return _raw_stream(device.index if device.index is not None else torch.cuda.current_device())
+
+
+def _raw_stream_api(index: int) -> int:
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+# torch's own accessor of the raw current stream (what its Triton launcher uses) skips building a
+# Stream object per call; the public API is the fallback.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None) or _raw_stream_api
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -79,6 +79,7 @@ class PagedLibrary:
     d_valid: int = 0                     # leading feature dims in use (the rest is zero padding)
     _frag: dict = field(default_factory=dict, repr=False, compare=False)
     _plans: dict = field(default_factory=dict, repr=False, compare=False)
+    _kept: dict = field(default_factory=dict, repr=False, compare=False)
 
     def __post_init__(self):
         for name in ("pages", "chunk_page", "chunk_nvalid", "chunk_ptr", "S"):
@@ -256,8 +257,12 @@ class PagedLibrary:
         return self.pages.device
 
     def kept(self, top_k: int) -> int:
-        """Width of the routed-index arrays: max over libraries of the kept chunk count."""
-        return max(c if (top_k <= 0 or top_k >= c) else top_k for c in self.n_chunks)
+        """Width of the routed-index arrays: max over libraries of the kept chunk count (kept per
+        top_k: the chunk counts of a pool do not change after construction)."""
+        k = self._kept.get(top_k)
+        if k is None:
+            k = self._kept[top_k] = max(c if (top_k <= 0 or top_k >= c) else top_k for c in self.n_chunks)
+        return k
 
     def check_prefill(self) -> None:
         """The MFMA prefill kernels step d and the slots by 64 and take a page of <= 512 slots."""
@@ -302,6 +307,10 @@ class PagedLibrary:
 
 
 def _groups(lib_: PagedLibrary, M: int, q_group) -> torch.Tensor:
+    if (isinstance(q_group, torch.Tensor) and q_group.is_cuda and q_group.dtype == torch.int32
+            and q_group.dim() == 1 and q_group.shape[0] == M and q_group.is_contiguous()
+            and q_group.device == lib_.device):
+        return q_group          # the per-token path: already a device int32 vector
     if q_group is None:
         if lib_.n_libraries != 1:
             raise ValueError("q_group is required when the pool holds several libraries")
@@ -321,7 +330,8 @@ def _query(q: torch.Tensor, d: int) -> torch.Tensor:
     _require_device(q, "q")
     if q.dim() != 2 or q.shape[1] != d:
         raise ValueError(f"q must be [M, {d}], got {tuple(q.shape)}")
-    q = q.to(torch.float32)
+    if q.dtype != torch.float32:
+        q = q.to(torch.float32)
     if q.stride(1) != 1 or q.stride(0) % 4 or q.data_ptr() % 16:
         q = q.contiguous()
     return q
@@ -355,10 +365,14 @@ class _Workspaces:
 
     def __init__(self):
         self._ws = {}
+        self._fits = set()       # (device, stream, M, kk, nsplit, d) already checked to fit
 
     def get(self, device: torch.device, stream: int, M: int, kk: int, nsplit: int, d: int):
         key = (device.index, stream)
-        buf, rows = self._ws.get(key, (None, 0))
+        hit = self._ws.get(key)
+        if hit is not None and (key, M, kk, nsplit, d) in self._fits:
+            return hit
+        buf, rows = hit if hit is not None else (None, 0)
         L = lib()
         if buf is None or rows < M or buf.numel() < L.xenc_decode_workspace_bytes(rows, kk, nsplit, d):
             rows = max(rows, M, 64)
@@ -368,6 +382,8 @@ class _Workspaces:
             buf = torch.empty(size, dtype=torch.uint8, device=device)
             check(L.xenc_decode_workspace_init(ptr(buf), size, rows, stream), "xenc_decode_workspace_init")
             self._ws[key] = (buf, rows)
+            self._fits = {f for f in self._fits if f[0] != key}
+        self._fits.add((key, M, kk, nsplit, d))
         return buf, rows
 
 

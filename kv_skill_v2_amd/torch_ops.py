@@ -35,7 +35,23 @@ import torch
 from torch import Tensor
 from torch.library import custom_op
 
-from ._lib import check, lib, ptr, stream_handle
+from ._lib import LIB_PATH, XencError, check, lib, ptr, stream_handle
+
+# The per-token operators (route_topk, library_read, route_read, paged_decode_joint) are defined
+# and implemented in C++ (csrc/torch_ops.cpp -> libxenc_torch.so): one dispatcher hop into the C
+# ABI per call.  Their fake kernels are registered below.
+TORCH_OPS_PATH = LIB_PATH.with_name("libxenc_torch.so")
+
+
+def _load_cpp_ops() -> None:
+    lib()  # libxenc_hip.so first: its C ABI is version-checked, and libxenc_torch.so links to it
+    if not TORCH_OPS_PATH.exists():
+        raise XencError(f"{TORCH_OPS_PATH} is not built: run kv_skill_v2_amd._build.build() "
+                        "(the Library read has no CPU path)")
+    torch.ops.load_library(str(TORCH_OPS_PATH))
+
+
+_load_cpp_ops()
 
 
 def _st(t: Tensor) -> int:
@@ -48,73 +64,21 @@ def kept_width(top_k: int, cmax: int) -> int:
 
 
 # ----------------------------------------------------------------------------- decode routing
-@custom_op("xenc::route_topk", mutates_args=())
-def route_topk(q: Tensor, S: Tensor, chunk_ptr: Tensor, q_group: Tensor, top_k: int, route_temp: float,
-               cmax: int, kk: int) -> tuple[Tensor, Tensor, Tensor]:
-    M, d = q.shape
-    w = torch.empty(M, cmax, dtype=torch.float32, device=q.device)
-    idx = torch.empty(M, kk, dtype=torch.int32, device=q.device)
-    wsel = torch.empty(M, kk, dtype=torch.float32, device=q.device)
-    if M:
-        check(lib().xenc_route_topk(ptr(q), q.stride(0), M, d, ptr(S), ptr(chunk_ptr), ptr(q_group),
-                                    chunk_ptr.numel() - 1, top_k, route_temp, ptr(w), w.stride(0), ptr(idx),
-                                    ptr(wsel), kk, _st(q)), "xenc_route_topk")
-    return w, idx, wsel
-
-
-@route_topk.register_fake
+@torch.library.register_fake("xenc::route_topk")
 def _(q, S, chunk_ptr, q_group, top_k, route_temp, cmax, kk):
     M = q.shape[0]
     return (q.new_empty(M, cmax), q.new_empty(M, kk, dtype=torch.int32), q.new_empty(M, kk))
 
 
 # ----------------------------------------------------------------------------- decode read
-@custom_op("xenc::library_read", mutates_args=("workspace",))
-def library_read(q: Tensor, pages: Tensor, chunk_page: Tensor, chunk_nvalid: Tensor, chunk_ptr: Tensor,
-                 q_group: Tensor, idx: Tensor, w_sel: Tensor, read_temp: float, softmax: bool, nsplit: int,
-                 workspace: Tensor, max_rows: int) -> Tensor:
-    M = q.shape[0]
-    d = pages.shape[-1]
-    r = torch.empty(M, d, dtype=torch.float32, device=q.device)
-    kk = idx.shape[1]
-    if M == 0 or kk == 0:
-        return r.zero_()
-    check(lib().xenc_library_read_decode(
-        ptr(q), q.stride(0), M, d, ptr(pages), pages.shape[1], pages.stride(0), ptr(chunk_page),
-        ptr(chunk_nvalid), ptr(chunk_ptr), ptr(q_group), chunk_ptr.numel() - 1, ptr(idx), ptr(w_sel), kk,
-        read_temp, int(softmax), nsplit, ptr(r), r.stride(0), ptr(workspace), workspace.numel(), max_rows,
-        _st(q)), "xenc_library_read_decode")
-    return r
-
-
-@library_read.register_fake
+@torch.library.register_fake("xenc::library_read")
 def _(q, pages, chunk_page, chunk_nvalid, chunk_ptr, q_group, idx, w_sel, read_temp, softmax, nsplit,
       workspace, max_rows):
     return q.new_empty(q.shape[0], pages.shape[-1])
 
 
 # ----------------------------------------------------------------------------- decode routing + read
-@custom_op("xenc::route_read", mutates_args=("workspace",))
-def route_read(q: Tensor, S: Tensor, pages: Tensor, chunk_page: Tensor, chunk_nvalid: Tensor, chunk_ptr: Tensor,
-               q_group: Tensor, top_k: int, route_temp: float, cmax: int, kk: int, read_temp: float, softmax: bool,
-               nsplit: int, workspace: Tensor, max_rows: int) -> tuple[Tensor, Tensor, Tensor, Tensor]:
-    """Routing and the read of few rows in one call -> (w [M, cmax], idx [M, kk], w_sel [M, kk], r [M, d]);
-    the top-k runs inside the read kernel when every library has at most 64 chunks."""
-    M, d = q.shape
-    w = torch.empty(M, cmax, dtype=torch.float32, device=q.device)
-    idx = torch.empty(M, kk, dtype=torch.int32, device=q.device)
-    wsel = torch.empty(M, kk, dtype=torch.float32, device=q.device)
-    r = torch.empty(M, pages.shape[-1], dtype=torch.float32, device=q.device)
-    if M:
-        check(lib().xenc_route_read_decode(
-            ptr(q), q.stride(0), M, d, ptr(S), ptr(pages), pages.shape[1], pages.stride(0), ptr(chunk_page),
-            ptr(chunk_nvalid), ptr(chunk_ptr), ptr(q_group), chunk_ptr.numel() - 1, top_k, route_temp, ptr(w),
-            w.stride(0), ptr(idx), ptr(wsel), kk, read_temp, int(softmax), nsplit, ptr(r), r.stride(0),
-            ptr(workspace), workspace.numel(), max_rows, _st(q)), "xenc_route_read_decode")
-    return w, idx, wsel, r
-
-
-@route_read.register_fake
+@torch.library.register_fake("xenc::route_read")
 def _(q, S, pages, chunk_page, chunk_nvalid, chunk_ptr, q_group, top_k, route_temp, cmax, kk, read_temp, softmax,
       nsplit, workspace, max_rows):
     M = q.shape[0]
@@ -306,29 +270,10 @@ library_prefill_fwd.register_autograd(_prefill_backward, setup_context=_prefill_
 _JOINT_DTYPES = {torch.float16: 0, torch.bfloat16: 1}
 
 
-@custom_op("xenc::paged_decode_joint", mutates_args=("workspace", "out"))
-def paged_decode_joint(q: Tensor, op_k: Tensor, op_v: Tensor, op_bt: Tensor, op_len: Tensor, own_k: Tensor,
-                       own_v: Tensor, own_bt: Tensor, own_len: Tensor, scale: float, nsplit: int, chunk: int,
-                       workspace: Tensor, max_n: int, out: Tensor) -> None:
-    """out[:N] = the joint softmax read over [operator rows ; own rows] per query head (GQA);
-    pools [num_blocks, block_size, hkv, d] fp16 / bf16, tables int32."""
-    N, hq, d = q.shape
-    hkv = op_k.shape[2]
-    if N == 0:
-        return
-    check(lib().xenc_paged_decode_joint(
-        _JOINT_DTYPES[op_k.dtype], N, hq, hkv, d, ptr(q), q.stride(0), q.stride(1),
-        ptr(op_k), ptr(op_v), op_k.stride(0), op_k.stride(1), op_k.stride(2), op_k.shape[1], ptr(op_bt),
-        op_bt.stride(0), ptr(op_len), ptr(own_k), ptr(own_v), own_k.stride(0), own_k.stride(1), own_k.stride(2),
-        own_k.shape[1], ptr(own_bt), own_bt.stride(0), ptr(own_len), scale, nsplit, chunk, ptr(out),
-        out.stride(0), out.stride(1), ptr(workspace), workspace.numel(), max_n, _st(q)), "xenc_paged_decode_joint")
-
-
-@paged_decode_joint.register_fake
+@torch.library.register_fake("xenc::paged_decode_joint")
 def _(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale, nsplit, chunk, workspace, max_n, out):
     return None
 
 
-__all__ = ["route_topk", "library_read", "route_read", "route_rows", "route_backward_", "library_prefill_lse",
-           "library_prefill_fwd",
-           "library_prefill_bwd_dq", "paged_decode_joint", "kept_width"]
+__all__ = ["route_rows", "route_backward_", "library_prefill_lse", "library_prefill_fwd",
+           "library_prefill_bwd_dq", "kept_width", "TORCH_OPS_PATH"]
