@@ -275,7 +275,9 @@ def graph_of(step, same):
         step()
     torch.cuda.current_stream().wait_stream(s)
     gph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(gph):
+    # Captured on the warm-up stream: the per-stream decode workspace already exists there, so
+    # its one-time counter initialisation is not captured into the graph.
+    with torch.cuda.graph(gph, stream=s):
         out = step()
     for _ in range(3):
         gph.replay()

@@ -351,10 +351,13 @@ def route_topk(q: torch.Tensor, lib_: PagedLibrary, q_group=None, top_k: int = 0
 
 def default_nsplit(units: int, slots_per_page: int) -> int:
     """Slot splits per routed page.  With >= 128 (query, page) units one workgroup per page
-    (measured best on the B = 64 batched decode); fewer units are split so that about 128
-    workgroups stream the pages, in pieces of >= 32 slots (more, smaller splits cost more in the
-    merge than they gain: 1 query x 4 pages measured 23 us at 4..16 splits, 29 us at 32)."""
-    want = max(1, math.ceil(128 / max(units, 1)))
+    (measured best on the B = 64 batched decode); fewer units are split so that about
+    min(8 * units, 128) workgroups stream the pages, in pieces of >= 32 slots.  Very few units
+    stay at 8 splits per page because the last workgroup merges every partial: one query x 4
+    pages (the single-sequence decode) measured 34.4 / 23.4 / 18.9 / 17.8 / 20.0 / 26.9 us per
+    step at 1 / 2 / 4 / 8 / 16 / 32 splits."""
+    units = max(units, 1)
+    want = max(1, math.ceil(min(8 * units, 128) / units))
     return int(max(1, min(want, max(1, slots_per_page // 32), 64)))
 
 
