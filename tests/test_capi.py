@@ -76,3 +76,18 @@ def test_host_side_validation_rejects_bad_sizes():
     assert joint() == -2
     assert joint(N=5) == -4
     assert L.xenc_joint_workspace_bytes(4, 4, 2, 4, 64) >= 4 * 4 * 2 * 4 * 64 * 4
+
+
+def test_cpp_operators_registered():
+    """libxenc_torch.so loads on a GPU-less host and defines the per-token operators in torch's
+    dispatcher with a device (HIP) kernel, plus the fake kernels registered from Python."""
+    import torch
+
+    from kv_skill_v2_amd import torch_ops
+    assert torch_ops.TORCH_OPS_PATH.exists()
+    for name in ("route_topk", "library_read", "route_read", "paged_decode_joint"):
+        op = getattr(torch.ops.xenc, name).default
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "CUDA"), name
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "Meta"), name
+    schema = str(torch.ops.xenc.route_read.default._schema)
+    assert "Tensor(a!) workspace" in schema and schema.endswith("-> (Tensor, Tensor, Tensor, Tensor)")
