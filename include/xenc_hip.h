@@ -82,15 +82,12 @@ int xenc_route_topk_rows(const float* q, long long ldq, int M, int d, const floa
  * over the valid slots n of the routed chunks c_j = idx[m,j] (entries < 0 are skipped).
  * Each slot row is read from HBM once for both the score and the value.  Page slots are
  * split into nsplit ranges of ceil(slots_per_page/nsplit) slots (nsplit in 1..64).
- * r is fp32 [M, ldr].  The partials of a query are merged in a fixed order, so results are
- * deterministic: launches of >= 256 (query, page, split) units merge in a second kernel, smaller
- * ones in the last workgroup of each query (same merge, bit-identical results).
+ * r is fp32 [M, ldr].  The partials of a query are merged in a fixed order by a second kernel
+ * of the same call, so results are deterministic.
  * Workspace: xenc_decode_workspace_bytes(max_rows, kk, nsplit, d) bytes for calls of up to
- * max_rows query rows (pass the same max_rows to every call); its first max_rows ints are
- * arrival counters that must be zero before the first call (xenc_decode_workspace_init does that
- * with a kernel, no memset).  Every call leaves them zero again, so a workspace is initialised
- * once and reused by calls of any M <= max_rows.  Calls that share a workspace must not overlap
- * (same stream, or ordered).
+ * max_rows query rows (pass the same max_rows to every call); set it up once with
+ * xenc_decode_workspace_init (a kernel, no memset), then reuse it for calls of any
+ * M <= max_rows.  Calls that share a workspace must not overlap (same stream, or ordered).
  * Replaces the read of LibraryInjector._branch (xenc/injector.py:236-265) when the routed
  * chunks are known: equal to reading every chunk with w = 0 off the top-k.
  */
@@ -127,13 +124,13 @@ int xenc_route_read_decode(const float* q, long long ldq, int M, int d, const fl
 
 /*
  * Allocation-free variant of xenc_library_read_decode: the same read, the same arguments without
- * the workspace.  Its partials, page order and arrival counters live in a file-scope device array
+ * the workspace.  Its partials and page order live in a file-scope device array
  * of XENC_DECODE_SCRATCH_BYTES bytes (64 MiB) that each GPU the library runs on holds until the
  * process ends; calls of up to XENC_DECODE_SCRATCH_ROWS query rows whose workspace
  * (xenc_decode_workspace_bytes(XENC_DECODE_SCRATCH_ROWS, kk, nsplit, d) for those rows) fits in
  * it are accepted, larger ones return XENC_ESCRATCH.  No hipMalloc, hipFree or allocating
  * library call is made.  The first call on a device (with that device current) looks the array
- * up and zeroes its counters with a kernel; make it before capturing a graph.  Every call on one
+ * up and sets it up with a kernel; make it before capturing a graph.  Every call on one
  * GPU shares that GPU's array: calls that overlap on one GPU (different streams, not ordered)
  * race and give wrong results.
  * No counterpart in the reference: it is for callers that cannot allocate device memory (code

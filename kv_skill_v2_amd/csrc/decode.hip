@@ -23,10 +23,11 @@
 //
 // Merge (merge_query): the k*nsplit partials of a query are combined by log-sum-exp, chunk j
 // scaled by w[j] / l_j, and summed in (j, s) order — a fixed order, so results are
-// deterministic.  Launches of >= kTwoPassUnits workgroups run it as a second kernel, one
-// workgroup per query (measured 3.5 % faster on B = 64: no release / acquire per workgroup and
-// no merge on the first kernel's critical path).  Smaller launches publish each partial and
-// increment the query's counter; the last workgroup of the query merges and re-arms the counter.
+// deterministic.  It runs as a second kernel (merge_kernel), launched after the read: one
+// workgroup per query, or for few queries several per query, each summing a slice of the
+// columns.  No workgroup of the read waits on a release / acquire or merges on its critical
+// path (measured faster than merging in the last-arriving workgroup of each query, for many
+// rows and for one).
 #include <algorithm>
 #include <mutex>
 
@@ -36,8 +37,8 @@
 // large two-pass launches take NW_STREAM waves (the kernel holds 179 VGPRs, two waves per SIMD,
 // so two 4-wave workgroups share a CU and one's prologue / tail overlaps the other's streaming:
 // B = 64 batched decode 0.197 -> 0.188 ms per step; 64 rows over 8 shared libraries, page-grouped:
-// 0.258 -> 0.252 ms per step); small launches (the in-kernel merge) keep NW_WIDE (one row x 4
-// pages: 36.5 against 38.4 us).
+// 0.258 -> 0.252 ms per step); small launches (fewer than 256 workgroups) keep NW_WIDE (one row
+// x 4 pages: 36.5 against 38.4 us).
 #ifndef XENC_DECODE_NW_STREAM
 #define XENC_DECODE_NW_STREAM 4
 #endif
@@ -76,7 +77,7 @@ constexpr int kLoadShared = 0;
 constexpr int kOrderShared = 1 << 30;
 
 struct DecodeWorkspace {
-  int* counters;    // [max_rows] arrivals per query (0 between calls; in-kernel merge only)
+  int* counters;    // [max_rows] reserved: zeroed once by xenc_decode_workspace_init, unused
   int* order;       // [M * kk]   (row, routed chunk) entries ranked by page (page-grouped runs),
                     //            kOrderShared set when more than one entry reads the page
   float2* part_ml;  // [units]    (max in log2 units, sum) per partial; sum 0 = empty
@@ -111,11 +112,11 @@ struct SelectLds {
   float sel[kWave];
 };
 
-// Dynamic LDS of the read kernel, in floats: the wave-merge tree [NW/2][d], reused by the
+// Dynamic LDS of the read kernel, in floats: the wave merge's rows [NW][d], reused by the
 // merge's per-partial lists [4 * kk * nsplit], rounded up to 16 bytes.  Launches with the
 // routing folded in add one SelectLds per wave after it; other launches allocate none.
 __host__ __device__ inline size_t read_red_floats(int nw, int d, int kk, int nsplit) {
-  const size_t tree = (size_t)(nw / 2 > 1 ? nw / 2 : 1) * d;
+  const size_t tree = (size_t)nw * d;
   const size_t lists = (size_t)4 * kk * nsplit;
   return ((tree > lists ? tree : lists) + 3) & ~size_t(3);
 }
@@ -142,7 +143,7 @@ __device__ __forceinline__ void select_row(const RouteFuse& rf, const float* dro
 // flight, so the result is independent of arrival order.
 __device__ void merge_query(const DecodeWorkspace& ws, int m, const int* __restrict__ idx,
                             const float* __restrict__ w_sel, int kk, int nsplit, int d, int softmax,
-                            float* __restrict__ r, long long ldr, float* lds) {
+                            float* __restrict__ r, long long ldr, float* lds, int dlo, int dhi) {
   const int nu = kk * nsplit;
   float* pm = lds;                                        // [nu] partial max (log2 units)
   float* pl = lds + nu;                                   // [nu] partial sum (0 = empty)
@@ -198,7 +199,7 @@ __device__ void merge_query(const DecodeWorkspace& ws, int m, const int* __restr
   __syncthreads();
   const int n = nlive;
   constexpr int kInFlight = 8;
-  for (int i = threadIdx.x * 4; i < d; i += blockDim.x * 4) {
+  for (int i = dlo + threadIdx.x * 4; i < dhi; i += blockDim.x * 4) {
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     int t = 0;
     for (; t + kInFlight <= n; t += kInFlight) {
@@ -329,12 +330,11 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
     const int* __restrict__ chunk_nvalid, const int* __restrict__ chunk_ptr,
     const int* __restrict__ q_group, int G, int* idx, float* w_sel, int kk, int nsplit,
     int split_slots, float scale2, int softmax, float* __restrict__ r, long long ldr,
-    DecodeWorkspace ws, int fused_merge, int grouped, RouteFuse rf) {
+    DecodeWorkspace ws, int grouped, RouteFuse rf) {
   // idx / w_sel: read (routed in advance) or written by split 0 of each slot (routing folded in),
   // so neither is declared read-only.
-  extern __shared__ __align__(16) float red[];  // [NW/2][d] wave-merge tree; reused by the merge
+  extern __shared__ __align__(16) float red[];  // [NW][d] wave-merge rows; reused by the merge
   __shared__ float wml[NW][2];
-  __shared__ int is_last;
   // One SelectLds per wave after the tree, allocated only when the routing is folded in.
   SelectLds* const sl = reinterpret_cast<SelectLds*>(red + read_red_floats(NW, d, kk, nsplit));
 
@@ -367,9 +367,22 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
     const float* drow = rf.dots + (long long)m * rf.ldw;
     if (rf.S) {
       __shared__ float row_dots[kDotsInRead];
-      for (int c = wv; c < C; c += NW) {
-        const float x = route_dot_wave<2 * CB>(q + (long long)m * ldq, rf.S + (long long)(cbeg + c) * d, d, lane);
-        if (lane == 0) row_dots[c] = x;
+      // Wave w forms the dots of chunks w, w + NW, ...: two at a time, so both summary rows load
+      // in one round trip (each dot summed exactly as route_dot_wave sums it).
+      const float* qrow = q + (long long)m * ldq;
+      for (int c = wv; c < C; c += 2 * NW) {
+        const int c2 = c + NW;
+        if (c2 < C) {
+          const float2 x = route_dot2_wave<2 * CB>(qrow, rf.S + (long long)(cbeg + c) * d,
+                                                   rf.S + (long long)(cbeg + c2) * d, d, lane);
+          if (lane == 0) {
+            row_dots[c] = x.x;
+            row_dots[c2] = x.y;
+          }
+        } else {
+          const float x = route_dot_wave<2 * CB>(qrow, rf.S + (long long)(cbeg + c) * d, d, lane);
+          if (lane == 0) row_dots[c] = x;
+        }
       }
       __syncthreads();
       drow = row_dots;
@@ -457,9 +470,10 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
       }
     }
 
-    // Merge the NW waves of this workgroup: rescale each wave to the common max, then a tree
-    // over LDS (round h: waves h..2h-1 hand their sums to waves 0..h-1) — a fixed order, so
-    // deterministic — and wave 0 writes the workgroup's partial from its registers.
+    // Merge the NW waves of this workgroup: rescale each wave to the common max, every wave puts
+    // its sums in its own LDS row, and each thread adds up its columns over the NW rows in a fixed
+    // pairwise order (round h: row i += row i + h, i < h; the order a tree over the waves would
+    // use), so the result is deterministic.  One LDS exchange instead of log2(NW) rounds.
     if (lane == 0) {
       wml[wv][0] = mrun;
       wml[wv][1] = lrun;
@@ -470,53 +484,37 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
     for (int w = 0; w < NW; ++w)
       if (wml[w][1] > 0.f) mall = fmaxf(mall, wml[w][0]);
     const float wscale = lrun > 0.f ? (softmax ? __builtin_amdgcn_exp2f(mrun - mall) : 1.f) : 0.f;
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[cb][i] *= wscale;
-#pragma unroll
-    for (int h = NW / 2; h >= 1; h /= 2) {
-      if (wv >= h && wv < 2 * h) {
-        float* dst = red + (wv - h) * d;
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          const int d0 = (cb * kWave + lane) * 8;
-          if (d0 < d) {
-            *reinterpret_cast<float4*>(dst + d0) =
-                make_float4(acc[cb][0], acc[cb][1], acc[cb][2], acc[cb][3]);
-            *reinterpret_cast<float4*>(dst + d0 + 4) =
-                make_float4(acc[cb][4], acc[cb][5], acc[cb][6], acc[cb][7]);
-          }
-        }
-      }
-      __syncthreads();
-      if (wv < h) {
-        const float* src = red + wv * d;
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          const int d0 = (cb * kWave + lane) * 8;
-          if (d0 < d) {
-            const float4 a = *reinterpret_cast<const float4*>(src + d0);
-            const float4 b = *reinterpret_cast<const float4*>(src + d0 + 4);
-            acc[cb][0] += a.x; acc[cb][1] += a.y; acc[cb][2] += a.z; acc[cb][3] += a.w;
-            acc[cb][4] += b.x; acc[cb][5] += b.y; acc[cb][6] += b.z; acc[cb][7] += b.w;
-          }
-        }
-      }
-      __syncthreads();
-    }
-    if (wv == 0) {
-      float* out = ws.part_acc + (long long)unit * d;
+    {
+      float* dst = red + wv * d;
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         const int d0 = (cb * kWave + lane) * 8;
         if (d0 < d) {
-          *reinterpret_cast<float4*>(out + d0) =
-              make_float4(acc[cb][0], acc[cb][1], acc[cb][2], acc[cb][3]);
-          *reinterpret_cast<float4*>(out + d0 + 4) =
-              make_float4(acc[cb][4], acc[cb][5], acc[cb][6], acc[cb][7]);
+          *reinterpret_cast<float4*>(dst + d0) =
+              make_float4(acc[cb][0] * wscale, acc[cb][1] * wscale, acc[cb][2] * wscale, acc[cb][3] * wscale);
+          *reinterpret_cast<float4*>(dst + d0 + 4) =
+              make_float4(acc[cb][4] * wscale, acc[cb][5] * wscale, acc[cb][6] * wscale, acc[cb][7] * wscale);
         }
       }
+    }
+    __syncthreads();
+    // Thread t sums columns 4t, 4t + 4 NW kWave, ... and stores them as the partial
+    // (merge_kernel reads it after this kernel).
+    float* const out = ws.part_acc + (long long)unit * d;
+    for (int i = threadIdx.x * 4; i < d; i += NW * kWave * 4) {
+      float4 v[NW];
+#pragma unroll
+      for (int w = 0; w < NW; ++w) v[w] = *reinterpret_cast<const float4*>(red + w * d + i);
+#pragma unroll
+      for (int h = NW / 2; h >= 1; h /= 2)
+#pragma unroll
+        for (int w = 0; w < h; ++w) {
+          v[w].x += v[w + h].x;
+          v[w].y += v[w + h].y;
+          v[w].z += v[w + h].z;
+          v[w].w += v[w + h].w;
+        }
+      *reinterpret_cast<float4*>(out + i) = v[0];
     }
     if (threadIdx.x == 0) {
       float lsum = 0.f;
@@ -530,26 +528,9 @@ __global__ __launch_bounds__(NW* kWave, XENC_DECODE_MIN_WAVES) void decode_read_
     ws.part_ml[unit] = make_float2(-INFINITY, 0.f);
   }
 
-  // Large launches merge in a second kernel (merge_kernel): the stream order publishes the
-  // partials, and no workgroup waits on a release / acquire or merges on the critical path.
-  if (!fused_merge) return;
-  // Publish this partial device-wide, then count it; the last workgroup of query m merges.
-  // Every store of the partial comes from wave 0 (thread 0's wave): its agent-scope release
-  // (L2 write-back, then a wait for the wave's own stores) covers them, one write-back per
-  // workgroup.  The barrier does not wait for other waves' stores, so no other wave may write
-  // any part of the partial.  Only the last workgroup pays the acquire.
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const int prev = __hip_atomic_fetch_add(&ws.counters[m], 1, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-    is_last = prev == kk * nsplit - 1;
-    if (is_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  }
-  __syncthreads();
-  if (!is_last) return;
-  merge_query(ws, m, idx, w_sel, kk, nsplit, d, softmax, r, ldr, red);
-  if (threadIdx.x == 0) atomicExch(&ws.counters[m], 0);  // re-arm for the next call
+  // The partials are merged by merge_kernel, launched after this kernel: the stream order
+  // publishes them, and no workgroup waits on a release / acquire or merges on the critical
+  // path.
 }
 
 // Page-grouped runs: entry i = (row i / kk, routed chunk i % kk) of the n = M * kk entries gets
@@ -596,7 +577,11 @@ __global__ __launch_bounds__(512) void merge_kernel(DecodeWorkspace ws, const in
                                                     int nsplit, int d, int softmax,
                                                     float* __restrict__ r, long long ldr) {
   extern __shared__ float lds[];
-  merge_query(ws, blockIdx.x, idx, w_sel, kk, nsplit, d, softmax, r, ldr, lds);
+  // gridDim.y workgroups share a query row, each summing one slice of its d columns (slice
+  // width `slice`, a multiple of 4): for few rows the partials are read by many CUs at once.
+  const int slice = ((d + (int)gridDim.y - 1) / (int)gridDim.y + 3) & ~3;
+  const int dlo = (int)blockIdx.y * slice;
+  merge_query(ws, blockIdx.x, idx, w_sel, kk, nsplit, d, softmax, r, ldr, lds, dlo, min(d, dlo + slice));
 }
 
 __global__ void fill_zero_kernel(int* p, int n) {
@@ -609,8 +594,8 @@ static size_t host_align256(size_t x) { return (x + 255) & ~size_t(255); }
 // (m, l) per partial | acc per partial], each region 256-B aligned.  The second region holds the
 // page order of page-grouped runs, or the q . S dots when the routing is folded into the read
 // (never both in one call).
-// The counter region depends only on the capacity max_rows, never on the call's row count, so
-// counters zeroed once stay in place (and zero) whatever sizes later calls use.
+// The first region (max_rows ints, zeroed once by xenc_decode_workspace_init) is kept so that the
+// layout and the set-up call stay as callers know them; the read no longer counts arrivals in it.
 static DecodeWorkspace carve(void* base, int max_rows, int M, int kk, int nsplit) {
   const size_t units = (size_t)M * kk * nsplit;
   char* p = static_cast<char*>(base);
@@ -631,18 +616,27 @@ static void launch_read(dim3 grid, size_t lds, hipStream_t st, const float* q, l
                         const int* chunk_page, const int* chunk_nvalid, const int* chunk_ptr,
                         const int* q_group, int G, const int* idx, const float* w_sel, int kk,
                         int nsplit, int split_slots, float scale2, int softmax, float* r,
-                        long long ldr, const DecodeWorkspace& ws, int fused_merge, int grouped,
-                        const RouteFuse& rf) {
+                        long long ldr, const DecodeWorkspace& ws, int grouped, const RouteFuse& rf) {
   constexpr int SPT = CB <= 4 ? XENC_DECODE_SPT : (CB == 5 ? XENC_DECODE_SPT_WIDE : 1);
   hipLaunchKernelGGL((decode_read_kernel<CB, SPT, NW>), grid, dim3(NW * kWave), lds, st, q, ldq,
                      d, pages, page_stride, spp, chunk_page, chunk_nvalid, chunk_ptr, q_group, G,
                      const_cast<int*>(idx), const_cast<float*>(w_sel), kk, nsplit, split_slots, scale2,
-                     softmax, r, ldr, ws, fused_merge, grouped, rf);
+                     softmax, r, ldr, ws, grouped, rf);
 }
 
-// Launches of at least this many workgroups merge in a second kernel; smaller ones (few query
-// rows, latency-bound) merge in the last workgroup of each row and save the launch.
-constexpr long long kTwoPassUnits = 256;
+// Launches of fewer workgroups than this (few query rows, latency-bound) use 8-wave workgroups,
+// larger ones 4-wave workgroups (two per CU).
+constexpr long long kWideUnits = 256;
+
+// Workgroups of merge_kernel per query row: for few rows the row's columns are split so that
+// about 8 workgroups read the partials side by side (slices of at least 256 columns).  The
+// single-sequence decode (1 row, 4 pages x 8 splits) measured 16.6 us per step this way, 17.5 us
+// with the merge done by the last-arriving workgroup of the read (one CU reading 32 partials
+// behind a device-scope release and an arrival count).
+static int merge_slices(int M, int d) {
+  const int want = std::max(1, 8 / std::max(M, 1));
+  return std::max(1, std::min(want, d / 256));
+}
 
 }  // namespace xenc
 
@@ -673,15 +667,14 @@ extern "C" int xenc_decode_workspace_init(void* workspace, size_t workspace_byte
 
 // Workgroup size and LDS bytes (dynamic, then the whole workgroup's) of a read launch.
 static int read_waves(long long units) {
-  return units < kTwoPassUnits ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
+  return units < kWideUnits ? XENC_DECODE_NW_WIDE : XENC_DECODE_NW_STREAM;
 }
 static size_t read_dynamic_lds(int nw, int d, int kk, int nsplit, bool fold) {
   return read_red_floats(nw, d, kk, nsplit) * sizeof(float) + (fold ? (size_t)nw * sizeof(SelectLds) : 0);
 }
 static size_t read_total_lds(int nw, int d, int kk, int nsplit, bool fold) {
-  // static part: wml[NW][2], is_last and row_dots[kDotsInRead]
-  return read_dynamic_lds(nw, d, kk, nsplit, fold) + (size_t)nw * 2 * sizeof(float) + sizeof(int) +
-         kDotsInRead * sizeof(float);
+  // static part: wml[NW][2] and row_dots[kDotsInRead]
+  return read_dynamic_lds(nw, d, kk, nsplit, fold) + (size_t)nw * 2 * sizeof(float) + kDotsInRead * sizeof(float);
 }
 
 // Every argument check of the decode read, done before anything is launched (the routing
@@ -725,7 +718,6 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
                                 workspace_bytes, max_rows, short_code, fold);
   if (vrc != XENC_OK || M == 0) return vrc;
   const long long units = (long long)M * kk * nsplit;
-  const int fused = units < kTwoPassUnits ? 1 : 0;
   // Page-grouped runs when rows share libraries and there are enough entries to matter.
   const long long entries = (long long)M * kk;
   const int grouped = (!fold && M > G && entries >= 128 && entries <= kOrderMax) ? 1 : 0;
@@ -749,12 +741,12 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
       launch_read<N, XENC_DECODE_NW_STREAM>(grid, lds, st, q, ldq, d, pg, page_stride,            \
                                             slots_per_page, chunk_page, chunk_nvalid, chunk_ptr,  \
                                             q_group, G, idx, w_sel, kk, nsplit, split_slots,      \
-                                            scale2, softmax, r, ldr, ws, fused, grouped, rf);     \
+                                            scale2, softmax, r, ldr, ws, grouped, rf);     \
     else                                                                                          \
       launch_read<N, XENC_DECODE_NW_WIDE>(grid, lds, st, q, ldq, d, pg, page_stride,              \
                                           slots_per_page, chunk_page, chunk_nvalid, chunk_ptr,    \
                                           q_group, G, idx, w_sel, kk, nsplit, split_slots,        \
-                                          scale2, softmax, r, ldr, ws, fused, grouped, rf);       \
+                                          scale2, softmax, r, ldr, ws, grouped, rf);       \
     break;
     XENC_CASE(1) XENC_CASE(2) XENC_CASE(3) XENC_CASE(4)
     XENC_CASE(5) XENC_CASE(6) XENC_CASE(7) XENC_CASE(8)
@@ -762,9 +754,8 @@ static int read_decode(const float* q, long long ldq, int M, int d, const void* 
     default:
       return XENC_EINVAL;
   }
-  if (!fused)
-    hipLaunchKernelGGL(merge_kernel, dim3(M), dim3(512), (size_t)4 * kk * nsplit * sizeof(float), st,
-                       ws, idx, w_sel, kk, nsplit, d, softmax, r, ldr);
+  hipLaunchKernelGGL(merge_kernel, dim3(M, merge_slices(M, d)), dim3(512), (size_t)4 * kk * nsplit * sizeof(float),
+                     st, ws, idx, w_sel, kk, nsplit, d, softmax, r, ldr);
   return check_launch();
 }
 
@@ -787,8 +778,8 @@ extern "C" int xenc_library_read_decode(const float* q, long long ldq, int M, in
 // its own copy (XENC_DECODE_SCRATCH_BYTES) until the process ends.  In host code `scratch` is
 // only a stand-in for the symbol; its device address is looked up once per device with
 // hipGetSymbolAddress (with that device current) and only that address reaches kernels.
-// The counter region is sized for kScratchRows rows and zeroed by a kernel the first time a
-// device is used; every call leaves it zero again (the merging workgroup re-arms its row).
+// The workspace layout is carved for kScratchRows rows; its first (reserved) region is zeroed by
+// a kernel the first time a device is used, as xenc_decode_workspace_init does for a caller's.
 static __device__ __align__(256) unsigned char scratch[XENC_DECODE_SCRATCH_BYTES];
 constexpr int kScratchRows = XENC_DECODE_SCRATCH_ROWS;
 constexpr int kMaxDevices = 64;

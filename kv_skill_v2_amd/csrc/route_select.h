@@ -104,6 +104,36 @@ __device__ __forceinline__ float route_dot_wave(const float* __restrict__ qrow,
   return wave_sum(a);
 }
 
+// Two dots of one query row, q . s_a and q . s_b, with q loaded once and both summary rows in
+// flight together; each is summed exactly as route_dot_wave sums it (bit-identical results).
+template <int CB4>
+__device__ __forceinline__ float2 route_dot2_wave(const float* __restrict__ qrow, const float* __restrict__ sa,
+                                                  const float* __restrict__ sb, int d, int lane) {
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  float4 qv[CB4];
+  f32x4 va[CB4], vb[CB4];
+#pragma unroll
+  for (int cb = 0; cb < CB4; ++cb) {
+    const int i = (cb * kWave + lane) * 4;
+    qv[cb] = i < d ? *reinterpret_cast<const float4*>(qrow + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    va[cb] = *reinterpret_cast<const f32x4*>(sa + min(i, d - 4));
+    vb[cb] = *reinterpret_cast<const f32x4*>(sb + min(i, d - 4));
+  }
+  float a = 0.f, b = 0.f;
+#pragma unroll
+  for (int cb = 0; cb < CB4; ++cb) {
+    a = fmaf(qv[cb].x, va[cb].x, a);
+    a = fmaf(qv[cb].y, va[cb].y, a);
+    a = fmaf(qv[cb].z, va[cb].z, a);
+    a = fmaf(qv[cb].w, va[cb].w, a);
+    b = fmaf(qv[cb].x, vb[cb].x, b);
+    b = fmaf(qv[cb].y, vb[cb].y, b);
+    b = fmaf(qv[cb].z, vb[cb].z, b);
+    b = fmaf(qv[cb].w, vb[cb].w, b);
+  }
+  return make_float2(wave_sum(a), wave_sum(b));
+}
+
 // q . S dots of every (row, chunk) pair into w_dense [M, ldw] (one wave per dot; route.hip).
 int launch_route_dots(const float* q, long long ldq, int M, int d, const float* S, const int* chunk_ptr,
                       const int* q_group, int G, float* w_dense, int ldw, hipStream_t st);
