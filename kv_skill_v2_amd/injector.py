@@ -297,9 +297,12 @@ class LibraryInjector(XEncInjector):
         get r = 0 (their routed-chunk lists are emptied on the device)."""
         lead, d = q.shape[:-1], q.shape[-1]
         rows = q.reshape(-1, d)
+        if keep is None or (torch.is_grad_enabled() and rows.requires_grad):
+            # (with autograd every row is read: the selector's weight zeroes the left-out ones)
+            r, w = ops.branch_read(rows, pool, self.top_k, self.read_temp, self.route_temp, self.read_softmax)
+            return r.view(*lead, -1), w.view(*lead, -1)
         w, idx, w_sel = ops.route_rows(rows, pool, self.top_k, self.route_temp)
-        if keep is not None:
-            idx = torch.where(keep.reshape(-1, 1), idx, torch.full_like(idx, -1))
+        idx = torch.where(keep.reshape(-1, 1), idx, torch.full_like(idx, -1))
         r = ops.read_rows(rows, w, idx, w_sel, pool, self.read_temp, self.read_softmax)
         return r.view(*lead, -1), w.view(*lead, -1)
 

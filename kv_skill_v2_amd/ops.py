@@ -889,6 +889,20 @@ def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int 
     routing pass also writes the fp16 rows the read takes, so q is read from HBM once."""
     if not prefill_ok(lib_) and not _mfma_pages_ok(lib_):
         lib_.check_prefill()
+    if prefill_ok(lib_) and plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
+        # routing and read as one autograd node (xenc::library_read_routed): the backward adds the
+        # routing term into the read's dq in place
+        q = _query(q, lib_.d)
+        if q.shape[0] != plan.M:
+            raise ValueError(f"q must have {plan.M} rows")
+        fk, fv, fvs, fkr, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles, readout_tiles, n_score, \
+            n_readout, slots = _prefill_operands(lib_, plan)
+        r, w, _, _, _ = torch.ops.xenc.library_read_routed(
+            q, lib_.S, chunk_ptr, row_ptr, plan.logit_tiles, plan.route_tiles, plan.n_logit, plan.n_route,
+            int(top_k), float(route_temp), lib_.cmax, lib_.kept(int(top_k)), fk, fv, fvs, fkr, chunk_page,
+            chunk_nvalid, score_tiles, readout_tiles, n_score, n_readout, slots, float(read_temp),
+            bool(read_softmax), min(lib_.n_chunks) != lib_.cmax)
+        return r, w
     w, _, _, qh = route_differentiable(q, lib_, plan, int(top_k), float(route_temp), emit_f16=True)
     if prefill_ok(lib_):
         r, _ = prefill_forward(q, w, lib_, plan, float(read_temp), bool(read_softmax), qh=qh)
@@ -1093,7 +1107,15 @@ def read_rows(q: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, w_sel: torch.
 
 def branch_read(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, read_temp: float = 12.0,
                 route_temp: float = 10.0, read_softmax: bool = True):
-    """(r [M, d_valid], w [M, C]): route_rows + read_rows."""
+    """(r [M, d_valid], w [M, C]): route_rows + read_rows; with autograd over many rows of a pool
+    the MFMA read takes directly, the two as one operator (library_read)."""
+    _single(lib_)
+    M = q.shape[0]
+    if (torch.is_grad_enabled() and q.requires_grad and prefill_ok(lib_) and M >= ROUTE_ROWS_MIN
+            and lib_.cmax <= 1024):
+        r, w = library_read(_pad_rows(q, lib_), lib_, lib_.plan([M]), int(top_k), float(read_temp),
+                            float(route_temp), bool(read_softmax))
+        return (r[:, :lib_.d_valid] if lib_.d != lib_.d_valid else r), w
     w, idx, wsel = route_rows(q, lib_, top_k, route_temp)
     return read_rows(q, w, idx, wsel, lib_, read_temp, read_softmax), w
 

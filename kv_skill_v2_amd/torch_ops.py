@@ -20,6 +20,8 @@ dispatcher, FakeTensor tracing and torch.compile see ordinary operators:
                                  and w (its backward is the next operator plus the route term)
     xenc::library_prefill_bwd_dq (dq through the read, gamma = dL/dw) from the upstream gradient
     xenc::route_backward_        dq += the routing term, in place
+    xenc::library_read_routed    route_rows + library_prefill_fwd as one autograd node (its
+                                 backward adds the routing term into the read's dq in place)
     xenc::paged_decode_joint     DecodeReader's joint read (xenc/d23_read_kernels.py:145-160) into
                                  a caller-owned output; writes its workspace
 
@@ -266,6 +268,68 @@ def _prefill_backward(ctx, dr, _dp):
 library_prefill_fwd.register_autograd(_prefill_backward, setup_context=_prefill_setup)
 
 
+# ----------------------------------------------------------------------------- routing + MFMA read, one node
+@custom_op("xenc::library_read_routed", mutates_args=())
+def library_read_routed(q: Tensor, S: Tensor, chunk_ptr: Tensor, row_ptr: Tensor, logit_tiles: Tensor,
+                        route_tiles: Tensor, n_logit: int, n_route: int, top_k: int, route_temp: float, cmax: int,
+                        kk: int, frag_k_scores: Tensor, frag_v_readout: Tensor, frag_v_scores: Tensor,
+                        frag_k_readout: Tensor, chunk_page: Tensor, chunk_nvalid: Tensor, score_tiles: Tensor,
+                        readout_tiles: Tensor, n_score: int, n_readout: int, slots: int, read_temp: float,
+                        softmax: bool, ragged: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
+    """(r [M, d], w [M, cmax], idx, w_sel, p): xenc::route_rows (which also writes q as fp16) then
+    xenc::library_prefill_fwd, as ONE autograd node.  Its backward writes dq once: the read's dq
+    (scores_kernel<1|3> + readout_kernel), then the routing term added in place
+    (route_backward_kernel) with dL/dw = gamma + the gradient that reaches w from elsewhere (the
+    injector's route_terms), so no zeroed gradient buffer and no gradient sum are needed."""
+    w, idx, wsel, qh = torch.ops.xenc.route_rows(q, S, chunk_ptr, row_ptr, logit_tiles, route_tiles, n_logit,
+                                                  n_route, top_k, route_temp, cmax, kk, True)
+    r, p = torch.ops.xenc.library_prefill_fwd(q, qh, w, frag_k_scores, frag_v_readout, frag_v_scores,
+                                              frag_k_readout, chunk_ptr, chunk_page, chunk_nvalid, row_ptr,
+                                              score_tiles, readout_tiles, n_score, n_readout, slots, read_temp,
+                                              softmax, ragged)
+    return r, w, idx, wsel, p
+
+
+@library_read_routed.register_fake
+def _(q, S, chunk_ptr, row_ptr, logit_tiles, route_tiles, n_logit, n_route, top_k, route_temp, cmax, kk,
+      frag_k_scores, frag_v_readout, frag_v_scores, frag_k_readout, chunk_page, chunk_nvalid, score_tiles,
+      readout_tiles, n_score, n_readout, slots, read_temp, softmax, ragged):
+    M, d = q.shape
+    return (q.new_empty(M, d), q.new_empty(M, cmax), q.new_empty(M, kk, dtype=torch.int32), q.new_empty(M, kk),
+            q.new_empty(cmax * slots // 8, M, 8, dtype=torch.float16))
+
+
+def _routed_setup(ctx, inputs, output):
+    (q, S, chunk_ptr, row_ptr, _lt, route_tiles, _nl, n_route, _tk, route_temp, _cmax, _kk, _fks, _fvr, fvs, fkr,
+     chunk_page, chunk_nvalid, score_tiles, readout_tiles, n_score, n_readout, slots, read_temp, softmax,
+     _ragged) = inputs
+    _, w, _, _, p = output
+    ctx.save_for_backward(w, p, fvs, fkr, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles, readout_tiles,
+                          S, route_tiles)
+    ctx.sizes = (n_score, n_readout, slots, read_temp, softmax)
+    ctx.route = (n_route, route_temp)
+    ctx.d = q.shape[1]
+    ctx.mark_non_differentiable(output[2], output[3], output[4])
+
+
+def _routed_backward(ctx, dr, dw, _didx, _dwsel, _dp):
+    w, p, fvs, fkr, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles, readout_tiles, S, route_tiles = \
+        ctx.saved_tensors
+    if dr is None:
+        dq = torch.zeros(w.shape[0], ctx.d, dtype=torch.float32, device=w.device)
+        gamma = torch.zeros_like(w)
+    else:
+        dq, gamma = torch.ops.xenc.library_prefill_bwd_dq(dr.contiguous(), w, p, fvs, fkr, chunk_ptr, chunk_page,
+                                                           chunk_nvalid, row_ptr, score_tiles, readout_tiles,
+                                                           *ctx.sizes)
+    torch.ops.xenc.route_backward_(dq, w, gamma, None if dw is None else dw.contiguous(), S, chunk_ptr, row_ptr,
+                                   route_tiles, *ctx.route)
+    return (dq,) + (None,) * 25
+
+
+library_read_routed.register_autograd(_routed_backward, setup_context=_routed_setup)
+
+
 # ----------------------------------------------------------------------------- op B
 _JOINT_DTYPES = {torch.float16: 0, torch.bfloat16: 1}
 
@@ -276,4 +340,4 @@ def _(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale, nsplit
 
 
 __all__ = ["route_rows", "route_backward_", "library_prefill_lse", "library_prefill_fwd",
-           "library_prefill_bwd_dq", "kept_width", "TORCH_OPS_PATH"]
+           "library_prefill_bwd_dq", "library_read_routed", "kept_width", "TORCH_OPS_PATH"]

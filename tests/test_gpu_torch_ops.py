@@ -74,6 +74,22 @@ def test_opcheck_prefill_and_routing_with_autograd(dev):
              plan.n_route, 10.0)
     torch.library.opcheck(torch.ops.xenc.route_backward_.default, gargs,
                           test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
+    # routing + read as one autograd node: schema, fakes, registered autograd ...
+    cargs = (q, lib.S, lib.chunk_ptr, plan.row_ptr, plan.logit_tiles, plan.route_tiles, plan.n_logit, plan.n_route,
+             2, 10.0, lib.cmax, kept_width(2, lib.cmax), *operands[:4], lib.chunk_page, lib.chunk_nvalid,
+             plan.score_tiles, plan.readout_tiles, plan.n_score, plan.n_readout, lib.slots_per_page, 12.0, True, True)
+    torch.library.opcheck(torch.ops.xenc.library_read_routed.default, cargs, test_utils=CHECKS)
+    # ... and the same values and gradients as the two operators, bit for bit, for a loss on both
+    # r and w (the gradient reaching w from elsewhere enters the routing term in place)
+    qa = q.detach().clone().requires_grad_(True)
+    qb = q.detach().clone().requires_grad_(True)
+    ra, wa, *_ = torch.ops.xenc.library_read_routed(qa, *cargs[1:])
+    ((ra * g).sum() + 3.0 * (wa * wa).sum()).backward()
+    wb, _, _, qhb = torch.ops.xenc.route_rows(qb, *rargs[1:8], 2, 10.0, lib.cmax, kept_width(2, lib.cmax), True)
+    rb, _ = torch.ops.xenc.library_prefill_fwd(qb, qhb, wb, *operands, 12.0, True, True)
+    ((rb * g).sum() + 3.0 * (wb * wb).sum()).backward()
+    assert torch.equal(ra, rb) and torch.equal(wa, wb)
+    assert torch.equal(qa.grad, qb.grad), float((qa.grad - qb.grad).abs().max())
     # autograd through both operators equals the oracle's closed-form dq
     r, w2 = ops.library_read(q, lib, plan)
     (r * g).sum().backward()
