@@ -320,9 +320,7 @@ def measure_prefill(steps: int, warmup: int, cpu_sample: int) -> dict:
         return w, r, p
 
     def bwd(w, p):
-        dq, gamma = ops.prefill_backward(g_up, w, p, lib, plan)
-        ops.route_backward(w, gamma, lib, plan, 10.0, dq)
-        return dq
+        return ops.prefill_backward_routed(g_up, w, p, lib, plan, route_temp=10.0)
 
     def step():
         w, _, p = fwd()

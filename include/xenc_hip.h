@@ -171,6 +171,11 @@ int xenc_library_read_decode_noalloc(const float* q, long long ldq, int M, int d
  *     is given (forward read) else 1 (backward: out = dq through the read).
  * xenc_route_backward: dq[t] += route_temp * sum_c w (dw - sum_c' w dw) S[c],
  *     dw = dw_read (+ dw_ext when not NULL): the gradient through routing.
+ * xenc_prefill_readout_routed: the backward's readout with the routing term in its epilogue:
+ *     dq[t] = sum_{c,n} ds[t, c, n] K[c, n] + sum_c dl[t, c] S[c], where
+ *     dl[t, c] = route_temp * w (dw - sum_c' w dw) (dw = dw_read (+ dw_ext)) is first written to
+ *     the caller's dl [a_rows, ldl >= cmax] fp32 buffer.  dq is written, not accumulated: one
+ *     pass over dq where xenc_prefill_readout + xenc_route_backward take three.
  * Replace the forward and the autograd backward of LibraryInjector.route + _branch
  * (xenc/injector.py:220-265) for registration (scripts/register_doc.py:699).
  */
@@ -192,6 +197,14 @@ int xenc_route_backward(const float* w, long long ldw, const float* dw_read, lon
                         const int* tile_ptr, int G, int n_tiles, int cmax, const float* S,
                         const int* chunk_ptr, int d, float route_temp, float* dq, long long ldq,
                         void* stream);
+int xenc_prefill_readout_routed(const void* ds, long long a_rows, const int* row_ptr,
+                                const int* tile_ptr, int G, int n_tiles, const void* pages_b,
+                                int slots_per_page, int d, long long page_stride,
+                                const int* chunk_ptr, const int* chunk_page, const float* w,
+                                long long ldw, const float* dw_read, long long ldr,
+                                const float* dw_ext, long long lde, const float* S, int cmax,
+                                float route_temp, float* dl, long long ldl, float* dq,
+                                long long ldq, void* stream);
 
 /*
  * ---- Write-back through the interface's B (decode path)

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (must be loaded first: shares its HIP runtime with the library)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libxenc_hip.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 _lock = threading.Lock()
 _lib = None
@@ -158,6 +158,14 @@ SIGNATURES = {
         c_void_p, c_longlong, c_void_p, c_void_p,    # dw_ext, lde, row_ptr, tile_ptr
         c_int, c_int, c_int, c_void_p, c_void_p,     # G, n_tiles, cmax, S, chunk_ptr
         c_int, c_float, c_void_p, c_longlong, c_void_p]),  # d, route_temp, dq, ldq, stream
+    "xenc_prefill_readout_routed": (c_int, [
+        c_void_p, c_longlong, c_void_p, c_void_p,    # ds, a_rows, row_ptr, tile_ptr
+        c_int, c_int, c_void_p, c_int, c_int,        # G, n_tiles, pages_b, slots_per_page, d
+        c_longlong, c_void_p, c_void_p,              # page_stride, chunk_ptr, chunk_page
+        c_void_p, c_longlong, c_void_p, c_longlong,  # w, ldw, dw_read, ldr
+        c_void_p, c_longlong, c_void_p, c_int,       # dw_ext, lde, S, cmax
+        c_float, c_void_p, c_longlong,               # route_temp, dl, ldl
+        c_void_p, c_longlong, c_void_p]),            # dq, ldq, stream
 }
 
 

@@ -21,4 +21,4 @@ extern "C" const char* xenc_strerror(int code) {
 
 extern "C" int xenc_last_hip_error(void) { return xenc::g_last_hip_error; }
 
-extern "C" int xenc_abi_version(void) { return 17; }
+extern "C" int xenc_abi_version(void) { return 18; }

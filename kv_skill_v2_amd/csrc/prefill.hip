@@ -27,6 +27,7 @@
 // slot scores of 4 query rows: the softmax over slots is an in-lane reduction plus one xor-32
 // shuffle plus an 8-wave LDS exchange.
 #include <algorithm>
+#include <climits>
 
 #include "xenc_common.h"
 
@@ -451,12 +452,15 @@ __global__ __launch_bounds__(512) void scores_kernel(
 // layout-B page copy (coalesced 1 KiB loads), refilled for the next k-step as they are consumed;
 // the 128 A rows are shared and staged through LDS (two swizzled stages of 16 KiB).
 // scale = w[t, c] when w != nullptr (forward read), else 1 (the backward dS already carries it).
-// Rows of one tile belong to one library.
-__global__ __launch_bounds__(256) void readout_kernel(
+// ROUTE (backward): the accumulators start from the routing term sum_c dl[t, c] S[c, :] over the
+// library's chunks (fp32 MFMAs) instead of 0.  Rows of one tile belong to one library.
+template <bool ROUTE>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void readout_kernel(
     const _Float16* __restrict__ A, long long a_rows, const int* __restrict__ row_ptr,
     const int* __restrict__ tile_ptr, int G, const _Float16* __restrict__ pages_b, int N, int d,
     long long page_stride, const int* __restrict__ chunk_ptr, const int* __restrict__ chunk_page,
-    const float* __restrict__ w, long long ldw, float* __restrict__ out, long long ldo) {
+    const float* __restrict__ w, long long ldw, const float* __restrict__ dl, long long ldl,
+    const float* __restrict__ S, float* __restrict__ out, long long ldo) {
   constexpr int RT = kReadoutRows;
   __shared__ _Float16 lA[3][RT * BK];
 
@@ -524,6 +528,36 @@ __global__ __launch_bounds__(256) void readout_kernel(
   for (int mt = 0; mt < NA; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt) acc[mt][nt] = (f32x16){};
+  if (ROUTE) {
+    // The routing term, k = 2 chunks per v_mfma_f32_32x32x2f32: lane l supplies A[l%32][l/32] =
+    // dl[row 32mt + l32][chunk c0 + hl] and B[l/32][l%32] = S[chunk c0 + hl][column], and the
+    // result lands in the accumulator layout of the read.  Rows past the library and columns past
+    // d read clamped addresses and are never stored; a chunk past C contributes 0.  Addresses are
+    // 32-bit lane offsets from the tile's (wave-uniform) bases: one register per load.
+    const float* dl_tile = dl + (long long)row0 * ldl;
+    const float* s_lib = S + (long long)cbeg * d;
+    int dlo[NA], so[2];
+#pragma unroll
+    for (int mt = 0; mt < NA; ++mt) dlo[mt] = (min(row0 + mt * 32 + l32, rend - 1) - row0) * (int)ldl;
+#pragma unroll
+    for (int nt = 0; nt < 2; ++nt) so[nt] = min(d0 + wv * 64 + nt * 32 + l32, d - 1);
+#pragma unroll 4
+    for (int c0 = 0; c0 < C; c0 += 2) {
+      const int cl = c0 + hl;
+      const bool live = cl < C;
+      const int cc = live ? cl : C - 1;
+      float av[NA], bv[2];
+#pragma unroll
+      for (int mt = 0; mt < NA; ++mt) av[mt] = live ? dl_tile[dlo[mt] + cc] : 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt) bv[nt] = live ? s_lib[so[nt] + cc * d] : 0.f;
+#pragma unroll
+      for (int mt = 0; mt < NA; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
+    }
+  }
   // fa0: the first k16 step's A fragments of the coming k-step, read before the barrier that
   // ends the previous k-step (as in the scores kernel).
   half8_t fa0[NA];
@@ -617,6 +651,32 @@ __global__ __launch_bounds__(256) void readout_kernel(
         if (dd < d) out[(long long)t * ldo + dd] = acc[mt][nt][r];
       }
     }
+}
+
+// ------------------------------------------------------------------------------------------
+// Routing coefficients of the backward: dl[t, c] = route_temp * w (dw - sum_c' w dw) for the
+// chunks c of row t's library (dw = dw_read (+ dw_ext when given)); one wave per row.  The
+// readout adds sum_c dl[t, c] S[c] to dq.
+__global__ __launch_bounds__(256) void route_coef_kernel(
+    const float* __restrict__ w, long long ldw, const float* __restrict__ dw_read, long long ldr,
+    const float* __restrict__ dw_ext, long long lde, const int* __restrict__ row_ptr, int G,
+    const int* __restrict__ chunk_ptr, int M, float route_temp, float* __restrict__ dl,
+    long long ldl) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  if (t >= M) return;
+  const int g = find_group(row_ptr, G, t);
+  const int C = chunk_ptr[g + 1] - chunk_ptr[g];
+  auto dw_of = [&](int c) {
+    float dv = dw_read[(long long)t * ldr + c];
+    if (dw_ext) dv += dw_ext[(long long)t * lde + c];
+    return dv;
+  };
+  float sdot = 0.f;
+  for (int c = lane; c < C; c += 64) sdot += w[(long long)t * ldw + c] * dw_of(c);
+  sdot = wave_sum(sdot);
+  for (int c = lane; c < C; c += 64)
+    dl[(long long)t * ldl + c] = route_temp * w[(long long)t * ldw + c] * (dw_of(c) - sdot);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -782,10 +842,42 @@ extern "C" int xenc_prefill_readout(const void* a, long long a_rows, const int* 
   if (!a || !row_ptr || !tile_ptr || !pages_b || !chunk_ptr || !chunk_page || !out)
     return XENC_ENULL;
   if (!aligned16(a) || !aligned16(pages_b)) return XENC_EALIGN;
-  hipLaunchKernelGGL(readout_kernel, dim3(n_tiles), dim3(256), 0,
+  hipLaunchKernelGGL(readout_kernel<false>, dim3(n_tiles), dim3(256), 0,
                      reinterpret_cast<hipStream_t>(stream), static_cast<const _Float16*>(a), a_rows,
                      row_ptr, tile_ptr, G, static_cast<const _Float16*>(pages_b), slots_per_page,
-                     d, page_stride, chunk_ptr, chunk_page, w, ldw, out, ldo);
+                     d, page_stride, chunk_ptr, chunk_page, w, ldw, nullptr, 0, nullptr, out, ldo);
+  return check_launch();
+}
+
+extern "C" int xenc_prefill_readout_routed(const void* ds, long long a_rows, const int* row_ptr,
+                                           const int* tile_ptr, int G, int n_tiles,
+                                           const void* pages_b, int slots_per_page, int d,
+                                           long long page_stride, const int* chunk_ptr,
+                                           const int* chunk_page, const float* w, long long ldw,
+                                           const float* dw_read, long long ldr,
+                                           const float* dw_ext, long long lde, const float* S,
+                                           int cmax, float route_temp, float* dl, long long ldl,
+                                           float* dq, long long ldq, void* stream) {
+  if (int rc = check_prefill_common(d, slots_per_page, page_stride)) return rc;
+  if (G <= 0 || n_tiles < 0 || a_rows < 0 || a_rows > INT_MAX || cmax <= 0 || ldq < d ||
+      ldl < cmax || ldw < cmax || ldr < cmax || (dw_ext && lde < cmax))
+    return XENC_EINVAL;
+  // 32-bit offsets inside a readout tile (128 rows of dl) and a library's summaries (cmax rows of S)
+  if ((long long)kReadoutRows * ldl > INT_MAX || (long long)cmax * d > INT_MAX) return XENC_EINVAL;
+  if (n_tiles == 0 || a_rows == 0) return XENC_OK;
+  if (!ds || !row_ptr || !tile_ptr || !pages_b || !chunk_ptr || !chunk_page || !w || !dw_read ||
+      !S || !dl || !dq)
+    return XENC_ENULL;
+  if (!aligned16(ds) || !aligned16(pages_b)) return XENC_EALIGN;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int M = (int)a_rows;
+  hipLaunchKernelGGL(route_coef_kernel, dim3((M + 3) / 4), dim3(256), 0, st, w, ldw, dw_read,
+                     ldr, dw_ext, lde, row_ptr, G, chunk_ptr, M, route_temp, dl, ldl);
+  if (int rc = check_launch()) return rc;
+  hipLaunchKernelGGL(readout_kernel<true>, dim3(n_tiles), dim3(256), 0, st,
+                     static_cast<const _Float16*>(ds), a_rows, row_ptr, tile_ptr, G,
+                     static_cast<const _Float16*>(pages_b), slots_per_page, d, page_stride,
+                     chunk_ptr, chunk_page, nullptr, 0, dl, ldl, S, dq, ldq);
   return check_launch();
 }
 

@@ -816,6 +816,28 @@ def prefill_backward(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, lib_: Pa
     return torch.ops.xenc.library_prefill_bwd_dq(g, w, p, fvs, fkr, *rest, float(read_temp), bool(softmax))
 
 
+def prefill_backward_routed(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
+                            read_temp: float = 12.0, softmax: bool = True, route_temp: float = 10.0,
+                            dw_ext: torch.Tensor | None = None) -> torch.Tensor:
+    """dq [M, d] fp32 through the read and the routing, given g = dL/dr (and dw_ext, the gradient
+    that reaches w from elsewhere): operator xenc::library_prefill_bwd_routed (scores_kernel<1|3>,
+    then route_coef_kernel and readout_kernel with the routing term in its epilogue).  Equals
+    prefill_backward's dq followed by route_backward with dw = gamma, in one pass over dq."""
+    g = _query(g, lib_.d)
+    M, d = g.shape
+    w = w.to(torch.float32).contiguous()
+    if p.shape != (lib_.cmax * lib_.slots_per_page // 8, M, 8) or not p.is_contiguous():
+        raise ValueError("p must be the octet-major probabilities prefill_forward returned")
+    if dw_ext is not None:
+        if dw_ext.shape != w.shape:
+            raise ValueError(f"dw_ext must have shape {tuple(w.shape)}")
+        dw_ext = dw_ext.to(torch.float32).contiguous()
+    _, _, fvs, fkr, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, st, rt, n_s, n_r, slots = _prefill_operands(lib_, plan)
+    return torch.ops.xenc.library_prefill_bwd_routed(g, w, p, dw_ext, lib_.S, fvs, fkr, chunk_ptr, chunk_page,
+                                                     chunk_nvalid, row_ptr, st, rt, n_s, n_r, slots, float(read_temp),
+                                                     bool(softmax), float(route_temp))
+
+
 def route_backward(w: torch.Tensor, dw: torch.Tensor, lib_: PagedLibrary, plan: RowPlan,
                    route_temp: float, dq: torch.Tensor, dw_ext: torch.Tensor | None = None) -> torch.Tensor:
     """dq += route_temp * sum_c w (dw - sum w dw) S_c, in place (operator xenc::route_backward_)."""

@@ -20,8 +20,9 @@ dispatcher, FakeTensor tracing and torch.compile see ordinary operators:
                                  and w (its backward is the next operator plus the route term)
     xenc::library_prefill_bwd_dq (dq through the read, gamma = dL/dw) from the upstream gradient
     xenc::route_backward_        dq += the routing term, in place
+    xenc::library_prefill_bwd_routed  dq through the read and the routing in one pass over dq
     xenc::library_read_routed    route_rows + library_prefill_fwd as one autograd node (its
-                                 backward adds the routing term into the read's dq in place)
+                                 backward is library_prefill_bwd_routed)
     xenc::paged_decode_joint     DecodeReader's joint read (xenc/d23_read_kernels.py:145-160) into
                                  a caller-owned output; writes its workspace
 
@@ -159,21 +160,61 @@ def library_prefill_bwd_dq(g: Tensor, w: Tensor, p: Tensor, frag_v_scores: Tenso
                            slots: int, read_temp: float, softmax: bool) -> tuple[Tensor, Tensor]:
     """(dq [M, d] through the read, gamma [M, cmax] = dL/dw) for the upstream gradient g [M, d]."""
     M, d = g.shape
-    G = chunk_ptr.numel() - 1
+    ds, gamma = _bwd_scores(g, w, p, frag_v_scores, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles,
+                            n_score, slots, read_temp, softmax)
+    dq = torch.empty(M, d, dtype=torch.float32, device=g.device)
+    check(lib().xenc_prefill_readout(ptr(ds), M, ptr(row_ptr), ptr(readout_tiles), chunk_ptr.numel() - 1,
+                                     n_readout, ptr(frag_k_readout), slots, d, frag_k_readout.stride(0),
+                                     ptr(chunk_ptr), ptr(chunk_page), None, 0, ptr(dq), dq.stride(0), _st(g)),
+          "xenc_prefill_readout")
+    return dq, gamma
+
+
+def _bwd_scores(g, w, p, frag_v_scores, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles, n_score, slots,
+                read_temp, softmax):
+    """The backward's scores pass: (dS octet-major like p, gamma [M, cmax] = dL/dw through the read)."""
+    M, d = g.shape
     L, st = lib(), _st(g)
     gh = torch.empty(M, d, dtype=torch.float16, device=g.device)
     check(L.xenc_cast_rows_f16(ptr(g), g.stride(0), M, d, ptr(gh), st), "xenc_cast_rows_f16")
     ds = torch.empty_like(p)
     gamma = torch.zeros(M, w.shape[1], dtype=torch.float32, device=g.device)
-    check(L.xenc_prefill_scores(1 if softmax else 3, ptr(gh), d, ptr(row_ptr), ptr(score_tiles), G, n_score,
-                                ptr(frag_v_scores), slots, frag_v_scores.stride(0), ptr(chunk_ptr),
-                                ptr(chunk_page), ptr(chunk_nvalid), read_temp, ptr(w), w.stride(0), ptr(p), M,
-                                ptr(ds), ptr(gamma), gamma.stride(0), st), "xenc_prefill_scores")
+    check(L.xenc_prefill_scores(1 if softmax else 3, ptr(gh), d, ptr(row_ptr), ptr(score_tiles),
+                                chunk_ptr.numel() - 1, n_score, ptr(frag_v_scores), slots, frag_v_scores.stride(0),
+                                ptr(chunk_ptr), ptr(chunk_page), ptr(chunk_nvalid), read_temp, ptr(w), w.stride(0),
+                                ptr(p), M, ptr(ds), ptr(gamma), gamma.stride(0), st), "xenc_prefill_scores")
+    return ds, gamma
+
+
+@custom_op("xenc::library_prefill_bwd_routed", mutates_args=())
+def library_prefill_bwd_routed(g: Tensor, w: Tensor, p: Tensor, dw_ext: Optional[Tensor], S: Tensor,
+                               frag_v_scores: Tensor, frag_k_readout: Tensor, chunk_ptr: Tensor, chunk_page: Tensor,
+                               chunk_nvalid: Tensor, row_ptr: Tensor, score_tiles: Tensor, readout_tiles: Tensor,
+                               n_score: int, n_readout: int, slots: int, read_temp: float, softmax: bool,
+                               route_temp: float) -> Tensor:
+    """dq [M, d] through the read AND the routing, for the upstream gradient g = dL/dr and the
+    gradient dw_ext that reaches w from elsewhere (None: none): the scores pass gives gamma =
+    dL/dw through the read, then route_coef_kernel + readout_kernel write
+    dq = dS . K + route_temp * sum_c w (dw - sum w dw) S_c with dw = gamma + dw_ext, the routing
+    term added in the readout's epilogue."""
+    M, d = g.shape
+    cmax = w.shape[1]
+    ds, gamma = _bwd_scores(g, w, p, frag_v_scores, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles,
+                            n_score, slots, read_temp, softmax)
+    dl = torch.empty(M, cmax, dtype=torch.float32, device=g.device)
     dq = torch.empty(M, d, dtype=torch.float32, device=g.device)
-    check(L.xenc_prefill_readout(ptr(ds), M, ptr(row_ptr), ptr(readout_tiles), G, n_readout,
-                                 ptr(frag_k_readout), slots, d, frag_k_readout.stride(0), ptr(chunk_ptr),
-                                 ptr(chunk_page), None, 0, ptr(dq), dq.stride(0), st), "xenc_prefill_readout")
-    return dq, gamma
+    check(lib().xenc_prefill_readout_routed(
+        ptr(ds), M, ptr(row_ptr), ptr(readout_tiles), chunk_ptr.numel() - 1, n_readout, ptr(frag_k_readout), slots,
+        d, frag_k_readout.stride(0), ptr(chunk_ptr), ptr(chunk_page), ptr(w), w.stride(0), ptr(gamma),
+        gamma.stride(0), ptr(dw_ext), dw_ext.stride(0) if dw_ext is not None else 0, ptr(S), cmax, route_temp,
+        ptr(dl), dl.stride(0), ptr(dq), dq.stride(0), _st(g)), "xenc_prefill_readout_routed")
+    return dq
+
+
+@library_prefill_bwd_routed.register_fake
+def _(g, w, p, dw_ext, S, frag_v_scores, frag_k_readout, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles,
+      readout_tiles, n_score, n_readout, slots, read_temp, softmax, route_temp):
+    return g.new_empty(g.shape)
 
 
 @library_prefill_bwd_dq.register_fake
@@ -277,10 +318,10 @@ def library_read_routed(q: Tensor, S: Tensor, chunk_ptr: Tensor, row_ptr: Tensor
                         readout_tiles: Tensor, n_score: int, n_readout: int, slots: int, read_temp: float,
                         softmax: bool, ragged: bool) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     """(r [M, d], w [M, cmax], idx, w_sel, p): xenc::route_rows (which also writes q as fp16) then
-    xenc::library_prefill_fwd, as ONE autograd node.  Its backward writes dq once: the read's dq
-    (scores_kernel<1|3> + readout_kernel), then the routing term added in place
-    (route_backward_kernel) with dL/dw = gamma + the gradient that reaches w from elsewhere (the
-    injector's route_terms), so no zeroed gradient buffer and no gradient sum are needed."""
+    xenc::library_prefill_fwd, as ONE autograd node.  Its backward (library_prefill_bwd_routed)
+    writes dq once, the routing term with dL/dw = gamma + the gradient that reaches w from
+    elsewhere (the injector's route_terms) added in the readout's epilogue, so no zeroed gradient
+    buffer, no second pass over dq and no gradient sum are needed."""
     w, idx, wsel, qh = torch.ops.xenc.route_rows(q, S, chunk_ptr, row_ptr, logit_tiles, route_tiles, n_logit,
                                                   n_route, top_k, route_temp, cmax, kk, True)
     r, p = torch.ops.xenc.library_prefill_fwd(q, qh, w, frag_k_scores, frag_v_readout, frag_v_scores,
@@ -315,15 +356,16 @@ def _routed_setup(ctx, inputs, output):
 def _routed_backward(ctx, dr, dw, _didx, _dwsel, _dp):
     w, p, fvs, fkr, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles, readout_tiles, S, route_tiles = \
         ctx.saved_tensors
-    if dr is None:
+    dw = None if dw is None else dw.contiguous()
+    if dr is None:  # only w reaches the loss: the routing term alone
         dq = torch.zeros(w.shape[0], ctx.d, dtype=torch.float32, device=w.device)
-        gamma = torch.zeros_like(w)
+        torch.ops.xenc.route_backward_(dq, w, torch.zeros_like(w), dw, S, chunk_ptr, row_ptr, route_tiles,
+                                       *ctx.route)
     else:
-        dq, gamma = torch.ops.xenc.library_prefill_bwd_dq(dr.contiguous(), w, p, fvs, fkr, chunk_ptr, chunk_page,
-                                                           chunk_nvalid, row_ptr, score_tiles, readout_tiles,
-                                                           *ctx.sizes)
-    torch.ops.xenc.route_backward_(dq, w, gamma, None if dw is None else dw.contiguous(), S, chunk_ptr, row_ptr,
-                                   route_tiles, *ctx.route)
+        n_score, n_readout, slots, read_temp, softmax = ctx.sizes
+        dq = torch.ops.xenc.library_prefill_bwd_routed(dr.contiguous(), w, p, dw, S, fvs, fkr, chunk_ptr, chunk_page,
+                                                        chunk_nvalid, row_ptr, score_tiles, readout_tiles, n_score,
+                                                        n_readout, slots, read_temp, softmax, ctx.route[1])
     return (dq,) + (None,) * 25
 
 
@@ -340,4 +382,4 @@ def _(q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len, scale, nsplit
 
 
 __all__ = ["route_rows", "route_backward_", "library_prefill_lse", "library_prefill_fwd",
-           "library_prefill_bwd_dq", "library_read_routed", "kept_width", "TORCH_OPS_PATH"]
+           "library_prefill_bwd_dq", "library_prefill_bwd_routed", "library_read_routed", "kept_width", "TORCH_OPS_PATH"]

@@ -150,9 +150,14 @@ def test_prefill_full_shape_row_sample(dev):
     with torch.no_grad():
         w, _, _, qh = ops.route_topk_rows(q, lib, plan, top_k=0, emit_f16=True)
         r, p = ops.prefill_forward(q, w, lib, plan, qh=qh)
-        dq, gamma = ops.prefill_backward(g_up, w, p, lib, plan)
-        ops.route_backward(w, gamma, lib, plan, 10.0, dq)
+        dq = ops.prefill_backward_routed(g_up, w, p, lib, plan, route_temp=10.0)
+        # the same gradient through the read's dq and a separate pass adding the routing term
+        dq2, gamma = ops.prefill_backward(g_up, w, p, lib, plan)
+        ops.route_backward(w, gamma, lib, plan, 10.0, dq2)
     torch.cuda.synchronize()
+    sep = float((dq - dq2).abs().max()) / float(dq2.abs().max())
+    say("routed backward vs separate route pass, max-abs / max", sep)
+    assert sep <= 1e-5
     # two rows in each 128-row tile, at varying offsets, plus the first and last row
     sample = sorted({0, T - 1} | {t * 128 + (37 * t + 5) % 128 for t in range(16)}
                     | {t * 128 + (91 * t + 64) % 128 for t in range(16)})

@@ -52,6 +52,11 @@ def test_opcheck_route_and_decode_read(dev):
         assert float((r[m] - ref.view(-1)).abs().max()) < 2e-3
 
 
+def _close(a, b, rel=1e-5):
+    """Equal up to fp32 rounding of a reordered sum: max-abs difference within rel of max |b|."""
+    return float((a - b).abs().max()) <= rel * float(b.abs().max())
+
+
 def test_opcheck_prefill_and_routing_with_autograd(dev):
     say("opcheck route_rows / library_prefill_fwd / bwd / route_backward_")
     P, lib = _pool(dev, counts=(3, 2), N=128, d=128)
@@ -74,13 +79,24 @@ def test_opcheck_prefill_and_routing_with_autograd(dev):
              plan.n_route, 10.0)
     torch.library.opcheck(torch.ops.xenc.route_backward_.default, gargs,
                           test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
+    # the backward with the routing term in the readout's epilogue == bwd_dq + route_backward_
+    dw_ext = torch.randn_like(w)
+    xargs = (g, w.detach(), p, dw_ext, lib.S, *operands[2:], 12.0, True, 10.0)
+    torch.library.opcheck(torch.ops.xenc.library_prefill_bwd_routed.default, xargs,
+                          test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
+    dq_x = torch.ops.xenc.library_prefill_bwd_routed(*xargs)
+    dq_r, gamma = torch.ops.xenc.library_prefill_bwd_dq(*bargs)
+    torch.ops.xenc.route_backward_(dq_r, w.detach(), gamma, dw_ext, lib.S, lib.chunk_ptr, plan.row_ptr,
+                                   plan.route_tiles, plan.n_route, 10.0)
+    assert _close(dq_x, dq_r), float((dq_x - dq_r).abs().max())
     # routing + read as one autograd node: schema, fakes, registered autograd ...
     cargs = (q, lib.S, lib.chunk_ptr, plan.row_ptr, plan.logit_tiles, plan.route_tiles, plan.n_logit, plan.n_route,
              2, 10.0, lib.cmax, kept_width(2, lib.cmax), *operands[:4], lib.chunk_page, lib.chunk_nvalid,
              plan.score_tiles, plan.readout_tiles, plan.n_score, plan.n_readout, lib.slots_per_page, 12.0, True, True)
     torch.library.opcheck(torch.ops.xenc.library_read_routed.default, cargs, test_utils=CHECKS)
-    # ... and the same values and gradients as the two operators, bit for bit, for a loss on both
-    # r and w (the gradient reaching w from elsewhere enters the routing term in place)
+    # ... and the same values (bit for bit) and gradients (to fp32 rounding: the routing term is
+    # summed in another order) as the two operators, for a loss on both r and w (the gradient
+    # reaching w from elsewhere enters the routing term)
     qa = q.detach().clone().requires_grad_(True)
     qb = q.detach().clone().requires_grad_(True)
     ra, wa, *_ = torch.ops.xenc.library_read_routed(qa, *cargs[1:])
@@ -89,7 +105,7 @@ def test_opcheck_prefill_and_routing_with_autograd(dev):
     rb, _ = torch.ops.xenc.library_prefill_fwd(qb, qhb, wb, *operands, 12.0, True, True)
     ((rb * g).sum() + 3.0 * (wb * wb).sum()).backward()
     assert torch.equal(ra, rb) and torch.equal(wa, wb)
-    assert torch.equal(qa.grad, qb.grad), float((qa.grad - qb.grad).abs().max())
+    assert _close(qa.grad, qb.grad), float((qa.grad - qb.grad).abs().max())
     # autograd through both operators equals the oracle's closed-form dq
     r, w2 = ops.library_read(q, lib, plan)
     (r * g).sum().backward()
