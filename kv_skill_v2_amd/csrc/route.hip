@@ -286,13 +286,20 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
     qsrc[i] = q + (long long)min(row0 + lrow[i], rend - 1) * ldq + lk[i];
     ssrc[i] = S + (long long)(c0 + min(cb0 + lrow[i], C - 1)) * d + lk[i];
   }
-  float4 qv[kRouteLoads], sv[kRouteLoads];
-  auto load = [&](int k0) {
+  // Four register slots: the loads of k-step j go out three steps ahead, during the MFMAs of
+  // step j - 3 (one step of MFMAs is much shorter than a memory round trip).  Every step is
+  // unconditional, so each slot keeps its registers through the loop: the k-loop runs a multiple
+  // of four steps, and steps past d load clamped addresses and store zeros.  Columns past d
+  // (d % 4 == 0, so a float4 is all in or all out) are zeroed at the store the same way, never
+  // by a masked load, which the compiler would wait for on the spot.
+  constexpr int NS = 4;
+  float4 qv[NS][kRouteLoads], sv[NS][kRouteLoads];
+  auto load = [&](int slot, int k0) {
 #pragma unroll
     for (int i = 0; i < kRouteLoads; ++i) {
-      const bool in = k0 + lk[i] < d;   // d % 4 == 0: a float4 is all in or all out
-      qv[i] = in ? *reinterpret_cast<const float4*>(qsrc[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
-      sv[i] = in ? *reinterpret_cast<const float4*>(ssrc[i] + k0) : make_float4(0.f, 0.f, 0.f, 0.f);
+      const int k = min(k0, d - 4 - lk[i]);
+      qv[slot][i] = *reinterpret_cast<const float4*>(qsrc[i] + k);
+      sv[slot][i] = *reinterpret_cast<const float4*>(ssrc[i] + k);
     }
   };
   typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -301,27 +308,25 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
   const int l32 = lane & 31, hl = lane >> 5;
   const bool write_h = qh != nullptr && cb0 == 0;
   f32x16 acc = {};
-  load(0);
-  for (int k0 = 0; k0 < d; k0 += kRouteK) {
+  // One k-step from register slot `slot` (a constant after inlining).
+  auto step = [&](int slot, int k0) {
     __syncthreads();   // the previous step's LDS reads are done
 #pragma unroll
     for (int i = 0; i < kRouteLoads; ++i) {
-      *reinterpret_cast<float4*>(&qs[lrow[i] * kRouteLd + lk[i]]) = qv[i];
-      *reinterpret_cast<float4*>(&ss[lrow[i] * kRouteLd + lk[i]]) = sv[i];
-    }
-    if (write_h) {
-#pragma unroll
-      for (int i = 0; i < kRouteLoads; ++i) {
-        const int row = row0 + lrow[i], k = k0 + lk[i];
-        if (row < rend && k < d) {
-          typedef _Float16 half4 __attribute__((ext_vector_type(4)));
-          const half4 h = {(_Float16)qv[i].x, (_Float16)qv[i].y, (_Float16)qv[i].z, (_Float16)qv[i].w};
-          *reinterpret_cast<half4*>(qh + (long long)row * d + k) = h;
-        }
+      const bool in = k0 + lk[i] < d;
+      const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+      const float4 a = in ? qv[slot][i] : z, b = in ? sv[slot][i] : z;
+      *reinterpret_cast<float4*>(&qs[lrow[i] * kRouteLd + lk[i]]) = a;
+      *reinterpret_cast<float4*>(&ss[lrow[i] * kRouteLd + lk[i]]) = b;
+      const int row = row0 + lrow[i];
+      if (write_h && in && row < rend) {
+        typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+        const half4 h = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
+        *reinterpret_cast<half4*>(qh + (long long)row * d + k0 + lk[i]) = h;
       }
     }
     __syncthreads();
-    if (k0 + kRouteK < d) load(k0 + kRouteK);   // in flight during this step's MFMAs
+    load(slot, k0 + NS * kRouteK);   // this slot is stored: refill it NS steps ahead
     // Lane l feeds row / chunk l % 32 and columns kb + 4 (l / 32) .. + 3 to four MFMAs: MFMA i
     // contracts column kb + 4h + i of both operands for lane half h.
     constexpr int kPerWave = kRouteK / 4;
@@ -333,6 +338,12 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[i], acc, 0, 0, 0);
     }
+  };
+#pragma unroll
+  for (int j = 0; j < NS; ++j) load(j, j * kRouteK);
+  for (int k0 = 0; k0 < d; k0 += NS * kRouteK) {
+#pragma unroll
+    for (int j = 0; j < NS; ++j) step(j, k0 + j * kRouteK);
   }
   // acc[r] = partial dot of row 8(r/4) + 4hl + r%4, chunk l32.  Sum the 4 waves in order.
   __syncthreads();

@@ -138,19 +138,21 @@ def test_prefill_variants_fwd_bwd(dev, variant):
 
 @pytest.mark.parametrize("counts,rows,top_k", [([32, 7, 130], [300, 64, 129], 0), ([32, 7, 130], [300, 0, 65], 5),
                                                ([1, 64], [70, 1], 1)])
-def test_route_rows_matches_per_row_kernel(dev, counts, rows, top_k):
+@pytest.mark.parametrize("d", [256, 456])
+def test_route_rows_matches_per_row_kernel(dev, counts, rows, top_k, d):
     """The many-row routing kernel gives the per-row kernel's routing: identical kept chunks
-    (rows whose fp64 top-k gap is below 1e-5 are exempt) and weights within 1e-6."""
-    say("route rows", dict(counts=counts, rows=rows, top_k=top_k))
-    d = 256
+    (rows whose fp64 top-k gap is below 1e-5 are exempt) and weights within 1e-6; its fp16 copy
+    of q is the cast.  d = 456 ends in a partial k-step of 72 columns."""
+    say("route rows", dict(counts=counts, rows=rows, top_k=top_k, d=d))
     P = synth.pool(counts, 64, d, device="cpu", tail_lo=1)
     lib = _lib(P, dev)
     plan = ops.row_plan(lib, rows)
     q = synth.queries(sum(rows), d, device="cpu", seed=31)
     qg = ops._plan_groups(plan)
     w1, i1, s1 = ops.route_topk(q.to(dev), lib, qg.to(dev), top_k=top_k)
-    w2, i2, s2 = ops.route_topk_rows(q.to(dev), lib, plan, top_k=top_k)
+    w2, i2, s2, qh = ops.route_topk_rows(q.to(dev), lib, plan, top_k=top_k, emit_f16=True)
     assert (w1 - w2).abs().max().item() <= 1e-6
+    assert torch.equal(qh, ops.cast_f16(q.to(dev)))
     i1, i2 = i1.cpu(), i2.cpu()
     off = 0
     for g, T in enumerate(rows):
