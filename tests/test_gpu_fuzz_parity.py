@@ -1,4 +1,4 @@
-"""Seeded random shapes through the product's decode and prefill paths against the CPU oracle.
+"""Seeded random shapes through the product's decode, prefill and op-B paths against the CPU oracle.
 
 Each case draws its shape from a fixed seed (page size, d, chunk and row counts per library,
 top-k, slot splits, softmax or linear read, how ragged the last page of a library is), so a
@@ -155,3 +155,47 @@ def test_prefill_random_shapes(dev, i):
             rm = float((x - y).abs().max() / y.abs().max().clamp_min(1e-30))
             assert rn <= 1e-2 and rm <= 1e-2, (g, rn, rm)
         off += T
+
+
+def _decode_reader_case(i: int) -> dict:
+    rng = random.Random(4000 + i)
+    G = rng.choice([1, 2, 3, 4, 8])
+    d = rng.choice([x for x in (8, 64, 80, 128, 136, 256, 512) if G * x <= 4096])
+    bs = rng.choice([1, 8, 16, 32])
+    N = rng.randint(1, 10)
+    op_blocks = rng.randint(1, max(1, 1024 // bs))
+    own_blocks = rng.randint(1, max(1, 128 // bs))
+    op_len = [rng.randint(0, op_blocks * bs) for _ in range(N)]
+    own_len = [rng.randint(0 if o else 1, own_blocks * bs) for o in op_len]   # every row reads >= 1 key
+    return dict(G=G, hkv=rng.choice([1, 2, 4]), d=d, bs=bs, N=N, op_blocks=op_blocks, own_blocks=own_blocks,
+                op_len=op_len, own_len=own_len, dtype=rng.choice([torch.float16, torch.bfloat16]),
+                chunk=rng.choice([None, 64, 128, 512]), seed=110 + i)
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_decode_reader_random_layouts(dev, i):
+    """Op B (DecodeReader's joint read over paged operator + own pools) on seeded random layouts
+    against the oracle's decode_read_ref: relative error < 2e-3 (the reference test's bar,
+    tests/test_d23_kernels.py:51-82 of the reference)."""
+    from kv_skill_v2_amd.decode_reader import DecodeReader
+
+    c = _decode_reader_case(i)
+    say("op B", i, {k: (str(v) if k == "dtype" else v) for k, v in c.items()})
+    g = torch.Generator().manual_seed(c["seed"])
+    hkv, d, bs, N, dt = c["hkv"], c["d"], c["bs"], c["N"], c["dtype"]
+    hq = c["G"] * hkv
+    nb_op, nb_own = c["op_blocks"] + 3, c["own_blocks"] * N + 2
+    op_k, op_v = (torch.randn(nb_op, bs, hkv, d, generator=g).to(dt) for _ in range(2))
+    own_k, own_v = (torch.randn(nb_own, bs, hkv, d, generator=g).to(dt) for _ in range(2))
+    q = torch.randn(N, hq, d, generator=g).to(dt)
+    op_bt = torch.stack([torch.randperm(nb_op, generator=g)[:c["op_blocks"]] for _ in range(N)]).int()
+    own_bt = torch.stack([torch.randperm(nb_own, generator=g)[:c["own_blocks"]] for _ in range(N)]).int()
+    op_len = torch.tensor(c["op_len"], dtype=torch.int32)
+    own_len = torch.tensor(c["own_len"], dtype=torch.int32)
+    args = [q, op_k, op_v, op_bt, op_len, own_k, own_v, own_bt, own_len]
+    max_keys = max(1, int((op_len + own_len).max()))
+    dec = DecodeReader(N, hq, hkv, d, max_keys=max_keys, device=dev, chunk=c["chunk"])
+    out = dec(*[a.to(dev) for a in args], d ** -0.5).double().cpu()
+    ref = O.decode_read_ref(*args, d ** -0.5).double()
+    rel = float((out - ref).norm() / ref.norm().clamp_min(1e-30))
+    assert rel < 2e-3, rel
