@@ -171,7 +171,8 @@ int xenc_library_read_decode_noalloc(const float* q, long long ldq, int M, int d
  *     is given (forward read) else 1 (backward: out = dq through the read).
  * xenc_route_backward: dq[t] += route_temp * sum_c w (dw - sum_c' w dw) S[c],
  *     dw = dw_read (+ dw_ext when not NULL): the gradient through routing.
- * xenc_prefill_readout_routed: the backward's readout with the routing term in its epilogue:
+ * xenc_prefill_readout_routed: the backward's readout with the routing term folded in (its
+ *     accumulators start from it):
  *     dq[t] = sum_{c,n} ds[t, c, n] K[c, n] + sum_c dl[t, c] S[c], where
  *     dl[t, c] = route_temp * w (dw - sum_c' w dw) (dw = dw_read (+ dw_ext)) is first written to
  *     the caller's dl [a_rows, ldl >= cmax] fp32 buffer.  dq is written, not accumulated: one
