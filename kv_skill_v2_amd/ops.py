@@ -821,7 +821,7 @@ def prefill_backward_routed(g: torch.Tensor, w: torch.Tensor, p: torch.Tensor, l
                             dw_ext: torch.Tensor | None = None) -> torch.Tensor:
     """dq [M, d] fp32 through the read and the routing, given g = dL/dr (and dw_ext, the gradient
     that reaches w from elsewhere): operator xenc::library_prefill_bwd_routed (scores_kernel<1|3>,
-    then route_coef_kernel and readout_kernel with the routing term in its epilogue).  Equals
+    then route_coef_kernel and readout_kernel with the routing term folded in).  Equals
     prefill_backward's dq followed by route_backward with dw = gamma, in one pass over dq."""
     g = _query(g, lib_.d)
     M, d = g.shape

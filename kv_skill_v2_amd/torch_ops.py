@@ -196,7 +196,7 @@ def library_prefill_bwd_routed(g: Tensor, w: Tensor, p: Tensor, dw_ext: Optional
     gradient dw_ext that reaches w from elsewhere (None: none): the scores pass gives gamma =
     dL/dw through the read, then route_coef_kernel + readout_kernel write
     dq = dS . K + route_temp * sum_c w (dw - sum w dw) S_c with dw = gamma + dw_ext, the routing
-    term added in the readout's epilogue."""
+    term folded into the readout (its accumulators start from it)."""
     M, d = g.shape
     cmax = w.shape[1]
     ds, gamma = _bwd_scores(g, w, p, frag_v_scores, chunk_ptr, chunk_page, chunk_nvalid, row_ptr, score_tiles,
@@ -320,7 +320,7 @@ def library_read_routed(q: Tensor, S: Tensor, chunk_ptr: Tensor, row_ptr: Tensor
     """(r [M, d], w [M, cmax], idx, w_sel, p): xenc::route_rows (which also writes q as fp16) then
     xenc::library_prefill_fwd, as ONE autograd node.  Its backward (library_prefill_bwd_routed)
     writes dq once, the routing term with dL/dw = gamma + the gradient that reaches w from
-    elsewhere (the injector's route_terms) added in the readout's epilogue, so no zeroed gradient
+    elsewhere (the injector's route_terms) folded into the readout, so no zeroed gradient
     buffer, no second pass over dq and no gradient sum are needed."""
     w, idx, wsel, qh = torch.ops.xenc.route_rows(q, S, chunk_ptr, row_ptr, logit_tiles, route_tiles, n_logit,
                                                   n_route, top_k, route_temp, cmax, kk, True)

@@ -79,7 +79,7 @@ def test_opcheck_prefill_and_routing_with_autograd(dev):
              plan.n_route, 10.0)
     torch.library.opcheck(torch.ops.xenc.route_backward_.default, gargs,
                           test_utils=("test_schema", "test_faketensor", "test_aot_dispatch_dynamic"))
-    # the backward with the routing term in the readout's epilogue == bwd_dq + route_backward_
+    # the backward with the routing term folded into the readout == bwd_dq + route_backward_
     dw_ext = torch.randn_like(w)
     xargs = (g, w.detach(), p, dw_ext, lib.S, *operands[2:], 12.0, True, 10.0)
     torch.library.opcheck(torch.ops.xenc.library_prefill_bwd_routed.default, xargs,
