@@ -41,8 +41,8 @@ def parse():
     ap.add_argument("--no-graph", action="store_true", help="time the eager step only (no HIP graph replay)")
     ap.add_argument("--no-prefill", action="store_true",
                     help="batched_paged_decode: leave out the prefill block of the JSON line")
-    ap.add_argument("--prefill-steps", type=int, default=10,
-                    help="batched_paged_decode: timed steps of the prefill block (3 warm-up steps)")
+    ap.add_argument("--prefill-steps", type=int, default=20,
+                    help="batched_paged_decode: timed steps of the prefill block (10 warm-up steps)")
     ap.add_argument("--calibration-copy-mib", type=int, default=0,
                     help="after the timed loop, copy a buffer of this size 3 times (a plain copy "
                          "kernel of known bytes, to scale rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -329,7 +329,7 @@ def measure_prefill(steps: int, warmup: int, cpu_sample: int) -> dict:
     for _ in range(warmup):
         step()
     stream = torch.cuda.current_stream(dev)
-    ms_step, _ = timed_steps(step, steps, stream)
+    ms_step, gpu_ms_step = timed_steps(step, steps, stream)
     # The split between the directions, from a second loop of K steps with events between the
     # forward and the backward (outside the timed region above: the events add idle time).
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
@@ -367,7 +367,7 @@ def measure_prefill(steps: int, warmup: int, cpu_sample: int) -> dict:
                           f"CPU oracle on {cpu_model()}, os.cpu_count()={os.cpu_count()}")}
     del lib, P, q, g_up
     torch.cuda.empty_cache()
-    return {"steps": steps, "warmup": warmup, "ms_per_step": ms_step,
+    return {"steps": steps, "warmup": warmup, "ms_per_step": ms_step, "gpu_ms_per_step": gpu_ms_step,
             "tflops_fwd_bwd": 2 * flops / (ms_step * 1e-3) / 1e12, "algorithmic_flops_per_direction": flops,
             "config": {"documents": G, "rows_per_document": T, "chunks": C, "slots_per_page": N, "d_s": d,
                        "routing": "dense (top_k=0)", "accumulate": "fp32", "fragment_pages_ms_once": frag_ms},
@@ -877,7 +877,7 @@ def bench_decode(args):
         # The north star's second target, measured in the same run: the prefill/registration read
         # (4 documents x 2048 rows x 32 x 512 slots, forward and dQ backward) against the fp16
         # MFMA peak.  `metric` and `value` stay the batched decode's.
-        out["prefill"] = measure_prefill(args.prefill_steps, 3, min(args.cpu_sample, 1))
+        out["prefill"] = measure_prefill(args.prefill_steps, 10, min(args.cpu_sample, 1))
     print(json.dumps(out), flush=True)
 
 
