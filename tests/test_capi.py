@@ -76,6 +76,20 @@ def test_host_side_validation_rejects_bad_sizes():
     assert joint() == -2
     assert joint(N=5) == -4
     assert L.xenc_joint_workspace_bytes(4, 4, 2, 4, 64) >= 4 * 4 * 2 * 4 * 64 * 4
+    # the prefill backward's readout with the routing term: d not a multiple of 64, NULL pointers,
+    # a dl row shorter than the chunk count, dl rows too long for 32-bit tile offsets, no tiles
+
+    def routed(**kw):
+        a = dict(G=1, n_tiles=1, d=64, cmax=2, ldl=2)
+        a.update(kw)
+        return L.xenc_prefill_readout_routed(None, 4, None, None, a["G"], a["n_tiles"], None, 64, a["d"], 64 * 64,
+                                             None, None, None, 2, None, 2, None, 0, None, a["cmax"], 10.0, None,
+                                             a["ldl"], None, 64, None)
+    assert routed(d=60) == -1
+    assert routed() == -2
+    assert routed(ldl=1) == -1
+    assert routed(ldl=1 << 25) == -1
+    assert routed(n_tiles=0) == 0
 
 
 def test_cpp_operators_registered():
