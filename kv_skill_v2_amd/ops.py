@@ -912,8 +912,8 @@ def library_read(q: torch.Tensor, lib_: PagedLibrary, plan: RowPlan, top_k: int 
     if not prefill_ok(lib_) and not _mfma_pages_ok(lib_):
         lib_.check_prefill()
     if prefill_ok(lib_) and plan.M >= ROUTE_ROWS_MIN and lib_.cmax <= 1024:
-        # routing and read as one autograd node (xenc::library_read_routed): the backward adds the
-        # routing term into the read's dq in place
+        # routing and read as one autograd node (xenc::library_read_routed): its backward writes dq
+        # once, with the routing term folded into the readout
         q = _query(q, lib_.d)
         if q.shape[0] != plan.M:
             raise ValueError(f"q must have {plan.M} rows")
@@ -1129,8 +1129,9 @@ def read_rows(q: torch.Tensor, w: torch.Tensor, idx: torch.Tensor, w_sel: torch.
 
 def branch_read(q: torch.Tensor, lib_: PagedLibrary, top_k: int = 0, read_temp: float = 12.0,
                 route_temp: float = 10.0, read_softmax: bool = True):
-    """(r [M, d_valid], w [M, C]): route_rows + read_rows; with autograd over many rows of a pool
-    the MFMA read takes directly, the two as one operator (library_read)."""
+    """(r [M, d_valid], w [M, C]): route_rows + read_rows.  Under autograd with at least
+    ROUTE_ROWS_MIN rows (and a pool the MFMA read takes), library_read instead: routing and read as
+    one operator."""
     _single(lib_)
     M = q.shape[0]
     if (torch.is_grad_enabled() and q.requires_grad and prefill_ok(lib_) and M >= ROUTE_ROWS_MIN
