@@ -395,26 +395,37 @@ __global__ __launch_bounds__(kSelectWaves * kWave) void route_rows_select_kernel
 }
 
 
-// Few query rows: one wave per (row, chunk) instead of one workgroup per row, so a handful of
-// rows still spreads over the whole GPU.  Each dot uses exactly the per-row kernel's arithmetic
-// (lane-owned float4 columns accumulated in block order, then the same xor butterfly), so the
-// dots, and hence the routing, are bit-identical to route_topk_kernel's.  Dots land in w_dense;
-// route_rows_select_kernel (with q_group) finishes.  Grid: (M, ceil(ldw / 8)); waves whose chunk
-// is past the row's library exit.
+// Few query rows: one wave per (row, two chunks) instead of one workgroup per row, so a handful
+// of rows still spreads over the whole GPU.  Each dot uses exactly the per-row kernel's
+// arithmetic (lane-owned float4 columns accumulated in block order, then the same xor
+// butterfly), so the dots, and hence the routing, are bit-identical to route_topk_kernel's.
+// Dots land in w_dense; route_rows_select_kernel (with q_group) finishes.  Grid:
+// (M, ceil(ldw / 16)) workgroups of 8 waves; waves whose chunks are past the row's library exit.
 template <int CB4>
 __global__ __launch_bounds__(8 * kWave) void route_dots_kernel(
     const float* __restrict__ q, long long ldq, int d, const float* __restrict__ S,
     const int* __restrict__ chunk_ptr, const int* __restrict__ q_group, int G,
     float* __restrict__ w_dense, int ldw) {
+  // Workgroup (m, y) covers chunks 16 y .. 16 y + 15 of row m: wave w forms the dots of chunks
+  // 16 y + w and 16 y + w + 8 from one round of loads (each summed as route_dot_wave sums it).
   const int m = blockIdx.x;
   const int lane = threadIdx.x & (kWave - 1);
-  const int c = blockIdx.y * 8 + (int)(threadIdx.x / kWave);
+  const int c = blockIdx.y * 16 + (int)(threadIdx.x / kWave), c2 = c + 8;
   const int g = min(max(q_group[m], 0), G - 1);
   const int c0 = chunk_ptr[g];
   const int C = min(chunk_ptr[g + 1] - c0, ldw);
-  if (c >= C) return;
-  const float a = route_dot_wave<CB4>(q + (long long)m * ldq, S + (long long)(c0 + c) * d, d, lane);
-  if (lane == 0) w_dense[(long long)m * ldw + c] = a;
+  if (c >= C) return;   // wave-uniform
+  const float* qrow = q + (long long)m * ldq;
+  if (c2 < C) {
+    const float2 x = route_dot2_wave<CB4>(qrow, S + (long long)(c0 + c) * d, S + (long long)(c0 + c2) * d, d, lane);
+    if (lane == 0) {
+      w_dense[(long long)m * ldw + c] = x.x;
+      w_dense[(long long)m * ldw + c2] = x.y;
+    }
+  } else {
+    const float a = route_dot_wave<CB4>(qrow, S + (long long)(c0 + c) * d, d, lane);
+    if (lane == 0) w_dense[(long long)m * ldw + c] = a;
+  }
 }
 
 int launch_route_select(int M, const int* chunk_ptr, const int* q_group, int G, int top_k,
@@ -430,7 +441,7 @@ int launch_route_select(int M, const int* chunk_ptr, const int* q_group, int G, 
 
 int launch_route_dots(const float* q, long long ldq, int M, int d, const float* S, const int* chunk_ptr,
                       const int* q_group, int G, float* w_dense, int ldw, hipStream_t st) {
-  const dim3 grid(M, (unsigned)((ldw + 7) / 8));
+  const dim3 grid(M, (unsigned)((ldw + 15) / 16));
   switch ((d + 255) / 256) {
 #define XENC_DOTS(N)                                                                             \
   case N:                                                                                        \
