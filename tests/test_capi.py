@@ -105,3 +105,21 @@ def test_cpp_operators_registered():
         assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "Meta"), name
     schema = str(torch.ops.xenc.route_read.default._schema)
     assert "Tensor(a!) workspace" in schema and schema.endswith("-> (Tensor, Tensor, Tensor, Tensor)")
+
+
+def test_python_operators_registered():
+    """The many-row operators (torch.library.custom_op in kv_skill_v2_amd.torch_ops) are in the
+    dispatcher with fake kernels, and the differentiable ones carry registered autograd."""
+    import torch
+
+    from kv_skill_v2_amd import torch_ops  # noqa: F401
+    names = ("route_rows", "route_backward_", "library_prefill_fwd", "library_prefill_lse", "library_prefill_bwd_dq",
+             "library_prefill_bwd_routed", "library_read_routed")
+    for name in names:
+        op = getattr(torch.ops.xenc, name).default
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "Meta"), name
+    for name in ("route_rows", "library_prefill_fwd", "library_read_routed"):
+        op = getattr(torch.ops.xenc, name).default
+        assert torch._C._dispatch_has_kernel_for_dispatch_key(op.name(), "Autograd"), name
+    schema = str(torch.ops.xenc.library_read_routed.default._schema)
+    assert schema.endswith("-> (Tensor, Tensor, Tensor, Tensor, Tensor)"), schema
