@@ -176,3 +176,45 @@ def test_graph_capture_through_torch_ops(dev):
         ref = step(q_new.clone())
         torch.cuda.synchronize()
         assert torch.equal(r_g, ref), seed
+
+
+def test_graph_capture_of_prefill_training_step(dev):
+    """A whole training step of the routed MFMA read (xenc::library_read_routed forward and its
+    backward through autograd) captured once in a HIP graph, as whole-network capture does it
+    (grads set to None before the capture), then replayed for new query rows written into the
+    captured leaf: r and q.grad of every replay equal an eager step bit for bit, with eager work
+    and synchronisation between the replays."""
+    say("graph capture of a prefill training step")
+    P, lib = _pool(dev, counts=(5, 3), N=128, d=256)
+    plan = ops.row_plan(lib, [80, 70])
+    g_up = torch.randn(plan.M, lib.d, generator=torch.Generator(device=dev).manual_seed(3), device=dev)
+    q_leaf = synth.queries(plan.M, lib.d, device=dev, seed=9).requires_grad_(True)
+
+    def step(q):
+        r, w = ops.library_read(q, lib, plan, top_k=2)
+        ((r * g_up).sum() + (w * w).sum()).backward()
+        return r
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            q_leaf.grad = None
+            step(q_leaf)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    q_leaf.grad = None
+    gph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gph):
+        r_g = step(q_leaf)
+    for seed in (21, 22, 23):
+        q_new = synth.queries(plan.M, lib.d, device=dev, seed=seed)
+        with torch.no_grad():
+            q_leaf.copy_(q_new)
+        gph.replay()
+        torch.cuda.synchronize()
+        q_ref = q_new.clone().requires_grad_(True)
+        r_ref = step(q_ref)
+        torch.cuda.synchronize()
+        assert torch.equal(r_g, r_ref), seed
+        assert torch.equal(q_leaf.grad, q_ref.grad), (seed, float((q_leaf.grad - q_ref.grad).abs().max()))
