@@ -285,7 +285,7 @@ def test_make_interface_noop_and_shapes():
     hn = rms_norm(torch.randn(2, 5, 40))
     assert itf.query(hn).shape == (2, 5, 24) and itf.gate(hn, 6).shape == (2, 5, 1)
     assert torch.equal(itf.write(torch.randn(2, 5, 24)), torch.zeros(2, 5, 40))
-    assert float(itf.gain(4)) == 1.0
+    assert float(itf.gain(4).detach()) == 1.0
     assert torch.allclose(itf.gate_b, torch.full((4,), -2.0)) and torch.equal(itf.log_gain, torch.zeros(4))
     assert itf._pos == {2: 0, 4: 1, 6: 2, 7: 3}
     with pytest.raises(ValueError):
