@@ -238,14 +238,19 @@ __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
 // q . S dots of a 32-row x 32-chunk tile are one fp32 GEMM tile on MFMA (each summary row is read
 // once per 32 query rows instead of once per row).  k steps of 128 are staged through LDS (row
 // stride 132 floats) with coalesced loads, the next step's global loads in flight while the
-// current step computes; wave w multiplies columns [32w, 32w + 32) of every step with
-// v_mfma_f32_32x32x2f32, and the 4 partial tiles are summed through LDS in wave order.  The raw
+// current step computes; wave w of 8 multiplies columns [16w, 16w + 16) of every step with
+// v_mfma_f32_32x32x2f32 (two waves per SIMD: two independent accumulation chains), and the 8
+// partial tiles are summed through LDS in wave order.  Workgroup b starts its k-loop at step
+// b mod (d / 128) and wraps around: when every workgroup walked its rows from column 0 in step,
+// the grid read the same 512-byte window of every q row at once (33.0 against 26.5 us for the
+// 8192 x 32 x 2048 prefill routing, with the 8 waves).  The raw
 // dots land in w_dense; route_rows_select_kernel then runs the same top-k + softmax as the
 // per-row kernel, one wave per row.  Fixed summation order per (row, chunk).  When qh is given,
 // the first chunk tile of each row tile also writes the rows it stages as fp16 (qh [M, d]), the
 // operand of the MFMA read, so q is read from HBM once for both.
 constexpr int kRouteRows = 32, kRouteChunks = 32, kRouteK = 128, kRouteLd = kRouteK + 4;
-constexpr int kRouteLoads = kRouteRows * kRouteK / 4 / 256;   // float4 per thread per operand
+constexpr int kRouteThreads = 512;
+constexpr int kRouteLoads = kRouteRows * kRouteK / 4 / kRouteThreads;   // float4 per thread per operand
 
 __device__ __forceinline__ int find_tile_group(const int* __restrict__ tile_ptr, int G, int b) {
   int lo = 0, hi = G - 1;
@@ -256,13 +261,14 @@ __device__ __forceinline__ int find_tile_group(const int* __restrict__ tile_ptr,
   return lo;
 }
 
-__global__ __launch_bounds__(256) void route_rows_logits_kernel(
+__global__ __launch_bounds__(kRouteThreads) void route_rows_logits_kernel(
     const float* __restrict__ q, long long ldq, int d, const float* __restrict__ S,
     const int* __restrict__ chunk_ptr, const int* __restrict__ row_ptr,
     const int* __restrict__ tile_ptr, int G, float* __restrict__ w_dense, long long ldw,
     _Float16* __restrict__ qh) {
-  __shared__ float qs[kRouteRows * kRouteLd];
-  __shared__ float ss[kRouteChunks * kRouteLd];
+  __shared__ float lds_rl[(kRouteRows + kRouteChunks) * kRouteLd];   // q rows | S rows; partials
+  float* const qs = lds_rl;
+  float* const ss = lds_rl + kRouteRows * kRouteLd;
   const int b = blockIdx.x;
   const int g = find_tile_group(tile_ptr, G, b);
   const int rbeg = row_ptr[g], rend = row_ptr[g + 1];
@@ -280,21 +286,30 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
   int lrow[kRouteLoads], lk[kRouteLoads];
 #pragma unroll
   for (int i = 0; i < kRouteLoads; ++i) {
-    const int id = tid + 256 * i;
+    const int id = tid + kRouteThreads * i;
     lrow[i] = id / (kRouteK / 4);
     lk[i] = (id % (kRouteK / 4)) * 4;
     qsrc[i] = q + (long long)min(row0 + lrow[i], rend - 1) * ldq + lk[i];
     ssrc[i] = S + (long long)(c0 + min(cb0 + lrow[i], C - 1)) * d + lk[i];
   }
-  // Four register slots: the loads of k-step j go out three steps ahead, during the MFMAs of
-  // step j - 3 (one step of MFMAs is much shorter than a memory round trip).  Every step is
-  // unconditional, so each slot keeps its registers through the loop: the k-loop runs a multiple
-  // of four steps, and steps past d load clamped addresses and store zeros.  Columns past d
-  // (d % 4 == 0, so a float4 is all in or all out) are zeroed at the store the same way, never
-  // by a masked load, which the compiler would wait for on the spot.
-  constexpr int NS = 4;
+  // Two register slots: the loads of k-step j go out during the MFMAs of step j - 2, right after
+  // the slot's previous contents were stored (8 waves keep 32 KiB of q and S rows in flight per
+  // workgroup; four slots measured no faster).  Every step is unconditional, so each slot keeps
+  // its registers through the loop: the k-loop runs a multiple of NS steps, and steps past d load
+  // clamped addresses and store zeros.  Columns past d (d % 4 == 0, so a float4 is all in or all
+  // out) are zeroed at the store the same way, never by a masked load, which the compiler would
+  // wait for on the spot.
+  constexpr int NS = 2;
   float4 qv[NS][kRouteLoads], sv[NS][kRouteLoads];
-  auto load = [&](int slot, int k0) {
+  // Loop step v reads k-step kreal(v) = (v + rot) % nreal (v < nreal; later steps are past d).
+  const int nreal = (d + kRouteK - 1) / kRouteK;
+  const int rot = b % nreal;
+  auto kreal = [&](int kv) {
+    const int v = kv / kRouteK;
+    return v < nreal ? ((v + rot) % nreal) * kRouteK : kv;
+  };
+  auto load = [&](int slot, int kv) {
+    const int k0 = kreal(kv);
 #pragma unroll
     for (int i = 0; i < kRouteLoads; ++i) {
       const int k = min(k0, d - 4 - lk[i]);
@@ -309,7 +324,8 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
   const bool write_h = qh != nullptr && cb0 == 0;
   f32x16 acc = {};
   // One k-step from register slot `slot` (a constant after inlining).
-  auto step = [&](int slot, int k0) {
+  auto step = [&](int slot, int kv) {
+    const int k0 = kreal(kv);
     __syncthreads();   // the previous step's LDS reads are done
 #pragma unroll
     for (int i = 0; i < kRouteLoads; ++i) {
@@ -326,10 +342,10 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
       }
     }
     __syncthreads();
-    load(slot, k0 + NS * kRouteK);   // this slot is stored: refill it NS steps ahead
+    load(slot, kv + NS * kRouteK);   // this slot is stored: refill it NS steps ahead
     // Lane l feeds row / chunk l % 32 and columns kb + 4 (l / 32) .. + 3 to four MFMAs: MFMA i
     // contracts column kb + 4h + i of both operands for lane half h.
-    constexpr int kPerWave = kRouteK / 4;
+    constexpr int kPerWave = kRouteK / (kRouteThreads / kWave);
 #pragma unroll
     for (int kq = 0; kq < kPerWave; kq += 8) {
       const int kb = wv * kPerWave + kq + hl * 4;
@@ -345,16 +361,19 @@ __global__ __launch_bounds__(256) void route_rows_logits_kernel(
 #pragma unroll
     for (int j = 0; j < NS; ++j) step(j, k0 + j * kRouteK);
   }
-  // acc[r] = partial dot of row 8(r/4) + 4hl + r%4, chunk l32.  Sum the 4 waves in order.
+  // acc[r] = partial dot of row 8(r/4) + 4hl + r%4, chunk l32.  Sum the 8 waves in order.
+  constexpr int NWV = kRouteThreads / kWave;
+  static_assert(NWV * 16 * kWave <= (kRouteRows + kRouteChunks) * kRouteLd, "partials fit");
   __syncthreads();
-  float* red = qs;   // 4 waves x 16 values x 64 lanes <= 32 x 132 floats
+  float* red = lds_rl;
 #pragma unroll
   for (int r = 0; r < 16; ++r) red[(wv * 16 + r) * kWave + lane] = acc[r];
   __syncthreads();
-  for (int i = tid; i < 16 * kWave; i += 256) {
+  for (int i = tid; i < 16 * kWave; i += kRouteThreads) {
     const int r = i / kWave, ln = i % kWave;
-    const float v = ((red[(0 * 16 + r) * kWave + ln] + red[(1 * 16 + r) * kWave + ln]) +
-                     red[(2 * 16 + r) * kWave + ln]) + red[(3 * 16 + r) * kWave + ln];
+    float v = red[r * kWave + ln];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) v += red[(w * 16 + r) * kWave + ln];
     const int row = row0 + (r >> 2) * 8 + (ln >> 5) * 4 + (r & 3);
     const int c = cb0 + (ln & 31);
     if (row < rend && c < C) w_dense[(long long)row * ldw + c] = v;
@@ -520,7 +539,7 @@ extern "C" int xenc_route_topk_rows(const float* q, long long ldq, int M, int d,
   if (q_f16 && !aligned16(q_f16)) return XENC_EALIGN;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (n_tiles > 0)
-    hipLaunchKernelGGL(route_rows_logits_kernel, dim3(n_tiles), dim3(256), 0, st, q, ldq, d, S,
+    hipLaunchKernelGGL(route_rows_logits_kernel, dim3(n_tiles), dim3(kRouteThreads), 0, st, q, ldq, d, S,
                        chunk_ptr, row_ptr, tile_ptr, G, w_dense, ldw, static_cast<_Float16*>(q_f16));
   hipLaunchKernelGGL(route_rows_select_kernel, dim3((M + kSelectWaves - 1) / kSelectWaves),
                      dim3(kSelectWaves * kWave), lds, st, M, chunk_ptr, row_ptr, nullptr, G, top_k,
