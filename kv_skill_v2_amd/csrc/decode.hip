@@ -56,9 +56,14 @@
 #ifndef XENC_DECODE_MIN_WAVES
 #define XENC_DECODE_MIN_WAVES 1
 #endif
+// The many-unit 4-wave launches at d <= 2048 step 2 slot rows per wave (8 KiB per wave step at
+// d = 2048: the B = 64 batched decode's read 165.1-165.3 against 166.6 us with 4 rows); the
+// few-unit 8-wave launches keep XENC_DECODE_SPT.
 // Measured and not kept (B = 64 batched decode, same box): two register tiles per wave with the
-// next one loading while the current one is consumed (184-185 us, no change), and score dots with
-// q rounded to fp16 through v_dot2_f32_f16 (no faster; moves scores by ~1e-5).
+// next one loading while the current one is consumed (184-185 us, no change; measured again on
+// the current kernel: step 182.8 against 175.8 us, the single decode 17.3 against 16.6 us, the
+// multi-depth step 251 against 238 us: more loads in flight per wave only lengthen the queues),
+// and score dots with q rounded to fp16 through v_dot2_f32_f16 (no faster; moves scores by ~1e-5).
 
 namespace xenc {
 
@@ -617,7 +622,10 @@ static void launch_read(dim3 grid, size_t lds, hipStream_t st, const float* q, l
                         const int* q_group, int G, const int* idx, const float* w_sel, int kk,
                         int nsplit, int split_slots, float scale2, int softmax, float* r,
                         long long ldr, const DecodeWorkspace& ws, int grouped, const RouteFuse& rf) {
-  constexpr int SPT = CB <= 4 ? XENC_DECODE_SPT : (CB == 5 ? XENC_DECODE_SPT_WIDE : 1);
+  constexpr int SPT = CB == 4 && NW == XENC_DECODE_NW_STREAM ? 2
+                      : CB <= 4                                 ? XENC_DECODE_SPT
+                      : CB == 5                                 ? XENC_DECODE_SPT_WIDE
+                                                                : 1;
   hipLaunchKernelGGL((decode_read_kernel<CB, SPT, NW>), grid, dim3(NW * kWave), lds, st, q, ldq,
                      d, pages, page_stride, spp, chunk_page, chunk_nvalid, chunk_ptr, q_group, G,
                      const_cast<int*>(idx), const_cast<float*>(w_sel), kk, nsplit, split_slots, scale2,
