@@ -303,6 +303,32 @@ def test_repeated_calls_are_bit_identical(dev):
         assert torch.equal(ops.library_read_decode(q, lib, idx, wsel, qg, nsplit=ns), ref[ns]), (rep, ns)
 
 
+@pytest.mark.parametrize("fused", [False, True])
+def test_large_launch_rows_equal_single_row_reads(dev, fused):
+    """A launch of at least 256 workgroups (64 rows x 8 routed pages: 4-wave workgroups, partials
+    merged by merge_kernel over whole rows) against the same rows read one call each (8-wave
+    workgroups, the merge split over column slices; another per-workgroup summation order, hence
+    a 1e-5 bound).  Twelve calls in a row, each on new queries, so a partial left from an earlier
+    call would show; with the routing folded into the read too (idx / w_sel written by it)."""
+    say("large launch vs single rows", dict(M=64, top_k=8, fused=fused))
+    counts = [8 + (7 * i) % 17 for i in range(64)]
+    P = synth.pool(counts, 256, 1024, device="cpu", tail_lo=1)
+    lib = _to_lib(P, dev)
+    qg = torch.arange(64, dtype=torch.int32, device=dev)
+    for rep in range(12):
+        q = synth.queries(64, 1024, device="cpu", seed=500 + rep).to(dev)
+        if fused:
+            _, idx, wsel, r = ops.route_read_decode(q, lib, qg, top_k=8)
+        else:
+            _, idx, wsel = ops.route_topk(q, lib, qg, top_k=8)
+            r = ops.library_read_decode(q, lib, idx, wsel, qg)
+        rows = torch.cat([ops.library_read_decode(q[m:m + 1], lib, idx[m:m + 1], wsel[m:m + 1], qg[m:m + 1])
+                          for m in range(64)])
+        torch.cuda.synchronize()
+        err = (r - rows).abs().max().item()
+        assert err <= 1e-5 * rows.abs().max().item(), (rep, err)
+
+
 def test_graph_capture_and_replay(dev):
     """Route + read captured in a HIP graph and replayed several times with eager work and new
     query values in between; every replay equals the eager result for the same inputs."""
