@@ -63,7 +63,7 @@ constexpr int kSchedMfma = 0x008, kSchedVmemRead = 0x020, kSchedDsRead = 0x100;
 __device__ __forceinline__ void stage_to_lds(_Float16* lds_wave_base, const _Float16* src) {
   const unsigned lds = __builtin_amdgcn_readfirstlane(
       (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_wave_base);
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory");
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(src) : "memory", "m0");
 }
 
 // Wait until at most N vector-memory operations of this wave are outstanding (they complete in
