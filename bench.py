@@ -49,12 +49,12 @@ def parse():
     return ap.parse_args()
 
 
-def traffic_from_profile(workload: str):
-    """HBM bytes per launch of the read kernel measured offline with rocprofv3 --pmc
+def traffic_from_profile(workload: str, name: str | None = None):
+    """HBM bytes per launch of the workload's kernels measured offline with rocprofv3 --pmc
     (FETCH_SIZE and WRITE_SIZE, scaled by the same counters on a copy of known size); the
     summary lives in profiles/ next to the command that produced it.  None when absent."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        f"decode_read_{workload}_traffic.json")
+                        name or f"decode_read_{workload}_traffic.json")
     try:
         with open(path) as f:
             return json.load(f)
@@ -383,6 +383,7 @@ def bench_prefill(args):
     """The prefill/registration read (measure_prefill) as its own JSON line."""
     pf = measure_prefill(args.steps, args.warmup, args.cpu_sample)
     fwd_tf = pf["fwd"]["tflops"]
+    traffic = traffic_from_profile("prefill", "prefill_read_traffic.json")
     out = {
         "metric": "Prefill/registration read TFLOP/s (fwd and dQ bwd), 4 docs x 2048 rows x 32x512 slots",
         "value": pf["tflops_fwd_bwd"], "unit": "TFLOP/s (fwd+bwd)", "n_gpus": 1,
@@ -392,7 +393,9 @@ def bench_prefill(args):
         "fwd": pf["fwd"], "bwd": pf["bwd"],
         "roofline": {"bound": "mfma", "kernel": "scores_kernel + readout_kernel (fwd)",
                      "achieved": fwd_tf, "peak": MFMA_FP16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS, "traffic": None,
+                     "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS,
+                     "traffic": traffic["bytes_per_launch"] if traffic else None,
+                     "traffic_source": traffic["source"] if traffic else None,
                      "algorithmic_flops": pf["algorithmic_flops_per_direction"],
                      "measured_peak": pf["measured_peak_tflops"],
                      "frac_of_measured": pf["fwd"]["frac_of_measured"]},
