@@ -464,9 +464,17 @@ JointLayout joint_layout(int max_n, int N, int hkv, int nsplit, int g, int d) {
 // MFMA form for head dims 128 and 256 (fp16 / bf16 pools, G <= 8).  Same split, launch order,
 // partial layout and merge as joint_read_kernel; inside a split, wave w takes the 16-key tiles
 // w, w + 4, ... of its range.
+//   Loads (WIDE: launches of 256 or more workgroups): the tile's K rows are read whole (each load
+//   instruction covers 512 / D key rows, D / 8 lanes a row, 16 bytes a lane), as the V rows are,
+//   and every pool load is nontemporal (each row is read once); a stream-only probe of this shape
+//   read the same bytes at 6.8-6.9 TB/s this way against 6.1 TB/s with K straight in the MFMA
+//   layout (16 rows x 64 bytes per instruction).  Smaller, latency-bound launches load K in the
+//   MFMA layout directly, with the default policy (the clamped re-reads of a split's last key then
+//   hit in cache): the LDS round trips of the whole-row form cost them more than the loads gain.
 //   Scores: one v_mfma_f32_16x16x32 per 32 dims, A = the tile's 16 key rows (lane l: key l % 16,
-//   dims 8 (l / 16) .. +8 of each 32-dim block), B = q^T (lane l: query head l % 16 of the kv
-//   head, zero past G), so lane l receives the scores of keys 4 (l / 16) + i, head l % 16.
+//   dims 8 (l / 16) .. +8 of each 32-dim block; WIDE: read back from the wave's LDS rows), B = q^T (lane
+//   l: query head l % 16 of the kv head, zero past G), so lane l receives the scores of keys
+//   4 (l / 16) + i, head l % 16.
 //   Softmax: per head in the log2 domain over the tile (max and sum across the four lanes of a
 //   head by the permlane swaps), one accumulator rescale per tile.
 //   Values: lane l owns dims l * D/64 .. +D/64 of every head; the tile's weights and V row
@@ -475,6 +483,13 @@ JointLayout joint_layout(int max_n, int N, int hkv, int nsplit, int g, int d) {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+
+template <bool NT, typename V>
+__device__ __forceinline__ V load_pool(const void* p) {
+  if constexpr (NT) return __builtin_nontemporal_load(reinterpret_cast<const V*>(p));
+  return *reinterpret_cast<const V*>(p);
+}
 
 template <typename T>
 __device__ __forceinline__ f32x4_t mfma16x16x32(const u32x4_t& a, const u32x4_t& b, f32x4_t c) {
@@ -496,12 +511,18 @@ __device__ __forceinline__ float half_to_f32(unsigned bits16) {
 
 constexpr int kTileKeys = 16;
 
-template <typename T, int G, int D>
+template <typename T, int G, int D, bool WIDE>
 __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArgs A) {
-  constexpr int KB = D / 32;    // 32-dim blocks of a key row
+  constexpr int KB = D / 32;    // 32-dim blocks of a key row; also K load instructions per tile
   constexpr int DPL = D / 64;   // value dims per lane
+  constexpr int LPR = D / 8;    // lanes per key row in the whole-row K loads
+  constexpr int KPI = 64 / LPR; // key rows per K load instruction
+  constexpr int KLD = D / 2 + 8;  // words per staged K row: 8 mod 64, so neither the row stores
+                                  // (LPR lanes a row) nor the MFMA-layout reads conflict
   static_assert(D == 128 || D == 256, "the MFMA form covers head dims 128 and 256");
+  static_assert(KB * KPI == kTileKeys, "one tile's K rows in KB load instructions");
   __shared__ float lds_acc[2][G][D];
+  __shared__ __align__(16) unsigned lds_k[WIDE ? kJointWaves : 1][kTileKeys][WIDE ? KLD : 4];   // tile K rows
   __shared__ float lds_ml[2][G][2];
   __shared__ __align__(16) float lds_p[kJointWaves][kTileKeys][8];   // tile weights [key][head]
   __shared__ long long lds_v[kJointWaves][kTileKeys];   // tile V rows: offset, own pool as ~offset
@@ -579,22 +600,33 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
   auto issue = [&](int blk, int row, bool ow, u32x4_t (&kf)[KB], unsigned (&vraw)[kTileKeys][DPL / 2]) {
     const unsigned long long off = ow ? (unsigned long long)(unsigned)blk * own_sb + (row * own_ss + own_h)
                                       : (unsigned long long)(unsigned)blk * op_sb + (row * op_ss + op_h);
-    const T* kp = (ow ? owk : opk) + off;
+    if constexpr (!WIDE) {   // this lane's key row, straight in the MFMA layout
+      const T* kp = (ow ? owk : opk) + off;
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) kf[kb] = *reinterpret_cast<const u32x4_t*>(kp + kb * 32 + 8 * lq);
+      for (int kb = 0; kb < KB; ++kb) kf[kb] = *reinterpret_cast<const u32x4_t*>(kp + kb * 32 + 8 * lq);
+    }
     if (lq == 0) lds_v[wv][l16] = ow ? ~(long long)off : (long long)off;
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
+    if constexpr (WIDE) {
+      // K rows whole: instruction j covers keys KPI j .. KPI j + KPI - 1, lane l key KPI j + l / LPR,
+      // dims 8 (l % LPR) .. +8 (staged to the MFMA layout when the tile is consumed).
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        const long long ko = lds_v[wv][j * KPI + lane / LPR];
+        kf[j] = load_pool<true, u32x4_t>((ko < 0 ? owk + ~ko : opk + ko) + (lane % LPR) * 8);
+      }
+    }
 #pragma unroll
     for (int k = 0; k < kTileKeys; ++k) {
       const long long vo = lds_v[wv][k];
       const T* vr = (vo < 0 ? owv + ~vo : opv + vo) + lane * DPL;
       if constexpr (DPL == 4) {
-        const uint2 v2 = *reinterpret_cast<const uint2*>(vr);
-        vraw[k][0] = v2.x;
-        vraw[k][1] = v2.y;
+        const u32x2_t v2 = load_pool<WIDE, u32x2_t>(vr);
+        vraw[k][0] = v2[0];
+        vraw[k][1] = v2[1];
       } else {
-        vraw[k][0] = *reinterpret_cast<const unsigned*>(vr);
+        vraw[k][0] = load_pool<WIDE, unsigned>(vr);
       }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -602,9 +634,25 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
   };
   // Scores, softmax and values of tile tb from its loaded fragments.
   auto consume = [&](int tb, const u32x4_t (&kf)[KB], const unsigned (&vraw)[kTileKeys][DPL / 2]) {
+    // WIDE: the tile's K rows through this wave's LDS rows, stored as loaded and read back in the
+    // MFMA layout (lane l: row l % 16, dims kb * 32 + 8 (l / 16) .. +8).
+    u32x4_t ka[KB];
+    if constexpr (WIDE) {
+#pragma unroll
+      for (int j = 0; j < KB; ++j)
+        *reinterpret_cast<u32x4_t*>(&lds_k[wv][j * KPI + lane / LPR][(lane % LPR) * 4]) = kf[j];
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) ka[kb] = *reinterpret_cast<const u32x4_t*>(&lds_k[wv][l16][kb * 16 + 4 * lq]);
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) ka[kb] = kf[kb];
+    }
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) sacc = mfma16x16x32<T>(kf[kb], qf[kb], sacc);
+    for (int kb = 0; kb < KB; ++kb) sacc = mfma16x16x32<T>(ka[kb], qf[kb], sacc);
     float sv[4];
     bool ok[4];
     float mt = -INFINITY;
@@ -738,10 +786,15 @@ __global__ __launch_bounds__(kJointThreads) void joint_read_mfma_kernel(JointArg
 
 template <typename T, int G>
 void launch_joint_g(dim3 grid, hipStream_t st, const JointArgs& a) {
-  if (a.d == 256)
-    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 256>), grid, dim3(kJointThreads), 0, st, a);
+  // Whole-row nontemporal pool loads in the two-pass (large) launches only.
+  if (a.d == 256 && a.two_pass)
+    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 256, true>), grid, dim3(kJointThreads), 0, st, a);
+  else if (a.d == 256)
+    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 256, false>), grid, dim3(kJointThreads), 0, st, a);
+  else if (a.d == 128 && a.two_pass)
+    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 128, true>), grid, dim3(kJointThreads), 0, st, a);
   else if (a.d == 128)
-    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 128>), grid, dim3(kJointThreads), 0, st, a);
+    hipLaunchKernelGGL((joint_read_mfma_kernel<T, G, 128, false>), grid, dim3(kJointThreads), 0, st, a);
   else if (a.tpr == 32)
     hipLaunchKernelGGL((joint_read_kernel<T, G, 32>), grid, dim3(kJointThreads), 0, st, a);
   else if (a.tpr == 16)
