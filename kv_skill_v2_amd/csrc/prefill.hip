@@ -20,7 +20,9 @@
 //   layout B [P][d/32][N/16][64][8]: lane l of block (db, nb) = K[16nb + 8(l/32) + e][32db + l%32]
 // The probabilities p and the backward dS are stored octet-major, [C*N/8][M][8] (8 slots of a
 // row in 16 bytes, rows fastest), so the scores epilogue writes 512 contiguous bytes per
-// instruction and the readout stages them with contiguous row loads.
+// instruction and the readout stages them with contiguous row loads.  The scores epilogues store
+// them (and the backward's reads p) nontemporally: each element passes there once, and the L2
+// keeps the page fragments and query rows the XCD's other tiles reuse.
 //
 // The scores tile covers a whole chunk (512 slots) x 128 query rows, so the chunk softmax is
 // local to the workgroup; S^T is formed (slots as the MFMA M dimension) so that each lane holds 32
@@ -313,7 +315,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e)
               h[e] = (_Float16)(s0 + e < nv ? acc[mt][nt][q4 * 4 + e] * inv : 0.f);
-            *reinterpret_cast<half4_t*>(P + poff(t, s0)) = h;
+            __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(P + poff(t, s0)));
           }
         }
     }
@@ -389,7 +391,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
                          (_Float16)(acc[mt][nt][q4 * 4 + 1] * rsum[nt]),
                          (_Float16)(acc[mt][nt][q4 * 4 + 2] * rsum[nt]),
                          (_Float16)(acc[mt][nt][q4 * 4 + 3] * rsum[nt])};
-            *reinterpret_cast<half4_t*>(P + poff(t, s0)) = h;
+            __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(P + poff(t, s0)));
           }
         }
     }
@@ -406,7 +408,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const int s0 = slot_of(mt, q4 * 4);
-          pv[mt][nt][q4] = s0 < N ? *reinterpret_cast<const half4_t*>(P + poff(t, s0)) : (half4_t){};
+          pv[mt][nt][q4] = s0 < N ? __builtin_nontemporal_load(reinterpret_cast<const half4_t*>(P + poff(t, s0))) : (half4_t){};
 #pragma unroll
           for (int e = 0; e < 4; ++e) s += (float)pv[mt][nt][q4][e] * acc[mt][nt][q4 * 4 + e];
         }
@@ -438,7 +440,7 @@ __global__ __launch_bounds__(512) void scores_kernel(
               h[e] = (_Float16)(MODE == 1 ? coef * (float)pv[mt][nt][q4][e] * (u - s)
                                           : (s0 + e < nv ? coef * u : 0.f));
             }
-            *reinterpret_cast<half4_t*>(dS + poff(t, s0)) = h;
+            __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(dS + poff(t, s0)));
           }
         }
     }
