@@ -96,9 +96,10 @@ __global__ void cast_rows_f16_kernel(const float* __restrict__ x, long long ldx,
   for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n4;
        i += (long long)gridDim.x * blockDim.x) {
     const long long row = i / (d / 4), col = (i % (d / 4)) * 4;
-    const float4 v = *reinterpret_cast<const float4*>(x + row * ldx + col);
-    half4_t h = {(_Float16)v.x, (_Float16)v.y, (_Float16)v.z, (_Float16)v.w};
-    *reinterpret_cast<half4_t*>(y + row * d + col) = h;
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    const f32x4v v = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(x + row * ldx + col));
+    const half4_t h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
+    __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(y + row * d + col));
   }
 }
 
@@ -650,7 +651,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void r
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const int dd = d0 + wv * 64 + nt * 32 + l32;
-        if (dd < d) out[(long long)t * ldo + dd] = acc[mt][nt][r];
+        if (dd < d) __builtin_nontemporal_store(acc[mt][nt][r], &out[(long long)t * ldo + dd]);
       }
     }
 }

@@ -249,6 +249,7 @@ __global__ __launch_bounds__(NW* kWave) void route_topk_kernel(
 // the first chunk tile of each row tile also writes the rows it stages as fp16 (qh [M, d]), the
 // operand of the MFMA read, so q is read from HBM once for both.
 constexpr int kRouteRows = 32, kRouteChunks = 32, kRouteK = 128, kRouteLd = kRouteK + 4;
+typedef float f32x4nt __attribute__((ext_vector_type(4)));
 constexpr int kRouteThreads = 512;
 constexpr int kRouteLoads = kRouteRows * kRouteK / 4 / kRouteThreads;   // float4 per thread per operand
 
@@ -313,7 +314,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_rows_logits_kernel(
 #pragma unroll
     for (int i = 0; i < kRouteLoads; ++i) {
       const int k = min(k0, d - 4 - lk[i]);
-      qv[slot][i] = *reinterpret_cast<const float4*>(qsrc[i] + k);
+      qv[slot][i] = __builtin_bit_cast(float4, __builtin_nontemporal_load(reinterpret_cast<const f32x4nt*>(qsrc[i] + k)));
       sv[slot][i] = *reinterpret_cast<const float4*>(ssrc[i] + k);
     }
   };
@@ -338,7 +339,7 @@ __global__ __launch_bounds__(kRouteThreads) void route_rows_logits_kernel(
       if (write_h && in && row < rend) {
         typedef _Float16 half4 __attribute__((ext_vector_type(4)));
         const half4 h = {(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w};
-        *reinterpret_cast<half4*>(qh + (long long)row * d + k0 + lk[i]) = h;
+        __builtin_nontemporal_store(h, reinterpret_cast<half4*>(qh + (long long)row * d + k0 + lk[i]));
       }
     }
     __syncthreads();
