@@ -52,13 +52,14 @@ class DecodeReader:
         self.G, self.hq, self.hkv, self.d = hq // hkv, int(hq), int(hkv), int(d)
         if not 1 <= self.G <= 8 or d % 8 or d > 512 or self.G * d > 4096:
             raise DecodeReaderError(f"unsupported head layout: G={self.G} (1..8), d={d} (multiple of 8, <= 512)")
-        if chunk is None:
-            chunk = self.auto_chunk(max_n, hkv, max_keys)
-        self.max_n, self.chunk, self.block_n = int(max_n), int(chunk), int(block_n)
-        self.S = max(1, math.ceil(max_keys / self.chunk))
         device = torch.device(device)
         if device.type != "cuda":
             raise DecodeReaderDeviceError("DecodeReader runs only on a ROCm GPU (there is no CPU path)")
+        if chunk is None:
+            cus = torch.cuda.get_device_properties(device).multi_processor_count
+            chunk = self.auto_chunk(max_n, hkv, max_keys, cus)
+        self.max_n, self.chunk, self.block_n = int(max_n), int(chunk), int(block_n)
+        self.S = max(1, math.ceil(max_keys / self.chunk))
         L = lib()
         nbytes = L.xenc_joint_workspace_bytes(self.max_n, self.hkv, self.S, self.G, self.d)
         self.workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
@@ -68,13 +69,18 @@ class DecodeReader:
         self.device = device
 
     @staticmethod
-    def auto_chunk(max_n: int, hkv: int, max_keys: int) -> int:
-        """Keys per split for about 1024 workgroups at full capacity (max_n rows x hkv heads x
-        splits), at least 512 keys, a multiple of 64 (the MFMA read's 16-key tiles over 4 waves).
-        At hkv 4 and 16,448 keys: 32 rows get 2,112 keys (0.41 ms against 0.49 ms at 1,024) and
-        one row 512 (37 us against 43 us at 256 and 48 us at 1,024)."""
-        want = max(1, -(-1024 // max(1, int(max_n) * int(hkv))))
-        chunk = max(512, -(-int(max_keys) // want))
+    def auto_chunk(max_n: int, hkv: int, max_keys: int, cus: int = 256) -> int:
+        """Keys per split: as many splits as keep a full-capacity launch (max_n rows x hkv heads x
+        splits) at one workgroup per CU at most, with at least 512 keys per split, a multiple of 64
+        (the MFMA read's 16-key tiles over 4 waves).  At hkv 4 and 16,448 keys on 256 CUs (hq 16,
+        d 256, bf16; the wall clock of 50 calls, three runs each): 32 rows get 8,256 keys (256
+        workgroups, 321 us against 326 us at 512 workgroups, 332 us at 1,024 and 362 us at 384),
+        8 rows 2,112 (90 us against 94 us at 512 and 105 us at 928), 4 rows 1,088 (54 us against
+        61 us at 464), one row 512 (132 workgroups, 35-36 us against 37 us at 172 and 39 us at
+        208).  Workgroup counts that do not divide evenly over the CUs leave a ragged last round."""
+        units = max(1, int(max_n) * int(hkv))
+        splits = max(1, int(cus) // units)
+        chunk = max(512, -(-int(max_keys) // splits))
         return -(-chunk // 64) * 64
 
     @staticmethod

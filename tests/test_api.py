@@ -316,14 +316,20 @@ def test_save_load_roundtrip(tmp_path):
 
 
 def test_decode_reader_auto_chunk():
-    """DecodeReader's split size (host logic): about 1024 workgroups at capacity, >= 512 keys,
-    a multiple of 64, and splits that cover max_keys."""
+    """DecodeReader's split size (host logic): at most one workgroup per CU at capacity (or one
+    split per (row, head) when even that is more), >= 512 keys, a multiple of 64, and splits
+    that cover max_keys."""
     import math
     from kv_skill_v2_amd.decode_reader import DecodeReader
-    assert DecodeReader.auto_chunk(32, 4, 16448) == 2112
-    assert DecodeReader.auto_chunk(1, 4, 16448) == 512
-    for max_n, hkv, mk in [(32, 4, 16448), (1, 4, 16448), (8, 4, 2048), (4, 16, 512), (256, 8, 100000), (1, 1, 1)]:
-        c = DecodeReader.auto_chunk(max_n, hkv, mk)
-        S = math.ceil(mk / c)
-        assert c >= 512 and c % 64 == 0 and S * c >= mk
-        assert max_n * hkv * S <= max(1024, max_n * hkv), (max_n, hkv, mk, c)
+    assert DecodeReader.auto_chunk(32, 4, 16448) == 8256      # 2 splits: 256 workgroups
+    assert DecodeReader.auto_chunk(8, 4, 16448) == 2112       # 8 splits: 256 workgroups
+    assert DecodeReader.auto_chunk(4, 4, 16448) == 1088       # 16 splits: 256 workgroups
+    assert DecodeReader.auto_chunk(1, 4, 16448) == 512        # 33 splits: 132 workgroups
+    assert DecodeReader.auto_chunk(32, 4, 16448, cus=512) == 4160
+    for cus in (80, 256, 304):
+        for max_n, hkv, mk in [(32, 4, 16448), (1, 4, 16448), (8, 4, 2048), (4, 16, 512), (256, 8, 100000),
+                               (1, 1, 1), (64, 8, 5000)]:
+            c = DecodeReader.auto_chunk(max_n, hkv, mk, cus)
+            S = math.ceil(mk / c)
+            assert c >= 512 and c % 64 == 0 and S * c >= mk
+            assert max_n * hkv * S <= max(cus, max_n * hkv), (cus, max_n, hkv, mk, c)
