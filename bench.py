@@ -172,6 +172,27 @@ def measured_stream_peak(dev, gib: int = 2) -> float:
     return best
 
 
+def settle(step, min_ms: float = 30.0, max_calls: int = 4000) -> int:
+    """Untimed calls of `step` until the GPU has been busy with them for `min_ms`, before a timed
+    region: these boxes raise their clocks only after several milliseconds of sustained load (the
+    op-B read timed 8 % slow after 10 warm-up calls of 0.34 ms, and a 16-step graph replayed once
+    right after its capture and checks ran 3 % behind the same graph replayed warm).  Returns the
+    number of calls; the workloads record it as config.settle_calls.  The W warm-up steps of the
+    command line follow it unchanged."""
+    step()                 # one-time set-up of a first call (allocations, code loading) stays
+    torch.cuda.synchronize()   # out of the window
+    n = 1
+    t0 = time.perf_counter()
+    while n < max_calls:
+        for _ in range(4):
+            step()
+        n += 4
+        torch.cuda.synchronize()
+        if (time.perf_counter() - t0) * 1e3 >= min_ms:
+            break
+    return n
+
+
 def timed_steps(step, steps: int, stream, host: list | None = None):
     """Times `steps` back-to-back calls of `step` with nothing else queued between them, closed
     by a device synchronisation on each side.  Returns (wall ms per step, GPU ms per step): the
@@ -245,9 +266,11 @@ def graph_timings(step, same, steps: int, dev, per_graph: int = 16) -> dict:
     out = {"ms": None, "span_ms": None, "ms_in_graph": None, "span_ms_in_graph": None}
     gph, _ = graph_of(step, same)
     if gph is not None:
+        settle(graph_replayer(gph, dev))
         out["ms"], out["span_ms"] = timed_steps(graph_replayer(gph, dev), steps, stream)
     gph16, _ = graph_of(lambda: [step() for _ in range(per_graph)][-1], same)
     if gph16 is not None:
+        settle(graph_replayer(gph16, dev))
         ms, span = timed_steps(graph_replayer(gph16, dev), max(1, steps // per_graph), stream)
         out["ms_in_graph"], out["span_ms_in_graph"] = ms / per_graph, span / per_graph
     return out
@@ -326,6 +349,7 @@ def measure_prefill(steps: int, warmup: int, cpu_sample: int) -> dict:
         w, _, p = fwd()
         bwd(w, p)
 
+    settle_calls = settle(step)
     for _ in range(warmup):
         step()
     stream = torch.cuda.current_stream(dev)
@@ -370,7 +394,8 @@ def measure_prefill(steps: int, warmup: int, cpu_sample: int) -> dict:
     return {"steps": steps, "warmup": warmup, "ms_per_step": ms_step, "gpu_ms_per_step": gpu_ms_step,
             "tflops_fwd_bwd": 2 * flops / (ms_step * 1e-3) / 1e12, "algorithmic_flops_per_direction": flops,
             "config": {"documents": G, "rows_per_document": T, "chunks": C, "slots_per_page": N, "d_s": d,
-                       "routing": "dense (top_k=0)", "accumulate": "fp32", "fragment_pages_ms_once": frag_ms},
+                       "routing": "dense (top_k=0)", "accumulate": "fp32", "fragment_pages_ms_once": frag_ms,
+                       "settle_calls": settle_calls},
             "fwd": {"ms": fwd_ms, "tflops": fwd_tf, "frac": fwd_tf / MFMA_FP16_PEAK_TFLOPS,
                     "frac_of_measured": fwd_tf / mfma_meas if mfma_meas else None},
             "bwd": {"ms": bwd_ms, "tflops": bwd_tf, "frac": bwd_tf / MFMA_FP16_PEAK_TFLOPS,
@@ -450,6 +475,7 @@ def bench_multi_depth(args):
     used = len(set(qg0.cpu().tolist()))
     bytes_step = (page_bytes + L * c["chunks"] * d * 4 + used * d * dr * 4
                   + 2 * B * c["k_sel"] * (d + dr) * 4 + B * dr * 4 * 2)
+    settle_calls = settle(step)
     for _ in range(args.warmup):
         step()
     stream = torch.cuda.current_stream(dev)
@@ -497,6 +523,7 @@ def bench_multi_depth(args):
         "config": {"workload": "multi_depth", "depths": L, "chunks_per_depth": c["chunks"],
                    "slots_per_page": c["N"], "d_s": d, "d_reader": dr, "batch": B,
                    "selector_top_k": c["k_sel"], "top_k": k, "B_dtype": "fp32", "accumulate": "fp32",
+                   "settle_calls": settle_calls,
                    "timing": timing, "ms_per_step_eager": ms_eager, "ms_per_step_graph": ms_graph,
                    "ms_per_step_in_16_step_graph": gt["ms_in_graph"],
                    "host_issue_us_per_step": host[0] * 1e3},
@@ -535,6 +562,7 @@ def bench_pool_build(args):
     def step():
         ops.build_pages(rows, off, d, N, d, mu)
 
+    settle_calls = settle(step)
     for _ in range(args.warmup):
         step()
     stream = torch.cuda.current_stream(dev)
@@ -576,7 +604,8 @@ def bench_pool_build(args):
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32 (fp16 in/out)", "data": "synthetic",
         "config": {"workload": "pool_build", "documents": len(P.n_chunks), "chunks": C,
-                   "slot_rows": R, "slots_per_page": N, "d_s": d, "centred": True},
+                   "slot_rows": R, "slots_per_page": N, "d_s": d, "centred": True,
+                   "settle_calls": settle_calls},
         "roofline": {"bound": "hbm", "kernel": "build_pages_kernel", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": None, "algorithmic_bytes": alg_bytes, "avg_launch_ms": k_ms,
@@ -626,6 +655,7 @@ def bench_d18(args):
 
     alg_bytes = (D * N * hkv * hd * 2 * 2 + (P + T) * hkv * hd * 2 * 4 + (D + 1) * T * hq * hd * 4
                  + T * hq * hd * 4 + 3 * hkv * G * T * D * 4)
+    settle_calls = settle(call)
     for _ in range(args.warmup):
         call()
     stream = torch.cuda.current_stream(dev)
@@ -666,7 +696,8 @@ def bench_d18(args):
         "value": T / (ms_step * 1e-3), "unit": "reader rows/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "fp32 (bf16 operators)", "data": "synthetic",
-        "config": {"workload": "d18", "documents": D, "rows_per_document": N, "hkv": hkv, "hq": hq,
+        "config": {"workload": "d18", "settle_calls": settle_calls, "documents": D, "rows_per_document": N,
+                   "hkv": hkv, "hq": hq,
                    "head_dim": hd, "own_rows": P, "reader_rows": T, "skip": skip, "key_splits": S,
                    "timing": timing, "ms_per_call_eager": ms_eager, "ms_per_call_graph": ms_graph,
                    "ms_per_call_in_16_call_graph": gt["ms_in_graph"]},
@@ -713,11 +744,8 @@ def bench_op_b(args):
         return dec(q, op_k, op_v, op_bt, op_l, own_k, own_v, own_bt, own_l, scale)
 
     alg_bytes = B * (op_len + own_len) * hkv * d * 2 * 2 + B * hq * d * (2 + 4)
-    # The GPU holds its clocks only after several milliseconds of sustained load: after 10 calls
-    # (3.4 ms at 32 rows) the 50 timed ones ran 8 % slower than after 100.  This workload has no
-    # graph-replay leg measured after a warm eager loop, so untimed calls settle the clocks first.
-    settle = max(0, 100 - args.warmup)
-    for _ in range(settle + args.warmup):
+    settle_calls = settle(call)
+    for _ in range(args.warmup):
         call()
     stream = torch.cuda.current_stream(dev)
     ms_step, k_ms = timed_steps(call, args.steps, stream)
@@ -757,7 +785,7 @@ def bench_op_b(args):
         "vs_baseline": None, "dtype": "fp32 (bf16 pools)", "data": "synthetic",
         "config": {"workload": "op_b", "rows": B, "operator_rows": op_len, "own_rows": own_len, "hq": hq,
                    "hkv": hkv, "head_dim": d, "block_size": bs, "key_splits": dec.S, "chunk": chunk,
-                   "settle_calls": settle},
+                   "settle_calls": settle_calls},
         "roofline": {"bound": "hbm", "kernel": "joint_read_mfma_kernel + joint_merge_kernel", "achieved": achieved,
                      "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
                      "algorithmic_bytes": alg_bytes, "avg_launch_ms": k_ms},
@@ -821,6 +849,7 @@ def bench_decode(args):
     read_bytes = routed_slots * d * 2 + 2 * B * d * 4
     route_bytes = sum(P.n_chunks) * d * 4 + B * d * 4
 
+    settle_calls = settle(step)
     for _ in range(args.warmup):
         step()
     stream = torch.cuda.current_stream(dev)
@@ -866,6 +895,7 @@ def bench_decode(args):
                    "chunks_per_library": f"U{{8..64}} (total {sum(P.n_chunks)})" if B > 1 else str(P.n_chunks[0]),
                    "slots_per_page": P.pages.shape[1], "top_k": top_k, "read_temp": read_temp,
                    "route_temp": route_temp, "accumulate": "fp32", "page_table": "seeded shuffle",
+                   "settle_calls": settle_calls,
                    "nsplit": args.nsplit or ops.default_nsplit(B * idx_h.shape[1], P.pages.shape[1]),
                    "timing": timing, "ms_per_step_eager": ms_eager, "ms_per_step_graph": ms_graph,
                    "ms_per_step_in_16_step_graph": gt["ms_in_graph"],
