@@ -137,7 +137,7 @@ __global__ __launch_bounds__(256) void fragment_pages_kernel(const _Float16* __r
 // [64w, 64w+64) (two 32-row MFMA tiles) x all 128 rows (four 32-column tiles).  The slot rows of
 // a wave are private to it: their fragments come straight from the layout-A page copy (one
 // coalesced 1 KiB load each), refilled for the next k-step as soon as they are consumed; the 128
-// query rows are shared by all waves and staged through LDS (two swizzled stages, one barrier
+// query rows are shared by all waves and staged through LDS (three swizzled stages, one barrier
 // per k-step).
 // MODE 0 (forward): writes p = masked softmax over the chunk's slots (fp16, octet-major), and
 //                    when gamma is given gamma[t, c] = log-sum-exp of the row's scaled scores.
@@ -458,7 +458,8 @@ __global__ __launch_bounds__(512) void scores_kernel(
 // Workgroup tile 128 rows x 256 dims, 4 waves; wave w owns dims [64w, 64w+64) x all 128 rows
 // (4 x 2 MFMA 32x32 tiles).  The dims of a wave are private to it: their fragments come from the
 // layout-B page copy (coalesced 1 KiB loads), refilled for the next k-step as they are consumed;
-// the 128 A rows are shared and staged through LDS (two swizzled stages of 16 KiB).
+// the 128 A rows are shared and staged through LDS (three swizzled stages of 16 KiB).  Two
+// workgroups run on each CU.
 // scale = w[t, c] when w != nullptr (forward read), else 1 (the backward dS already carries it).
 // ROUTE (backward): the accumulators start from the routing term sum_c dl[t, c] S[c, :] over the
 // library's chunks (fp32 MFMAs) instead of 0.  Rows of one tile belong to one library.
