@@ -89,17 +89,34 @@ __device__ __forceinline__ int find_group(const int* __restrict__ tile_ptr, int 
 }
 
 // ------------------------------------------------------------------------------------------
-// fp32 -> fp16 rows: y [M, d] (contiguous) from x [M, ldx].
-__global__ void cast_rows_f16_kernel(const float* __restrict__ x, long long ldx, int M, int d,
-                                     _Float16* __restrict__ y) {
-  const long long n4 = (long long)M * (d / 4);
-  for (long long i = blockIdx.x * (long long)blockDim.x + threadIdx.x; i < n4;
-       i += (long long)gridDim.x * blockDim.x) {
-    const long long row = i / (d / 4), col = (i % (d / 4)) * 4;
-    typedef float f32x4v __attribute__((ext_vector_type(4)));
-    const f32x4v v = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(x + row * ldx + col));
-    const half4_t h = {(_Float16)v[0], (_Float16)v[1], (_Float16)v[2], (_Float16)v[3]};
-    __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(y + row * d + col));
+// fp32 -> fp16 rows: y [M, d] (contiguous) from x [M, ldx].  A workgroup converts whole rows
+// (rows blockIdx.x, + gridDim.x, ...); each thread issues the loads of up to kCastPer groups of 4
+// elements of a row before it converts and stores them.
+constexpr int kCastThreads = 256, kCastPer = 4;
+__global__ __launch_bounds__(kCastThreads) void cast_rows_f16_kernel(const float* __restrict__ x,
+                                                                     long long ldx, int M, int d,
+                                                                     _Float16* __restrict__ y) {
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+  const int n4 = d / 4;
+  for (int row = blockIdx.x; row < M; row += gridDim.x) {
+    const float* xr = x + (long long)row * ldx;
+    _Float16* yr = y + (long long)row * d;
+    for (int c0 = threadIdx.x; c0 < n4; c0 += kCastThreads * kCastPer) {
+      f32x4v v[kCastPer];
+#pragma unroll
+      for (int u = 0; u < kCastPer; ++u) {
+        const int cc = c0 + u * kCastThreads;
+        if (cc < n4) v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4v*>(xr + 4 * cc));
+      }
+#pragma unroll
+      for (int u = 0; u < kCastPer; ++u) {
+        const int cc = c0 + u * kCastThreads;
+        if (cc < n4) {
+          const half4_t h = {(_Float16)v[u][0], (_Float16)v[u][1], (_Float16)v[u][2], (_Float16)v[u][3]};
+          __builtin_nontemporal_store(h, reinterpret_cast<half4_t*>(yr + 4 * cc));
+        }
+      }
+    }
   }
 }
 
@@ -773,9 +790,8 @@ extern "C" int xenc_cast_rows_f16(const float* x, long long ldx, int M, int d, v
   if (M == 0) return XENC_OK;
   if (!x || !y) return XENC_ENULL;
   if (!aligned16(x) || !aligned16(y)) return XENC_EALIGN;
-  const long long n4 = (long long)M * (d / 4);
-  const int blocks = (int)std::min<long long>((n4 + 255) / 256, 4096);
-  hipLaunchKernelGGL(cast_rows_f16_kernel, dim3(blocks), dim3(256), 0,
+  const int blocks = std::min(M, 8192);
+  hipLaunchKernelGGL(cast_rows_f16_kernel, dim3(blocks), dim3(kCastThreads), 0,
                      reinterpret_cast<hipStream_t>(stream), x, ldx, M, d,
                      static_cast<_Float16*>(y));
   return check_launch();

@@ -212,3 +212,17 @@ def test_prefill_single_slot_chunks(dev):
         assert rn <= 1e-2 and (r.detach().cpu().double() - ref[0].detach()).abs().max() <= 2e-3, soft
         rn, rm = _rel(qd.grad, qo.grad[0])
         assert rn <= 1e-2 and rm <= 1e-2, (soft, rn, rm)
+
+
+@pytest.mark.parametrize("M,d,ldx", [(1, 8, 8), (37, 64, 68), (300, 2048, 2048), (5, 4104, 4112), (9000, 32, 36)])
+def test_cast_rows_f16_is_torch_rounding(dev, M, d, ldx):
+    """xenc_cast_rows_f16 on strided fp32 rows equals torch's fp16 rounding bit for bit: rows past
+    one workgroup per row (M > 8192), rows longer than one pass of the workgroup's threads
+    (d / 4 > 1024), padded strides, and values past fp16's range and in its subnormals."""
+    say("cast rows f16", dict(M=M, d=d, ldx=ldx))
+    g = torch.Generator().manual_seed(M * 7 + d)
+    base = torch.randn(M, ldx, generator=g) * torch.logspace(-9, 6, ldx)[None, :]
+    x = base.to(dev)[:, :d]
+    y = ops.cast_f16(x)
+    assert y.shape == (M, d) and y.is_contiguous()
+    assert torch.equal(y.view(torch.int16).cpu(), base[:, :d].half().view(torch.int16))
