@@ -196,6 +196,13 @@ __global__ __launch_bounds__(512) void scores_kernel(
   const int lane = tid & 63;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hl = lane >> 5;   // lane half: k-group of the fragments, +4 row offset of D
+  // Waves 0-3 issue at priority 1, waves 4-7 at 0.  With the waves placed on the SIMDs in turn,
+  // waves w and w + 4 share one, and the two, otherwise identical, fall out of step inside a
+  // k-step, so one's tail (waits, the next step's first fragments, the barrier) overlaps the
+  // other's MFMAs (~0.4 % faster than equal priority, three alternating runs; raising only the
+  // k-step body, as the readout does, changed nothing here: both waves of a SIMD meet at the
+  // same barrier every k-step).
+  if (wv < 4) __builtin_amdgcn_s_setprio(1);
   const int l32 = lane & 31;
 
   // A fragments of this wave's two slot groups (groups past N/32 re-read the last one; those
@@ -242,13 +249,9 @@ __global__ __launch_bounds__(512) void scores_kernel(
   // LDS while the MFMAs of step ks issue (MFMA and ds_read alternating), and the two A fragment
   // refills go out between the last MFMAs, so no MFMA waits on a read issued just before it.
   // The group barriers fix that order; left alone, the compiler sinks every read to just before
-  // its first use.  A wave runs its k-step body at issue priority 1 and its tail (the waits, the
-  // first fragments of the next step, the barrier) at 0: where the two waves of a SIMD are in
-  // different phases, the one issuing MFMAs wins the arbitration (forward and backward ~3 %
-  // faster than at equal priority).
+  // its first use.
   auto compute = [&](int st, int knext) {
     half8_t fbn[4];
-    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       half8_t fb[4];
@@ -307,7 +310,6 @@ __global__ __launch_bounds__(512) void scores_kernel(
     stage_b((k + 2) % 3, min(k + 2, nk - 1) * BK);
     __builtin_amdgcn_sched_barrier(0);
     compute(k % 3, k1);
-    __builtin_amdgcn_s_setprio(0);
     wait_vmem<8>();
     read_fb0((k + 1) % 3);
     __syncthreads();
@@ -594,7 +596,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void r
   };
   // As in the scores kernel: the A fragments of k16 step ks + 1 are read while the MFMAs of
   // step ks issue, the B refills go out between the last MFMAs, and the body runs at issue
-  // priority 1, the tail (the staging stores, the next step's first fragments, the barrier) at 0.
+  // priority 1, the tail (the staging stores, the next step's first fragments, the barrier) at 0:
+  // the CU's two workgroups are in different phases, and the one issuing MFMAs wins the
+  // arbitration (forward and backward ~3 % faster than at equal priority).
   auto compute = [&](int st, const _Float16* kbn, int nbn) {
     half8_t fan[NA];
     __builtin_amdgcn_s_setprio(1);
