@@ -90,6 +90,17 @@ def test_host_side_validation_rejects_bad_sizes():
     assert routed(ldl=1) == -1
     assert routed(ldl=1 << 25) == -1
     assert routed(n_tiles=0) == 0
+    # the fp32 -> fp16 row cast: d not a multiple of 8, a row stride below d or not a multiple
+    # of 4, no rows, NULL pointers, and (fake, never dereferenced) pointers off 16-byte alignment
+    cast = L.xenc_cast_rows_f16
+    assert cast(None, 16, 4, 12, None, None) == -1
+    assert cast(None, 8, 4, 16, None, None) == -1
+    assert cast(None, 18, 4, 16, None, None) == -1
+    assert cast(None, 16, -1, 16, None, None) == -1
+    assert cast(None, 16, 0, 16, None, None) == 0
+    assert cast(None, 16, 4, 16, None, None) == -2
+    assert cast(0x1004, 16, 4, 16, 0x2000, None) == -3
+    assert cast(0x1000, 16, 4, 16, 0x2008, None) == -3
 
 
 def test_cpp_operators_registered():
